@@ -1,0 +1,333 @@
+"""ctypes binding of the MI355X libraries (include/cbis_kernels.h and
+include/cbis_runtime.h) with Python twins of the reference's host classes:
+
+    PagedKVCache       include/paged_kv_cache.hpp:17-51
+    ModelWeights       include/model_weights.hpp:7-25
+    TransformerRunner  include/transformer.hpp:15-34
+    run_continuous     src/bench_batching.cpp:98-179
+
+The compute is the HIP code in lib/libcbis_kernels.so, reached through the
+C-ABI; nothing here computes on the CPU.  Importing fails loudly when the
+libraries have not been built (``make -C`` this directory, or
+``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+KERNELS_SO = os.path.join(LIB_DIR, "libcbis_kernels.so")
+RUNTIME_SO = os.path.join(LIB_DIR, "libcbis.so")
+
+F32, BF16, FP8E4M3 = 0, 1, 2
+EPI_NONE, EPI_GELU = 0, 1
+DTYPES = {"f32": F32, "bf16": BF16, "fp8": FP8E4M3}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_U64 = ctypes.c_uint64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+_IP = ctypes.POINTER(ctypes.c_int)
+
+
+class GemmDesc(ctypes.Structure):
+    _fields_ = [("M", _I), ("N", _I), ("K", _I),
+                ("x_dtype", _I), ("X", _P), ("ldx", _I64),
+                ("w_dtype", _I), ("W", _P), ("ldw", _I64),
+                ("w_scale", _P), ("bias", _P), ("epilogue", _I),
+                ("residual", _P), ("ldr", _I64),
+                ("y_dtype", _I), ("Y", _P), ("ldy", _I64),
+                ("kv_col0", _I), ("kv_width", _I), ("kv_dtype", _I), ("page_size", _I),
+                ("k_pool", _P), ("v_pool", _P), ("write_page", _P), ("write_offset", _P)]
+
+
+class AttnDesc(ctypes.Structure):
+    _fields_ = [("n_rows", _I), ("rows", _P), ("n_heads", _I), ("head_dim", _I), ("page_size", _I),
+                ("q_dtype", _I), ("q", _P), ("ldq", _I64),
+                ("kv_dtype", _I), ("k_pool", _P), ("v_pool", _P), ("num_pages", _I),
+                ("block_table", _P), ("bt_stride", _I64), ("row_bt", _P), ("row_pos", _P),
+                ("out_dtype", _I), ("out", _P), ("ldo", _I64),
+                ("max_kv_len", _I), ("split_tokens", _I), ("workspace", _P), ("workspace_bytes", _SZ)]
+
+
+class ModelConfig(ctypes.Structure):
+    _fields_ = [("vocab", _I), ("d_model", _I), ("n_heads", _I), ("head_dim", _I), ("n_layers", _I),
+                ("mlp", _I), ("max_seq", _I), ("page_size", _I), ("weight_dtype", _I), ("kv_dtype", _I)]
+
+    @classmethod
+    def make(cls, vocab=1000, d_model=256, n_heads=8, head_dim=32, n_layers=4, mlp=1024, max_seq=32768,
+             page_size=16, weight_dtype="f32", kv_dtype="f32"):
+        return cls(vocab, d_model, n_heads, head_dim, n_layers, mlp, max_seq, page_size,
+                   DTYPES[weight_dtype] if isinstance(weight_dtype, str) else weight_dtype,
+                   DTYPES[kv_dtype] if isinstance(kv_dtype, str) else kv_dtype)
+
+
+# Every symbol the two headers declare, with its ctypes signature.
+KERNEL_SYMBOLS = {
+    "cbis_last_error": (ctypes.c_char_p, []),
+    "cbis_linear_forward": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "cbis_embed_lookup_add": (_I, [_P, _P, _P, _P, _P, _I, _I, _P]),
+    "cbis_layernorm_forward": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "cbis_gelu_forward": (_I, [_P, _I, _I, _P]),
+    "cbis_residual_add": (_I, [_P, _P, _I, _I, _P]),
+    "cbis_scatter_kv_to_cache": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "cbis_fused_paged_causal_attention": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "cbis_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
+    "cbis_paged_attention_workspace_size": (_SZ, [ctypes.POINTER(AttnDesc)]),
+    "cbis_paged_attention": (_I, [ctypes.POINTER(AttnDesc), _P]),
+    "cbis_paged_prefill_attention": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
+    "cbis_embed": (_I, [_I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P]),
+    "cbis_layernorm": (_I, [_I, _I, _P, _I64, _P, _P, _F, _I, _P, _I64, _P]),
+    "cbis_argmax_rows": (_I, [_I, _I, _P, _I64, _P, _P]),
+    "cbis_fill_normal_exact": (_I, [_P, _I, _I64, _U64, _U64, _U64, _F, _P]),
+    "cbis_fill_normal_fast": (_I, [_P, _I, _I64, _U64, _F, _P]),
+    "cbis_convert_f32": (_I, [_P, _I, _P, _I64, _P]),
+    "cbis_quantize_fp8_rows": (_I, [_P, _P, _P, _I, _I, _P]),
+}
+
+RUNTIME_SYMBOLS = {
+    "cbis_runtime_last_error": (ctypes.c_char_p, []),
+    "cbis_default_config": (None, [ctypes.POINTER(ModelConfig)]),
+    "cbis_cache_create": (_P, [_I, _I, _I, _I, _I, _I, _I, _I]),
+    "cbis_cache_destroy": (None, [_P]),
+    "cbis_cache_allocate_sequence": (_I, [_P]),
+    "cbis_cache_free_sequence": (None, [_P, _I]),
+    "cbis_cache_ensure_capacity": (_I, [_P, _I, _I]),
+    "cbis_cache_resolve_slot": (_I, [_P, _I, _I, _IP, _IP]),
+    "cbis_cache_page_table": (_I, [_P, _I, _IP, _I]),
+    "cbis_cache_seq_pages": (_I, [_P, _I, _IP, _I]),
+    "cbis_cache_num_free_pages": (_I, [_P]),
+    "cbis_cache_max_pages": (_I, [_P]),
+    "cbis_cache_page_size": (_I, [_P]),
+    "cbis_cache_k_base": (_P, [_P, _I]),
+    "cbis_cache_v_base": (_P, [_P, _I]),
+    "cbis_cache_fill_normal": (_I, [_P, _U64, _F]),
+    "cbis_weights_synthetic": (_P, [ctypes.POINTER(ModelConfig), _U64, _F]),
+    "cbis_weights_load": (_P, [ctypes.c_char_p, ctypes.POINTER(ModelConfig)]),
+    "cbis_weights_destroy": (None, [_P]),
+    "cbis_weights_device_bytes": (_SZ, [_P]),
+    "cbis_weights_tensor": (_P, [_P, ctypes.c_char_p]),
+    "cbis_runner_create": (_P, [_P, _P, _I]),
+    "cbis_runner_destroy": (None, [_P]),
+    "cbis_runner_forward_step": (_I, [_P, _I, _IP, _IP, _IP, ctypes.POINTER(ctypes.c_float)]),
+    "cbis_runner_forward_step_greedy": (_I, [_P, _I, _IP, _IP, _IP, _IP]),
+    "cbis_runner_logits_device": (_P, [_P]),
+    "cbis_runner_stream": (_P, [_P]),
+    "cbis_runner_set_graphs": (None, [_P, _I]),
+    "cbis_run_continuous": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _IP, ctypes.POINTER(ctypes.c_double), _I]),
+}
+
+_kern = None
+_rt = None
+
+
+def _load(path, symbols):
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built: run __graft_entry__.build() (the HIP path has no CPU fallback)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in symbols.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def kernels():
+    global _kern
+    if _kern is None:
+        _kern = _load(KERNELS_SO, KERNEL_SYMBOLS)
+    return _kern
+
+
+def runtime():
+    global _rt
+    if _rt is None:
+        kernels()
+        _rt = _load(RUNTIME_SO, RUNTIME_SYMBOLS)
+    return _rt
+
+
+class CbisError(RuntimeError):
+    pass
+
+
+def check(rc, what="cbis"):
+    if rc != 0:
+        msg = kernels().cbis_last_error()
+        raise CbisError(f"{what} failed with status {rc}: {msg.decode() if msg else ''}")
+
+
+def _rt_check(rc, what):
+    if rc is None or (isinstance(rc, int) and rc < 0):
+        msg = runtime().cbis_runtime_last_error()
+        text = msg.decode() if msg else ""
+        if text.startswith("out_of_range"):
+            raise IndexError(f"{what}: {text}")
+        raise CbisError(f"{what}: {text}")
+    return rc
+
+
+def _iarr(vals):
+    vals = list(int(v) for v in vals)
+    return (ctypes.c_int * max(1, len(vals)))(*vals)
+
+
+# --------------------------------------------------------------------------
+# Reference-API twins
+# --------------------------------------------------------------------------
+
+class PagedKVCache:
+    """src/paged_kv_cache.cpp semantics; device pools optional."""
+
+    _h = None
+
+    def __init__(self, num_layers, max_pages, page_size=16, n_heads=8, head_dim=32, kv_dtype="f32",
+                 pages_per_seq=2048, alloc_device=True):
+        self._h = _rt_check(runtime().cbis_cache_create(num_layers, max_pages, page_size, n_heads, head_dim,
+                                                        DTYPES[kv_dtype], pages_per_seq, int(alloc_device)),
+                            "PagedKVCache")
+        self.num_layers, self.n_heads, self.head_dim = num_layers, n_heads, head_dim
+        self.kv_dtype, self.pages_per_seq = kv_dtype, pages_per_seq
+
+    def close(self):
+        if self._h:
+            runtime().cbis_cache_destroy(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def allocate_sequence(self) -> int:
+        return _rt_check(runtime().cbis_cache_allocate_sequence(self._h), "allocate_sequence")
+
+    def free_sequence(self, seq_id: int) -> None:
+        runtime().cbis_cache_free_sequence(self._h, seq_id)
+
+    def ensure_capacity(self, seq_id: int, token_pos: int) -> bool:
+        return bool(_rt_check(runtime().cbis_cache_ensure_capacity(self._h, seq_id, token_pos), "ensure_capacity"))
+
+    def resolve_slot(self, seq_id: int, token_pos: int):
+        p, o = ctypes.c_int(), ctypes.c_int()
+        _rt_check(runtime().cbis_cache_resolve_slot(self._h, seq_id, token_pos, ctypes.byref(p), ctypes.byref(o)),
+                  "resolve_slot")
+        return p.value, o.value
+
+    def page_table(self, seq_id: int) -> list:
+        buf = (ctypes.c_int * self.pages_per_seq)()
+        n = _rt_check(runtime().cbis_cache_page_table(self._h, seq_id, buf, self.pages_per_seq), "page_table")
+        return list(buf[:n])
+
+    def pages(self, seq_id: int) -> list:
+        n = _rt_check(runtime().cbis_cache_seq_pages(self._h, seq_id, None, 0), "pages")
+        buf = (ctypes.c_int * max(1, n))()
+        runtime().cbis_cache_seq_pages(self._h, seq_id, buf, n)
+        return list(buf[:n])
+
+    def num_free_pages(self) -> int:
+        return runtime().cbis_cache_num_free_pages(self._h)
+
+    def max_pages(self) -> int:
+        return runtime().cbis_cache_max_pages(self._h)
+
+    def page_size(self) -> int:
+        return runtime().cbis_cache_page_size(self._h)
+
+    def k_base(self, layer: int) -> int:
+        return _rt_check(runtime().cbis_cache_k_base(self._h, layer), "k_base")
+
+    def v_base(self, layer: int) -> int:
+        return _rt_check(runtime().cbis_cache_v_base(self._h, layer), "v_base")
+
+    def fill_normal(self, seed: int, std: float = 1.0) -> None:
+        _rt_check(runtime().cbis_cache_fill_normal(self._h, seed, std), "fill_normal")
+
+
+class ModelWeights:
+    _h = None
+
+    def __init__(self, handle, cfg: ModelConfig):
+        self._h = handle
+        self.cfg = cfg
+
+    @classmethod
+    def synthetic(cls, cfg: ModelConfig, seed: int = 0, std: float = 0.02):
+        return cls(_rt_check(runtime().cbis_weights_synthetic(ctypes.byref(cfg), seed, std), "ModelWeights.synthetic"), cfg)
+
+    @classmethod
+    def load(cls, path: str, cfg: ModelConfig):
+        return cls(_rt_check(runtime().cbis_weights_load(path.encode(), ctypes.byref(cfg)), "ModelWeights.load"), cfg)
+
+    def tensor(self, name: str) -> int:
+        return _rt_check(runtime().cbis_weights_tensor(self._h, name.encode()), f"tensor {name}")
+
+    def device_bytes(self) -> int:
+        return runtime().cbis_weights_device_bytes(self._h)
+
+    def close(self):
+        if self._h:
+            runtime().cbis_weights_destroy(self._h)
+            self._h = None
+
+    __del__ = close
+
+
+class TransformerRunner:
+    _h = None
+
+    def __init__(self, weights: ModelWeights, cache: PagedKVCache, max_total_rows: int):
+        self.weights, self.cache = weights, cache  # keep them alive
+        self.vocab = weights.cfg.vocab
+        self._h = _rt_check(runtime().cbis_runner_create(weights._h, cache._h, max_total_rows), "TransformerRunner")
+
+    def close(self):
+        if self._h:
+            runtime().cbis_runner_destroy(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def forward_step(self, token_ids, positions, seq_ids):
+        """Returns [rows, vocab] fp32 logits as a flat list-backed ctypes array -> numpy via caller."""
+        import numpy as np
+        n = len(token_ids)
+        out = np.empty((n, self.vocab), dtype=np.float32)
+        _rt_check(runtime().cbis_runner_forward_step(self._h, n, _iarr(token_ids), _iarr(positions), _iarr(seq_ids),
+                                                     out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))),
+                  "forward_step")
+        return out
+
+    def forward_step_greedy(self, token_ids, positions, seq_ids):
+        n = len(token_ids)
+        out = (ctypes.c_int * max(1, n))()
+        _rt_check(runtime().cbis_runner_forward_step_greedy(self._h, n, _iarr(token_ids), _iarr(positions),
+                                                            _iarr(seq_ids), out), "forward_step_greedy")
+        return list(out[:n])
+
+    def logits_device(self) -> int:
+        return runtime().cbis_runner_logits_device(self._h)
+
+    def stream(self) -> int:
+        return runtime().cbis_runner_stream(self._h) or 0
+
+    def set_graphs(self, enable: bool) -> None:
+        runtime().cbis_runner_set_graphs(self._h, int(enable))
+
+
+def run_continuous(runner: TransformerRunner, cache: PagedKVCache, prompts, decode_lens, max_slots=16,
+                   max_steps=4096):
+    """Returns (tokens per request, per-step wall ms)."""
+    lens = [len(p) for p in prompts]
+    flat = [t for p in prompts for t in p]
+    out = (ctypes.c_int * max(1, sum(decode_lens)))()
+    ms = (ctypes.c_double * max_steps)()
+    n = _rt_check(runtime().cbis_run_continuous(runner._h, cache._h, len(prompts), _iarr(lens), _iarr(flat),
+                                                _iarr(decode_lens), max_slots, out, ms, max_steps),
+                  "run_continuous")
+    toks, o = [], 0
+    for d in decode_lens:
+        toks.append(list(out[o: o + d]))
+        o += d
+    return toks, list(ms[: min(n, max_steps)])

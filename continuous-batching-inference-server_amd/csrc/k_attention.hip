@@ -1,0 +1,549 @@
+// Paged causal attention for gfx950.
+//
+// Reference: fused_attention_kernel, kernels/attention.cu:57-98 -- one 32-lane
+// warp per (row, head) walking keys one at a time (page lookup, shuffle-tree
+// dot, two expf per key).  Semantics kept: row r attends to keys
+// j in [0, pos_r] of its sequence (kv_len = pos_r + 1, :67-68), key j is slot
+// j % page_size of physical page table[j / page_size] (:79-83), scores are
+// scaled by 1/sqrt(head_dim) (:72) and softmax-normalised (python/model.py:40-44).
+//
+// Decode kernel (HBM-bound).  A workgroup of NW waves owns one
+// (row, head block, kv split).  A head block is the heads whose head_dim
+// slices of one token row form 1 KiB: 8 heads for fp32 K/V, 16 for bf16, so
+// one 16-byte-per-lane wave load reads one token's slice of the block fully
+// coalesced, and a 16-token page is 16 such loads at the token stride.  Each
+// lane holds 4 (fp32) or 8 (bf16) dims of one head; q.k is finished with
+// 2-3 DPP steps inside the lane group.  Waves take whole pages round-robin,
+// run an online softmax per page (one max / rescale per 16 keys, exp2 with
+// log2(e) folded into q), merge through LDS, and either write the output
+// (single split) or fp32 partials (m, l, acc) that a merge kernel combines.
+//
+// Prefill kernel (MFMA).  One wave per (32-row query tile, head); four heads
+// per workgroup.  S^T = K Q^T on v_mfma_f32_32x32x16_bf16 with K read straight
+// from the pages in the A-operand layout, online softmax per query column,
+// O^T = V^T P^T with P taken from the S^T accumulators in registers (their
+// lane layout is the B-operand layout up to a fixed permutation of the key
+// index, applied to V^T as well) and V^T gathered from an LDS copy of the
+// 32-key V tile.
+#include "common.hpp"
+
+namespace cbis {
+namespace {
+
+constexpr int kHD = 32;  // head_dim supported by these kernels
+constexpr int kPS = 16;  // page_size supported by these kernels
+constexpr int kWS = kHD + 4;  // floats per split partial: acc[32], m, l, pad
+
+struct DecodeArgs {
+  const int* rows;
+  const void* q;
+  int64_t ldq;
+  int q_bf16;
+  const void* kpool;
+  const void* vpool;
+  int num_pages;
+  const int* bt;
+  int64_t bt_stride;
+  const int* row_bt;
+  const int* row_pos;
+  void* out;
+  int64_t ldo;
+  int out_bf16;
+  float* ws;  // [n_rows][n_splits][H][kWS]: acc[kHD], m, l, 2 pad (16-byte rows)
+  int n_heads;
+  int n_hblocks;
+  int n_splits;
+  int split_tokens;
+  int max_kv;  // clamp for kv_len (bt_stride * page_size)
+  float qscale;
+};
+
+template <typename KVT>
+struct KVTraits;
+template <>
+struct KVTraits<float> {
+  static constexpr int EPL = 4;  // elements per 16-byte lane load
+  __device__ static inline void unpack(const uint4& r, float* f) {
+    f[0] = __uint_as_float(r.x);
+    f[1] = __uint_as_float(r.y);
+    f[2] = __uint_as_float(r.z);
+    f[3] = __uint_as_float(r.w);
+  }
+};
+template <>
+struct KVTraits<uint16_t> {
+  static constexpr int EPL = 8;
+  __device__ static inline void unpack(const uint4& r, float* f) {
+    f[0] = bf16lo(r.x); f[1] = bf16hi(r.x);
+    f[2] = bf16lo(r.y); f[3] = bf16hi(r.y);
+    f[4] = bf16lo(r.z); f[5] = bf16hi(r.z);
+    f[6] = bf16lo(r.w); f[7] = bf16hi(r.w);
+  }
+};
+
+template <typename KVT, int NW>
+__global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs a) {
+  constexpr int EPL = KVTraits<KVT>::EPL;
+  constexpr int G = kHD / EPL;  // lanes per head
+  constexpr int HPB = 64 / G;   // heads per block (one 1 KiB wave load)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  int bid = blockIdx.x;
+  const int hb = bid % a.n_hblocks;
+  bid /= a.n_hblocks;
+  const int split = bid % a.n_splits;
+  const int ridx = bid / a.n_splits;
+  const int row = a.rows ? a.rows[ridx] : ridx;
+  const int kv_len = min(a.row_pos[row] + 1, a.max_kv);
+  const int t0 = split * a.split_tokens;
+  if (kv_len <= 0 || t0 >= kv_len) return;
+  const int t1 = min(kv_len, t0 + a.split_tokens);
+  const int nsplit_row = (kv_len + a.split_tokens - 1) / a.split_tokens;
+  const int* bt = a.bt + (int64_t)(a.row_bt ? a.row_bt[row] : row) * a.bt_stride;
+
+  const int head = hb * HPB + lane / G;
+  const int sub = lane % G;
+  const int D = a.n_heads * kHD;
+  const int lane_off = head * kHD + sub * EPL;
+
+  float q[EPL];
+  if (a.q_bf16) {
+    const uint16_t* qp = (const uint16_t*)a.q + (int64_t)row * a.ldq + lane_off;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) q[e] = bf16_to_f32(qp[e]) * a.qscale;
+  } else {
+    const float* qp = (const float*)a.q + (int64_t)row * a.ldq + lane_off;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) q[e] = qp[e] * a.qscale;
+  }
+
+  const int64_t tok_stride = D;                  // elements between consecutive slots
+  const int64_t page_stride = tok_stride * kPS;  // elements per page
+  const KVT* kbase = (const KVT*)a.kpool + lane_off;
+  const KVT* vbase = (const KVT*)a.vpool + lane_off;
+
+  float m = -INFINITY, l = 0.f;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+
+  const int p_first = t0 / kPS, p_last = (t1 - 1) / kPS;
+  for (int p = p_first + wave; p <= p_last; p += NW) {
+    int phys = bt[p];
+    phys = min(max(phys, 0), a.num_pages - 1);
+    const KVT* kp = kbase + (int64_t)phys * page_stride;
+    const KVT* vp = vbase + (int64_t)phys * page_stride;
+    uint4 kr[kPS], vr[kPS];
+#pragma unroll
+    for (int t = 0; t < kPS; ++t) kr[t] = *(const uint4*)(kp + t * tok_stride);
+#pragma unroll
+    for (int t = 0; t < kPS; ++t) vr[t] = *(const uint4*)(vp + t * tok_stride);
+    const int nvalid = min(kPS, t1 - p * kPS);  // >= 1; < kPS only on the sequence's last page
+    float s[kPS];
+    float mp = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < kPS; ++t) {
+      float kf[EPL];
+      KVTraits<KVT>::unpack(kr[t], kf);
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) d += q[e] * kf[e];
+      d = group_sum<G>(d);
+      s[t] = (t < nvalid) ? d : -INFINITY;
+      mp = fmaxf(mp, s[t]);
+    }
+    const float mn = fmaxf(m, mp);
+    const float corr = fast_exp2(m - mn);
+    l *= corr;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] *= corr;
+#pragma unroll
+    for (int t = 0; t < kPS; ++t) {
+      const float pt = fast_exp2(s[t] - mn);
+      l += pt;
+      float vf[EPL];
+      KVTraits<KVT>::unpack(vr[t], vf);
+      if (t < nvalid) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] += pt * vf[e];
+      }
+    }
+    m = mn;
+  }
+
+  // Merge the NW waves' states through LDS.
+  __shared__ float sm[NW][64], sl[NW][64], sacc[NW][EPL][64];
+  sm[wave][lane] = m;
+  sl[wave][lane] = l;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) sacc[wave][e][lane] = acc[e];
+  __syncthreads();
+  if (wave != 0) return;
+  float M = sm[0][lane];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, sm[w][lane]);
+  float L = 0.f, O[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) O[e] = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const float c = fast_exp2(sm[w][lane] - M);  // waves with no pages: m=-inf -> 0
+    L += sl[w][lane] * c;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) O[e] += sacc[w][e][lane] * c;
+  }
+  if (nsplit_row == 1) {
+    const float inv = 1.f / L;
+    if (a.out_bf16) {
+      uint16_t* op = (uint16_t*)a.out + (int64_t)row * a.ldo + lane_off;
+#pragma unroll
+      for (int e = 0; e < EPL; e += 2) *(uint32_t*)(op + e) = pack_bf16x2(O[e] * inv, O[e + 1] * inv);
+    } else {
+      float* op = (float*)a.out + (int64_t)row * a.ldo + lane_off;
+#pragma unroll
+      for (int e = 0; e < EPL; e += 4) *(float4*)(op + e) = make_float4(O[e] * inv, O[e + 1] * inv, O[e + 2] * inv, O[e + 3] * inv);
+    }
+  } else {
+    float* w = a.ws + (((int64_t)ridx * a.n_splits + split) * a.n_heads + head) * kWS;
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4) *(float4*)(w + sub * EPL + e) = make_float4(O[e], O[e + 1], O[e + 2], O[e + 3]);
+    if (sub == 0) {
+      w[kHD] = M;
+      w[kHD + 1] = L;
+    }
+  }
+}
+
+// Combines split partials: one thread per (row, head, dim).
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a, int n_rows) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int d = (int)(gid % kHD);
+  const int64_t rh = gid / kHD;
+  const int head = (int)(rh % a.n_heads);
+  const int ridx = (int)(rh / a.n_heads);
+  if (ridx >= n_rows) return;
+  const int row = a.rows ? a.rows[ridx] : ridx;
+  const int kv_len = min(a.row_pos[row] + 1, a.max_kv);
+  if (kv_len <= 0) return;
+  const int ns = (kv_len + a.split_tokens - 1) / a.split_tokens;
+  if (ns <= 1) return;
+  const float* w = a.ws + ((int64_t)ridx * a.n_splits * a.n_heads + head) * kWS;
+  const int64_t sstride = (int64_t)a.n_heads * kWS;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, w[s * sstride + kHD]);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const float c = fast_exp2(w[s * sstride + kHD] - M);
+    L += w[s * sstride + kHD + 1] * c;
+    O += w[s * sstride + d] * c;
+  }
+  const float r = O / L;
+  const int64_t o = (int64_t)row * a.ldo + head * kHD + d;
+  if (a.out_bf16) ((uint16_t*)a.out)[o] = f32_to_bf16(r);
+  else ((float*)a.out)[o] = r;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill on MFMA.
+// ---------------------------------------------------------------------------
+struct PrefillArgs {
+  const int* tiles;  // [n_tiles][4]: first_row, n_valid, bt_row, first_pos
+  const void* q;
+  int64_t ldq;
+  int q_bf16;
+  const uint16_t* kpool;
+  const uint16_t* vpool;
+  int num_pages;
+  const int* bt;
+  int64_t bt_stride;
+  void* out;
+  int64_t ldo;
+  int out_bf16;
+  int n_heads;
+  int max_kv;
+  float qscale;  // log2(e) / sqrt(head_dim), applied to S in fp32
+};
+
+// Wave tile: 32 queries x one head.  Workgroup: 4 heads of the same tile.
+__global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n_hgroups = a.n_heads / 4;
+  const int tile = blockIdx.x / n_hgroups;
+  const int head = (blockIdx.x % n_hgroups) * 4 + wave;
+  const int4 td = *(const int4*)(a.tiles + 4 * (int64_t)tile);
+  const int row0 = td.x, nvalid = td.y, pos0 = td.w;
+  const int* bt = a.bt + (int64_t)td.z * a.bt_stride;
+  const int D = a.n_heads * kHD;
+  const int col = lane & 31;  // query index within the tile (B / C column)
+  const int half = lane >> 5;
+
+  // Q^T as the B operand: lane holds q[col][half*8 + 0..7] (MFMA 0) and
+  // q[col][16 + half*8 + 0..7] (MFMA 1), bf16.
+  bf16x8_t qb0, qb1;
+  {
+    const int qr = row0 + min(col, nvalid - 1);
+    float f[16];
+    if (a.q_bf16) {
+      const uint16_t* qp = (const uint16_t*)a.q + (int64_t)qr * a.ldq + head * kHD;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        f[e] = bf16_to_f32(qp[half * 8 + e]);
+        f[8 + e] = bf16_to_f32(qp[16 + half * 8 + e]);
+      }
+    } else {
+      const float* qp = (const float*)a.q + (int64_t)qr * a.ldq + head * kHD;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        f[e] = qp[half * 8 + e];
+        f[8 + e] = qp[16 + half * 8 + e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      qb0[e] = (short)f32_to_bf16(f[e]);
+      qb1[e] = (short)f32_to_bf16(f[8 + e]);
+    }
+  }
+  const int qpos = pos0 + min(col, nvalid - 1);  // this lane's query position
+  const int kv_end = min(pos0 + nvalid, a.max_kv);  // keys [0, kv_end) needed by the tile
+
+  __shared__ uint16_t vt[4][32][kHD + 2];  // per-wave V tile [key][dim], padded
+  f32x16_t o;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = 0.f;
+  float m = -INFINITY, l = 0.f;
+
+  for (int j0 = 0; j0 < kv_end; j0 += 32) {
+    // K rows for keys j0 + col (A operand: lane = key (col), dims half*8..).
+    const int key = j0 + col;
+    const int kc = min(key, kv_end - 1);
+    int phys = bt[kc / kPS];
+    phys = min(max(phys, 0), a.num_pages - 1);
+    const int64_t slot = ((int64_t)phys * kPS + (kc % kPS)) * D + head * kHD;
+    const bf16x8_t ka0 = *(const bf16x8_t*)(a.kpool + slot + half * 8);
+    const bf16x8_t ka1 = *(const bf16x8_t*)(a.kpool + slot + 16 + half * 8);
+    // V tile into LDS: lane (key=col, half) copies dims half*16 .. +15.
+    {
+      const uint4* vs = (const uint4*)(a.vpool + slot + half * 16);
+      const uint4 v0 = vs[0], v1 = vs[1];
+      uint32_t* dst = (uint32_t*)&vt[wave][col][half * 16];
+      dst[0] = v0.x; dst[1] = v0.y; dst[2] = v0.z; dst[3] = v0.w;
+      dst[4] = v1.x; dst[5] = v1.y; dst[6] = v1.z; dst[7] = v1.w;
+    }
+    f32x16_t s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka0, qb0, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka1, qb1, s, 0, 0, 0);
+    // s[i]: key j0 + 8*(i/4) + 4*half + (i%4), query col.
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kj = j0 + 8 * (i >> 2) + 4 * half + (i & 3);
+      s[i] = (kj <= qpos && kj < kv_end) ? s[i] * a.qscale : -INFINITY;
+      mloc = fmaxf(mloc, s[i]);
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float mn = fmaxf(m, mloc);
+    const float corr = fast_exp2(m - mn);  // mn finite: key j0 <= qpos always
+    float lsum = 0.f;
+    bf16x8_t pb0, pb1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = fast_exp2(s[i] - mn);
+      lsum += p;
+      if (i < 8) pb0[i] = (short)f32_to_bf16(p);
+      else pb1[i - 8] = (short)f32_to_bf16(p);
+    }
+    lsum += __shfl_xor(lsum, 32, 64);
+    l = l * corr + lsum;
+    m = mn;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] *= corr;
+    // V^T as the A operand: lane = dim (col), k-slot e of MFMA b holds key
+    // 16*b + 8*(e/4) + 4*half + (e%4), matching P's register order.
+    __syncthreads();
+    bf16x8_t va0, va1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int kk = 8 * (e >> 2) + 4 * half + (e & 3);
+      va0[e] = (short)vt[wave][kk][col];
+      va1[e] = (short)vt[wave][16 + kk][col];
+    }
+    o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va0, pb0, o, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va1, pb1, o, 0, 0, 0);
+    __syncthreads();
+  }
+  // o[i]: dim 8*(i/4) + 4*half + (i%4) of query col.
+  if (col < nvalid) {
+    const float inv = 1.f / l;
+    const int64_t ob = (int64_t)(row0 + col) * a.ldo + head * kHD;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = 8 * (i >> 2) + 4 * half + (i & 3);
+      if (a.out_bf16) ((uint16_t*)a.out)[ob + d] = f32_to_bf16(o[i] * inv);
+      else ((float*)a.out)[ob + d] = o[i] * inv;
+    }
+  }
+}
+
+int resolve_split(const cbis_attn_desc* d, int hblocks, int* n_splits) {
+  int split = d->split_tokens;
+  const int max_kv = std::max(1, d->max_kv_len);
+  if (split <= 0) {
+    if (d->max_kv_len <= 0) {
+      split = 1 << 30;  // single pass
+    } else {
+      // Aim for >= 2048 workgroups across the chip.
+      const int64_t units = (int64_t)std::max(1, d->n_rows) * hblocks;
+      const int64_t want = std::max<int64_t>(1, cdiv(2048, units));
+      int64_t s = cdiv(max_kv, want);
+      s = std::max<int64_t>(64, cdiv(s, 64) * 64);
+      split = (int)std::min<int64_t>(s, 1 << 30);
+    }
+  }
+  *n_splits = (int)cdiv(max_kv, split);
+  if (*n_splits < 1) *n_splits = 1;
+  return split;
+}
+
+int validate(const cbis_attn_desc* d, const char* who) {
+  CBIS_REQUIRE(d, CBIS_ERR_INVALID, "%s: null descriptor", who);
+  CBIS_REQUIRE(d->head_dim == kHD && d->page_size == kPS, CBIS_ERR_UNSUPPORTED,
+               "%s: head_dim %d / page_size %d (this build supports 32 / 16)", who, d->head_dim, d->page_size);
+  CBIS_REQUIRE(d->kv_dtype == CBIS_F32 || d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: kv dtype", who);
+  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
+  CBIS_REQUIRE(d->n_heads > 0 && d->n_heads % hpb == 0, CBIS_ERR_UNSUPPORTED,
+               "%s: n_heads %d must be a multiple of %d for this K/V dtype", who, d->n_heads, hpb);
+  CBIS_REQUIRE(d->q_dtype == CBIS_F32 || d->q_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: q dtype", who);
+  CBIS_REQUIRE(d->out_dtype == CBIS_F32 || d->out_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: out dtype", who);
+  CBIS_REQUIRE(d->n_rows >= 0 && d->num_pages > 0 && d->bt_stride > 0, CBIS_ERR_INVALID, "%s: bad sizes", who);
+  CBIS_REQUIRE(d->q && d->k_pool && d->v_pool && d->block_table && d->out, CBIS_ERR_INVALID, "%s: null pointer", who);
+  CBIS_REQUIRE(d->ldo % 4 == 0 && ((uintptr_t)d->out & 15u) == 0, CBIS_ERR_INVALID, "%s: out rows must be 16-byte aligned", who);
+  CBIS_REQUIRE(((uintptr_t)d->k_pool & 15u) == 0 && ((uintptr_t)d->v_pool & 15u) == 0, CBIS_ERR_INVALID,
+               "%s: pools must be 16-byte aligned", who);
+  return CBIS_OK;
+}
+
+}  // namespace
+}  // namespace cbis
+
+using namespace cbis;
+
+extern "C" {
+
+size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d) {
+  if (!d || d->head_dim != kHD || d->n_heads <= 0) return 0;
+  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
+  int ns = 1;
+  resolve_split(d, std::max(1, d->n_heads / hpb), &ns);
+  if (ns <= 1) return 0;
+  return (size_t)d->n_rows * ns * d->n_heads * kWS * sizeof(float);
+}
+
+int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream) {
+  int rc = validate(d, "cbis_paged_attention");
+  if (rc) return rc;
+  CBIS_REQUIRE(d->row_pos, CBIS_ERR_INVALID, "cbis_paged_attention: null row_pos");
+  if (d->n_rows == 0) return CBIS_OK;
+  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
+  const int hblocks = d->n_heads / hpb;
+  int ns = 1;
+  const int split = resolve_split(d, hblocks, &ns);
+  if (ns > 1) {
+    const size_t need = (size_t)d->n_rows * ns * d->n_heads * kWS * sizeof(float);
+    CBIS_REQUIRE(d->workspace && d->workspace_bytes >= need, CBIS_ERR_WORKSPACE,
+                 "cbis_paged_attention: workspace %zu bytes, need %zu", d->workspace_bytes, need);
+  }
+  DecodeArgs a;
+  a.rows = d->rows;
+  a.q = d->q;
+  a.ldq = d->ldq;
+  a.q_bf16 = d->q_dtype == CBIS_BF16;
+  a.kpool = d->k_pool;
+  a.vpool = d->v_pool;
+  a.num_pages = d->num_pages;
+  a.bt = d->block_table;
+  a.bt_stride = d->bt_stride;
+  a.row_bt = d->row_bt;
+  a.row_pos = d->row_pos;
+  a.out = d->out;
+  a.ldo = d->ldo;
+  a.out_bf16 = d->out_dtype == CBIS_BF16;
+  a.ws = (float*)d->workspace;
+  a.n_heads = d->n_heads;
+  a.n_hblocks = hblocks;
+  a.n_splits = ns;
+  a.split_tokens = split;
+  a.max_kv = (int)std::min<int64_t>(d->bt_stride * kPS, 1 << 30);
+  a.qscale = kLog2e / sqrtf((float)kHD);
+  const int64_t grid = (int64_t)d->n_rows * ns * hblocks;
+  CBIS_REQUIRE(grid < (1LL << 31), CBIS_ERR_UNSUPPORTED, "cbis_paged_attention: grid too large");
+  hipStream_t s = (hipStream_t)stream;
+  if (d->kv_dtype == CBIS_F32) paged_decode_kernel<float, 4><<<(unsigned)grid, 256, 0, s>>>(a);
+  else paged_decode_kernel<uint16_t, 4><<<(unsigned)grid, 256, 0, s>>>(a);
+  rc = check_launch("cbis_paged_attention");
+  if (rc || ns <= 1) return rc;
+  const int64_t threads = (int64_t)d->n_rows * d->n_heads * kHD;
+  paged_decode_merge_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, s>>>(a, d->n_rows);
+  return check_launch("cbis_paged_attention(merge)");
+}
+
+int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int* tiles, cbis_stream_t stream) {
+  int rc = validate(d, "cbis_paged_prefill_attention");
+  if (rc) return rc;
+  CBIS_REQUIRE(d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_paged_prefill_attention: needs bf16 K/V");
+  CBIS_REQUIRE(d->n_heads % 4 == 0, CBIS_ERR_UNSUPPORTED, "cbis_paged_prefill_attention: n_heads %% 4");
+  CBIS_REQUIRE(n_tiles >= 0, CBIS_ERR_INVALID, "cbis_paged_prefill_attention: n_tiles < 0");
+  if (n_tiles == 0) return CBIS_OK;
+  CBIS_REQUIRE(tiles && ((uintptr_t)tiles & 15u) == 0, CBIS_ERR_INVALID,
+               "cbis_paged_prefill_attention: tiles must be a 16-byte aligned device array");
+  PrefillArgs a;
+  a.tiles = tiles;
+  a.q = d->q;
+  a.ldq = d->ldq;
+  a.q_bf16 = d->q_dtype == CBIS_BF16;
+  a.kpool = (const uint16_t*)d->k_pool;
+  a.vpool = (const uint16_t*)d->v_pool;
+  a.num_pages = d->num_pages;
+  a.bt = d->block_table;
+  a.bt_stride = d->bt_stride;
+  a.out = d->out;
+  a.ldo = d->ldo;
+  a.out_bf16 = d->out_dtype == CBIS_BF16;
+  a.n_heads = d->n_heads;
+  a.max_kv = (int)std::min<int64_t>(d->bt_stride * kPS, 1 << 30);
+  a.qscale = kLog2e / sqrtf((float)kHD);
+  const int64_t grid = (int64_t)n_tiles * (d->n_heads / 4);
+  paged_prefill_kernel<<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>(a);
+  return check_launch("cbis_paged_prefill_attention");
+}
+
+int cbis_fused_paged_causal_attention(const float* Q, const float* kp, const float* vp, const int* row_page_table,
+                                      const int* row_query_pos, float* out, int total_rows, int n_heads, int head_dim,
+                                      int page_size, int pages_per_seq, cbis_stream_t stream) {
+  cbis_attn_desc d = {};
+  d.n_rows = total_rows;
+  d.n_heads = n_heads;
+  d.head_dim = head_dim;
+  d.page_size = page_size;
+  d.q_dtype = CBIS_F32;
+  d.q = Q;
+  d.ldq = (int64_t)n_heads * head_dim;
+  d.kv_dtype = CBIS_F32;
+  d.k_pool = kp;
+  d.v_pool = vp;
+  d.num_pages = 0x7FFFFFFF;  // the reference launcher carries no pool size
+  d.block_table = row_page_table;
+  d.bt_stride = pages_per_seq;
+  d.row_pos = row_query_pos;
+  d.out_dtype = CBIS_F32;
+  d.out = out;
+  d.ldo = (int64_t)n_heads * head_dim;
+  d.max_kv_len = 0;  // single pass, no workspace
+  return cbis_paged_attention(&d, stream);
+}
+
+}  // extern "C"

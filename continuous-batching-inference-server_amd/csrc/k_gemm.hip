@@ -1,0 +1,371 @@
+// Flattened continuous-batch linear layers on gfx950 MFMA.
+//
+// Reference: linear_forward, kernels/linear.cu:15-34 -- cuBLAS SGEMM on the
+// row-major Y[T,out] = X[T,in] . W[out,in]^T identity of docs/gemm_layout.md
+// :16-41, then a separate bias launch (add_bias_rowmajor, :6-12), and in
+// src/transformer.cpp:82-89 separate GELU and residual launches.  Here one
+// kernel computes Y = epilogue(X . W^T) with the epilogue (per-channel fp8
+// scale, bias, exact-erf GELU, fp32 residual, K/V page scatter) applied to
+// the accumulators before the single store.
+//
+// Tiling.  Both operands are K-contiguous, so A (X) and B (W) tiles are
+// staged the same way: rows of 128 bytes of K (64 bf16 / 32 fp32) in LDS,
+// with the 16-byte chunk index XOR-swizzled by (row & 7) so the
+// ds_read_b128 fragment loads of 8 consecutive rows hit distinct banks.
+// Two LDS buffers; the next K tile is fetched into registers while the
+// current one feeds the MFMAs (one barrier per K step).  Each wave owns a
+// (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks:
+//   bf16 / fp8:  v_mfma_f32_32x32x16_bf16 (fp8 weights are decoded to bf16
+//                exactly when stored to LDS; the per-channel scale is applied
+//                in the epilogue),
+//   fp32:        v_mfma_f32_32x32x2_f32, four per ds_read_b128 fragment.
+// Workgroups are renumbered so that each XCD (dispatch is round-robin over
+// the 8 XCDs) receives a contiguous run of tiles, M-tile fastest, so the
+// workgroups sharing a W column block share one L2.
+// Optional split-K (gridDim.z) writes fp32 partials to a caller workspace
+// and a second kernel reduces them and applies the epilogue.
+#include "common.hpp"
+
+namespace cbis {
+namespace {
+
+struct GemmArgs {
+  int M, N, K;
+  const void* X;
+  int64_t ldx;
+  const void* W;
+  int64_t ldw;
+  const float* w_scale;
+  const float* bias;
+  int gelu;
+  const float* residual;
+  int64_t ldr;
+  int y_bf16;
+  void* Y;
+  int64_t ldy;
+  int kv_col0, kv_width, kv_bf16, page_size;
+  void* k_pool;
+  void* v_pool;
+  const int* wpage;
+  const int* woff;
+  int ksplit;     // gridDim.z
+  int k_per;      // K elements per split (multiple of BK)
+  float* partial; // [ksplit][M][N] when ksplit > 1
+};
+
+__device__ inline float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f)); }
+
+// Applies the epilogue to one accumulator and stores it.
+__device__ inline void epilogue_store(const GemmArgs& g, int row, int col, float v) {
+  if (g.w_scale) v *= g.w_scale[col];
+  if (g.bias) v += g.bias[col];
+  if (g.gelu) v = gelu_erf(v);
+  if (g.residual) v += g.residual[(int64_t)row * g.ldr + col];
+  if (g.k_pool && col >= g.kv_col0) {
+    const int c = col - g.kv_col0;
+    const bool is_v = c >= g.kv_width;
+    const int e = is_v ? c - g.kv_width : c;
+    const int64_t off = ((int64_t)g.wpage[row] * g.page_size + g.woff[row]) * g.kv_width + e;
+    void* pool = is_v ? g.v_pool : g.k_pool;
+    if (g.kv_bf16) ((uint16_t*)pool)[off] = f32_to_bf16(v);
+    else ((float*)pool)[off] = v;
+    return;
+  }
+  const int64_t o = (int64_t)row * g.ldy + col;
+  if (g.y_bf16) ((uint16_t*)g.Y)[o] = f32_to_bf16(v);
+  else ((float*)g.Y)[o] = v;
+}
+
+template <typename WT>
+struct WLoad;  // global W chunk (covering 16 bytes of LDS) -> uint4 of the compute type
+template <>
+struct WLoad<float> {
+  typedef uint4 raw_t;
+  static constexpr int EPC = 4;
+  __device__ static inline raw_t load(const float* p) { return *(const uint4*)p; }
+  __device__ static inline uint4 cvt(const raw_t& r) { return r; }
+};
+template <>
+struct WLoad<uint16_t> {
+  typedef uint4 raw_t;
+  static constexpr int EPC = 8;
+  __device__ static inline raw_t load(const uint16_t* p) { return *(const uint4*)p; }
+  __device__ static inline uint4 cvt(const raw_t& r) { return r; }
+};
+template <>
+struct WLoad<uint8_t> {
+  typedef uint2 raw_t;
+  static constexpr int EPC = 8;
+  __device__ static inline raw_t load(const uint8_t* p) { return *(const uint2*)p; }
+  __device__ static inline uint4 cvt(const raw_t& r) {
+    uint4 o;
+    o.x = (uint32_t)e4m3_to_bf16(r.x & 0xFF) | ((uint32_t)e4m3_to_bf16((r.x >> 8) & 0xFF) << 16);
+    o.y = (uint32_t)e4m3_to_bf16((r.x >> 16) & 0xFF) | ((uint32_t)e4m3_to_bf16(r.x >> 24) << 16);
+    o.z = (uint32_t)e4m3_to_bf16(r.y & 0xFF) | ((uint32_t)e4m3_to_bf16((r.y >> 8) & 0xFF) << 16);
+    o.w = (uint32_t)e4m3_to_bf16((r.y >> 16) & 0xFF) | ((uint32_t)e4m3_to_bf16(r.y >> 24) << 16);
+    return o;
+  }
+};
+
+__device__ inline int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+
+template <int BM, int BN, int WM, int WN, typename XT, typename WT>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
+  constexpr bool F32 = sizeof(XT) == 4;
+  constexpr int NT = WM * WN * 64;
+  constexpr int BK = F32 ? 32 : 64;       // K elements per 128-byte LDS row
+  constexpr int XE = F32 ? 4 : 8;         // X elements per 16-byte chunk
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int A_PER = BM * 8 / NT, B_PER = BN * 8 / NT;
+  static_assert(A_PER * NT == BM * 8 && B_PER * NT == BN * 8, "tile / thread mismatch");
+  typedef WLoad<WT> WL;
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  // buffer b: A tile at smem + b*(BM+BN)*128, B tile right after it
+  auto lA = [&](int b) { return smem + b * (BM + BN) * 128; };
+  auto lB = [&](int b) { return smem + b * (BM + BN) * 128 + BM * 128; };
+
+  // Tile index with XCD-contiguous renumbering.
+  const int mt = (g.M + BM - 1) / BM;
+  const int nwg = gridDim.x;
+  int bid = blockIdx.x;
+  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  const int tm = bid % mt, tn = bid / mt;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kz = blockIdx.z;
+  const int kbeg = kz * g.k_per;
+  const int KT = min(g.k_per, g.K - kbeg) / BK;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int half = lane >> 5, l32 = lane & 31;
+
+  const XT* X = (const XT*)g.X;
+  const WT* W = (const WT*)g.W;
+
+  uint4 ra[A_PER];
+  typename WL::raw_t rb[B_PER];
+
+  auto gload = [&](int kt) {
+    const int k0 = kbeg + kt * BK;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int c = tid + i * NT;
+      const int r = c >> 3, kc = c & 7;
+      const int gr = min(m0 + r, g.M - 1);
+      ra[i] = *(const uint4*)(X + (int64_t)gr * g.ldx + k0 + kc * XE);
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      const int c = tid + i * NT;
+      const int r = c >> 3, kc = c & 7;
+      const int gr = min(n0 + r, g.N - 1);
+      rb[i] = WL::load(W + (int64_t)gr * g.ldw + k0 + kc * WL::EPC);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int c = tid + i * NT;
+      *(uint4*)(lA(buf) + swz(c >> 3, c & 7)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      const int c = tid + i * NT;
+      *(uint4*)(lB(buf) + swz(c >> 3, c & 7)) = WL::cvt(rb[i]);
+    }
+  };
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) gload(kt + 1);
+    const uint8_t* A = lA(buf);
+    const uint8_t* B = lB(buf);
+    if constexpr (F32) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int kc = 2 * j + half;
+        f32x4_t af[FM], bf[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[i] = *(const f32x4_t*)(A + swz(wm * TM + i * 32 + l32, kc));
+#pragma unroll
+        for (int i = 0; i < FN; ++i) bf[i] = *(const f32x4_t*)(B + swz(wn * TN + i * 32 + l32, kc));
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int jj = 0; jj < FN; ++jj)
+              acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][e], bf[jj][e], acc[i][jj], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int kc = 2 * ks + half;
+        bf16x8_t af[FM], bf[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[i] = *(const bf16x8_t*)(A + swz(wm * TM + i * 32 + l32, kc));
+#pragma unroll
+        for (int i = 0; i < FN; ++i) bf[i] = *(const bf16x8_t*)(B + swz(wn * TN + i * 32 + l32, kc));
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < FN; ++jj)
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[jj], acc[i][jj], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < KT) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue straight from the accumulators: acc[i][j][e] is row
+  // 8*(e/4) + 4*half + (e%4), column l32 of block (i, j).
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + wn * TN + j * 32 + l32;
+      if (col >= g.N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+        if (row >= g.M) continue;
+        if (g.ksplit > 1) g.partial[((int64_t)kz * g.M + row) * g.N + col] = acc[i][j][e];
+        else epilogue_store(g, row, col, acc[i][j][e]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs g) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t MN = (int64_t)g.M * g.N;
+  if (idx >= MN) return;
+  float v = 0.f;
+  for (int z = 0; z < g.ksplit; ++z) v += g.partial[z * MN + idx];
+  epilogue_store(g, (int)(idx / g.N), (int)(idx % g.N), v);
+}
+
+template <int BM, int BN, int WM, int WN, typename XT, typename WT>
+int launch(const GemmArgs& g, hipStream_t s) {
+  const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
+  const size_t lds = 2 * (size_t)(BM + BN) * 128;
+  auto k = gemm_kernel<BM, BN, WM, WN, XT, WT>;
+  static bool attr_set = false;  // raise the dynamic-LDS cap once per instantiation
+  if (!attr_set && lds > 65536) {
+    (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr_set = true;
+  }
+  k<<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, lds, s>>>(g);
+  int rc = check_launch("cbis_gemm");
+  if (rc || g.ksplit <= 1) return rc;
+  splitk_reduce_kernel<<<(unsigned)cdiv((int64_t)g.M * g.N, 256), 256, 0, s>>>(g);
+  return check_launch("cbis_gemm(split-k reduce)");
+}
+
+// Picks a tile shape from the problem size: the largest tile that still
+// gives the 256 CUs at least about one workgroup each.
+template <typename XT, typename WT>
+int dispatch(const GemmArgs& g, hipStream_t s) {
+  const int64_t t128 = cdiv(g.M, 128) * cdiv(g.N, 128);
+  if constexpr (sizeof(XT) == 4) {
+    if (t128 >= 192) return launch<128, 128, 2, 2, XT, WT>(g, s);
+    if (g.M <= 32) return launch<32, 64, 1, 2, XT, WT>(g, s);
+    return launch<64, 64, 2, 2, XT, WT>(g, s);
+  } else {
+    if (t128 >= 192) return launch<128, 128, 2, 2, XT, WT>(g, s);
+    if (g.M <= 32) return launch<32, 128, 1, 4, XT, WT>(g, s);
+    return launch<64, 128, 2, 2, XT, WT>(g, s);
+  }
+}
+
+}  // namespace
+}  // namespace cbis
+
+using namespace cbis;
+
+extern "C" {
+
+// Bytes of split-K workspace cbis_gemm would use for this problem if given;
+// 0 when it runs without split-K.  (Exposed for callers that want to give a
+// workspace; cbis_gemm runs without one.)
+int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
+  CBIS_REQUIRE(d, CBIS_ERR_INVALID, "cbis_gemm: null descriptor");
+  CBIS_REQUIRE(d->M >= 0 && d->N > 0 && d->K > 0, CBIS_ERR_INVALID, "cbis_gemm: bad M/N/K %d/%d/%d", d->M, d->N, d->K);
+  if (d->M == 0) return CBIS_OK;
+  CBIS_REQUIRE(d->X && d->W, CBIS_ERR_INVALID, "cbis_gemm: null X/W");
+  const bool f32 = d->x_dtype == CBIS_F32;
+  CBIS_REQUIRE((f32 && d->w_dtype == CBIS_F32) ||
+                   (d->x_dtype == CBIS_BF16 && (d->w_dtype == CBIS_BF16 || d->w_dtype == CBIS_FP8E4M3)),
+               CBIS_ERR_UNSUPPORTED, "cbis_gemm: x dtype %d with w dtype %d", d->x_dtype, d->w_dtype);
+  const int bk = f32 ? 32 : 64;
+  CBIS_REQUIRE(d->K % bk == 0, CBIS_ERR_UNSUPPORTED, "cbis_gemm: K=%d must be a multiple of %d", d->K, bk);
+  const int xe = f32 ? 4 : 2;
+  const int we = d->w_dtype == CBIS_F32 ? 4 : (d->w_dtype == CBIS_BF16 ? 2 : 1);
+  CBIS_REQUIRE(((uintptr_t)d->X & 15u) == 0 && (d->ldx * xe) % 16 == 0 && d->ldx >= d->K, CBIS_ERR_INVALID,
+               "cbis_gemm: X rows must be 16-byte aligned");
+  CBIS_REQUIRE(((uintptr_t)d->W & 7u) == 0 && (d->ldw * we) % 8 == 0 && d->ldw >= d->K, CBIS_ERR_INVALID,
+               "cbis_gemm: W rows must be 8-byte aligned");
+  CBIS_REQUIRE(d->w_dtype != CBIS_FP8E4M3 || d->w_scale, CBIS_ERR_INVALID, "cbis_gemm: fp8 weights need w_scale");
+  CBIS_REQUIRE(d->y_dtype == CBIS_F32 || d->y_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_gemm: y dtype");
+  CBIS_REQUIRE(d->epilogue == CBIS_EPI_NONE || d->epilogue == CBIS_EPI_GELU, CBIS_ERR_INVALID, "cbis_gemm: epilogue");
+  const bool kv = d->k_pool != nullptr;
+  if (kv) {
+    CBIS_REQUIRE(d->v_pool && d->write_page && d->write_offset && d->kv_width > 0 && d->page_size > 0 &&
+                     d->kv_col0 >= 0 && d->kv_col0 + 2 * d->kv_width == d->N,
+                 CBIS_ERR_INVALID, "cbis_gemm: K/V scatter needs kv_col0 + 2*kv_width == N and slot arrays");
+    CBIS_REQUIRE(d->kv_dtype == CBIS_F32 || d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_gemm: kv dtype");
+  }
+  CBIS_REQUIRE(!(kv && d->kv_col0 == 0) ? (d->Y != nullptr) : true, CBIS_ERR_INVALID, "cbis_gemm: null Y");
+
+  GemmArgs g;
+  g.M = d->M; g.N = d->N; g.K = d->K;
+  g.X = d->X; g.ldx = d->ldx;
+  g.W = d->W; g.ldw = d->ldw;
+  g.w_scale = d->w_scale;
+  g.bias = d->bias;
+  g.gelu = d->epilogue == CBIS_EPI_GELU;
+  g.residual = d->residual; g.ldr = d->ldr;
+  g.y_bf16 = d->y_dtype == CBIS_BF16;
+  g.Y = d->Y; g.ldy = d->ldy;
+  g.kv_col0 = kv ? d->kv_col0 : 0x7FFFFFFF;
+  g.kv_width = d->kv_width; g.kv_bf16 = d->kv_dtype == CBIS_BF16; g.page_size = d->page_size;
+  g.k_pool = kv ? d->k_pool : nullptr; g.v_pool = d->v_pool;
+  g.wpage = d->write_page; g.woff = d->write_offset;
+  g.ksplit = 1;
+  g.k_per = d->K;
+  g.partial = nullptr;
+
+  hipStream_t s = (hipStream_t)stream;
+  if (f32) return dispatch<float, float>(g, s);
+  if (d->w_dtype == CBIS_BF16) return dispatch<uint16_t, uint16_t>(g, s);
+  return dispatch<uint16_t, uint8_t>(g, s);
+}
+
+int cbis_linear_forward(const float* X, const float* W, const float* b, float* Y, int T, int in_features,
+                        int out_features, cbis_stream_t stream) {
+  cbis_gemm_desc d = {};
+  d.M = T; d.N = out_features; d.K = in_features;
+  d.x_dtype = CBIS_F32; d.X = X; d.ldx = in_features;
+  d.w_dtype = CBIS_F32; d.W = W; d.ldw = in_features;
+  d.bias = b;
+  d.y_dtype = CBIS_F32; d.Y = Y; d.ldy = out_features;
+  return cbis_gemm(&d, stream);
+}
+
+}  // extern "C"

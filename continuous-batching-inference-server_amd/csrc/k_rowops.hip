@@ -1,0 +1,419 @@
+// Row and elementwise kernels of the per-step forward, wave64-native:
+// embedding gather (kernels/elementwise.cu:7-17), LayerNorm
+// (kernels/elementwise.cu:21-57), GELU (:59-66), residual add (:68-73),
+// K/V page scatter (kernels/attention.cu:7-19), greedy argmax
+// (src/bench_batching.cpp:66-73) and the synthetic-data fills.
+//
+// LayerNorm runs one wave per row with the row held in registers (two-pass
+// mean / variance over registers, DPP/shuffle reductions), instead of the
+// reference's one 256-thread block per row with a shared-memory tree.
+#include <cstdarg>
+
+#include "common.hpp"
+
+namespace cbis {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(CBIS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return CBIS_OK;
+}
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Embedding: one wave per row, 16-byte accesses.
+// ---------------------------------------------------------------------------
+template <typename ET>
+__global__ __launch_bounds__(256) void embed_kernel(int T, int D, const int* __restrict__ tok,
+                                                    const int* __restrict__ pos, const ET* __restrict__ te,
+                                                    const ET* __restrict__ pe, int vocab, int max_pos,
+                                                    float* __restrict__ out) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const int lane = threadIdx.x & 63;
+  const int t = min(max(tok[row], 0), vocab - 1);
+  const int p = min(max(pos[row], 0), max_pos - 1);
+  const ET* a = te + (int64_t)t * D;
+  const ET* b = pe + (int64_t)p * D;
+  float* o = out + (int64_t)row * D;
+  for (int c = lane * 4; c < D; c += 256) {
+    float4 r;
+    if constexpr (sizeof(ET) == 4) {
+      const float4 x = *(const float4*)(a + c);
+      const float4 y = *(const float4*)(b + c);
+      r = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+    } else {
+      const uint2 x = *(const uint2*)(a + c);
+      const uint2 y = *(const uint2*)(b + c);
+      r = make_float4(bf16lo(x.x) + bf16lo(y.x), bf16hi(x.x) + bf16hi(y.x), bf16lo(x.y) + bf16lo(y.y),
+                      bf16hi(x.y) + bf16hi(y.y));
+    }
+    *(float4*)(o + c) = r;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm: one wave per row; VPL float4 per lane held in registers.
+// ---------------------------------------------------------------------------
+template <int VPL, typename YT>
+__global__ __launch_bounds__(256) void layernorm_kernel(int T, int D, const float* __restrict__ X, int64_t ldx,
+                                                        const float* __restrict__ g, const float* __restrict__ b,
+                                                        float eps, YT* __restrict__ Y, int64_t ldy) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const int lane = threadIdx.x & 63;
+  const float* x = X + (int64_t)row * ldx;
+  float4 v[VPL];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 4;
+    v[i] = c < D ? *(const float4*)(x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  }
+  const float mean = wave_sum(s) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 4;
+    if (c < D) {
+      const float a0 = v[i].x - mean, a1 = v[i].y - mean, a2 = v[i].z - mean, a3 = v[i].w - mean;
+      q += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+    }
+  }
+  const float inv = rsqrtf(wave_sum(q) / (float)D + eps);
+  YT* y = Y + (int64_t)row * ldy;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 4;
+    if (c >= D) continue;
+    const float4 gg = *(const float4*)(g + c);
+    const float4 bb = *(const float4*)(b + c);
+    const float o0 = (v[i].x - mean) * inv * gg.x + bb.x;
+    const float o1 = (v[i].y - mean) * inv * gg.y + bb.y;
+    const float o2 = (v[i].z - mean) * inv * gg.z + bb.z;
+    const float o3 = (v[i].w - mean) * inv * gg.w + bb.w;
+    if constexpr (sizeof(YT) == 4) {
+      *(float4*)(y + c) = make_float4(o0, o1, o2, o3);
+    } else {
+      *(uint2*)(y + c) = make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
+    }
+  }
+}
+
+__global__ void gelu_kernel(float* X, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const float v = X[i];
+    X[i] = 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+  }
+}
+
+__global__ void residual_kernel(float* X, const float* Y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) X[i] += Y[i];
+}
+
+// One wave per row; the row's d_model floats of K and V land contiguously in
+// their slot, so the copy is two coalesced streams.
+__global__ __launch_bounds__(256) void scatter_kv_kernel(int rows, int D, const float* __restrict__ K,
+                                                         const float* __restrict__ V, float* __restrict__ kp,
+                                                         float* __restrict__ vp, const int* __restrict__ wpage,
+                                                         const int* __restrict__ woff, int page_size) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t base = ((int64_t)wpage[row] * page_size + woff[row]) * D;
+  for (int c = lane; c < D; c += 64) {
+    kp[base + c] = K[(int64_t)row * D + c];
+    vp[base + c] = V[(int64_t)row * D + c];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Greedy argmax: one 256-thread block per row; (value, index) pairs reduced
+// with the lowest index winning ties, as a sequential strict-> scan does.
+// ---------------------------------------------------------------------------
+__device__ inline void argmax_combine(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(int N, const float* __restrict__ L, int64_t ld,
+                                                     int* __restrict__ out) {
+  const float* row = L + (int64_t)blockIdx.x * ld;
+  float bv = -INFINITY;
+  int bi = 0x7FFFFFFF;
+  for (int c = threadIdx.x; c < N; c += 256) argmax_combine(bv, bi, row[c], c);
+  for (int off = 32; off > 0; off >>= 1) {
+    const float v2 = __shfl_xor(bv, off, 64);
+    const int i2 = __shfl_xor(bi, off, 64);
+    argmax_combine(bv, bi, v2, i2);
+  }
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[w] = bv;
+    si[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 4; ++k) argmax_combine(bv, bi, sv[k], si[k]);
+    // A row that is all -inf (or NaN) keeps index 0, like the sequential scan.
+    out[blockIdx.x] = (bi == 0x7FFFFFFF) ? 0 : bi;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic fills.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void fill_exact_kernel(T* dst, int64_t n, uint64_t key, uint64_t start, double stddev) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float f = (float)(stddev * normal_exact(key, start + (uint64_t)i));
+    if constexpr (sizeof(T) == 4) dst[i] = f;
+    else dst[i] = f32_to_bf16(f);
+  }
+}
+
+__device__ inline uint32_t hash32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7FEB352Du;
+  x ^= x >> 15;
+  x *= 0x846CA68Bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// Two normals per 32-bit hash (Box-Muller on two 16-bit uniforms).
+template <typename T>
+__global__ void fill_fast_kernel(T* dst, int64_t n, uint32_t k0, uint32_t k1, float stddev) {
+  const int64_t npair = (n + 1) / 2;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < npair; i += (int64_t)gridDim.x * blockDim.x) {
+    const uint32_t h = hash32((uint32_t)i ^ hash32((uint32_t)(i >> 32) ^ k0) ^ k1);
+    const float u1 = ((float)(h >> 16) + 0.5f) * (1.0f / 65536.0f);
+    const float u2 = ((float)(h & 0xFFFFu) + 0.5f) * (1.0f / 65536.0f);
+    const float r = stddev * sqrtf(-2.0f * __logf(u1));
+    float sn, cs;
+    __sincosf(6.283185307179586f * u2, &sn, &cs);
+    const float z0 = r * cs, z1 = r * sn;
+    const int64_t j = 2 * i;
+    if constexpr (sizeof(T) == 4) {
+      dst[j] = z0;
+      if (j + 1 < n) dst[j + 1] = z1;
+    } else {
+      dst[j] = f32_to_bf16(z0);
+      if (j + 1 < n) dst[j + 1] = f32_to_bf16(z1);
+    }
+  }
+}
+
+// One 256-thread block per weight row: absmax, then quantise.
+__global__ __launch_bounds__(256) void quantize_fp8_rows_kernel(uint8_t* codes, float* scale, const float* src,
+                                                                int K) {
+  const int n = blockIdx.x;
+  const float* row = src + (int64_t)n * K;
+  float amax = 0.f;
+  for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(row[k]));
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  __shared__ float sm[4];
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+  float sc = amax / 448.0f;
+  if (sc == 0.f) sc = 1.f;
+  if (threadIdx.x == 0) scale[n] = sc;
+  for (int k = threadIdx.x; k < K; k += 256) codes[(int64_t)n * K + k] = f32_to_e4m3(row[k] / sc);
+}
+
+template <typename T>
+__global__ void convert_kernel(T* dst, const float* src, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if constexpr (sizeof(T) == 4) dst[i] = src[i];
+    else dst[i] = f32_to_bf16(src[i]);
+  }
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+}  // namespace cbis
+
+using namespace cbis;
+
+extern "C" {
+
+const char* cbis_last_error(void) { return g_last_error.c_str(); }
+
+int cbis_embed(int T, int D, const int* tok, const int* pos, int emb_dtype, const void* te, const void* pe, int vocab,
+               int max_pos, float* out, cbis_stream_t stream) {
+  CBIS_REQUIRE(T >= 0 && D > 0 && D % 4 == 0, CBIS_ERR_INVALID, "cbis_embed: bad T=%d d_model=%d", T, D);
+  CBIS_REQUIRE(vocab > 0 && max_pos > 0, CBIS_ERR_INVALID, "cbis_embed: vocab/max_pos must be > 0");
+  if (T == 0) return CBIS_OK;
+  CBIS_REQUIRE(tok && pos && te && pe && out, CBIS_ERR_INVALID, "cbis_embed: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)cdiv(T, 4));
+  if (emb_dtype == CBIS_F32)
+    embed_kernel<float><<<grid, 256, 0, s>>>(T, D, tok, pos, (const float*)te, (const float*)pe, vocab, max_pos, out);
+  else if (emb_dtype == CBIS_BF16)
+    embed_kernel<uint16_t><<<grid, 256, 0, s>>>(T, D, tok, pos, (const uint16_t*)te, (const uint16_t*)pe, vocab,
+                                                max_pos, out);
+  else
+    return fail(CBIS_ERR_UNSUPPORTED, "cbis_embed: embedding dtype %d", emb_dtype);
+  return check_launch("cbis_embed");
+}
+
+int cbis_layernorm(int T, int D, const float* X, int64_t ldx, const float* g, const float* b, float eps, int y_dtype,
+                   void* Y, int64_t ldy, cbis_stream_t stream) {
+  CBIS_REQUIRE(T >= 0 && D > 0 && D % 4 == 0 && D <= 8192, CBIS_ERR_UNSUPPORTED,
+               "cbis_layernorm: d_model %d (needs a multiple of 4, <= 8192)", D);
+  if (T == 0) return CBIS_OK;
+  CBIS_REQUIRE(X && g && b && Y, CBIS_ERR_INVALID, "cbis_layernorm: null pointer");
+  CBIS_REQUIRE(ldx % 4 == 0 && ldy % 4 == 0 && aligned16(X), CBIS_ERR_INVALID, "cbis_layernorm: misaligned rows");
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)cdiv(T, 4));
+  const int vpl = (int)cdiv(D, 256);
+#define CBIS_LN(V)                                                                                         \
+  if (y_dtype == CBIS_F32)                                                                                 \
+    layernorm_kernel<V, float><<<grid, 256, 0, s>>>(T, D, X, ldx, g, b, eps, (float*)Y, ldy);             \
+  else                                                                                                     \
+    layernorm_kernel<V, uint16_t><<<grid, 256, 0, s>>>(T, D, X, ldx, g, b, eps, (uint16_t*)Y, ldy);
+  CBIS_REQUIRE(y_dtype == CBIS_F32 || y_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_layernorm: y dtype");
+  if (vpl <= 1) { CBIS_LN(1) }
+  else if (vpl <= 2) { CBIS_LN(2) }
+  else if (vpl <= 4) { CBIS_LN(4) }
+  else if (vpl <= 8) { CBIS_LN(8) }
+  else if (vpl <= 16) { CBIS_LN(16) }
+  else { CBIS_LN(32) }
+#undef CBIS_LN
+  return check_launch("cbis_layernorm");
+}
+
+int cbis_argmax_rows(int T, int N, const float* L, int64_t ld, int* out, cbis_stream_t stream) {
+  CBIS_REQUIRE(T >= 0 && N > 0 && ld >= N, CBIS_ERR_INVALID, "cbis_argmax_rows: bad sizes");
+  if (T == 0) return CBIS_OK;
+  CBIS_REQUIRE(L && out, CBIS_ERR_INVALID, "cbis_argmax_rows: null pointer");
+  argmax_kernel<<<T, 256, 0, (hipStream_t)stream>>>(N, L, ld, out);
+  return check_launch("cbis_argmax_rows");
+}
+
+int cbis_fill_normal_exact(void* dst, int dtype, int64_t n, uint64_t seed, uint64_t stream_id, uint64_t start,
+                           float stddev, cbis_stream_t stream) {
+  CBIS_REQUIRE(n >= 0, CBIS_ERR_INVALID, "cbis_fill_normal_exact: n < 0");
+  if (n == 0) return CBIS_OK;
+  CBIS_REQUIRE(dst, CBIS_ERR_INVALID, "cbis_fill_normal_exact: null dst");
+  const uint64_t key = prng_key(seed, stream_id);
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(n, 256), 65536);
+  if (dtype == CBIS_F32)
+    fill_exact_kernel<float><<<blocks, 256, 0, (hipStream_t)stream>>>((float*)dst, n, key, start, (double)stddev);
+  else if (dtype == CBIS_BF16)
+    fill_exact_kernel<uint16_t><<<blocks, 256, 0, (hipStream_t)stream>>>((uint16_t*)dst, n, key, start,
+                                                                          (double)stddev);
+  else
+    return fail(CBIS_ERR_UNSUPPORTED, "cbis_fill_normal_exact: dtype %d", dtype);
+  return check_launch("cbis_fill_normal_exact");
+}
+
+int cbis_fill_normal_fast(void* dst, int dtype, int64_t n, uint64_t seed, float stddev, cbis_stream_t stream) {
+  CBIS_REQUIRE(n >= 0, CBIS_ERR_INVALID, "cbis_fill_normal_fast: n < 0");
+  if (n == 0) return CBIS_OK;
+  CBIS_REQUIRE(dst, CBIS_ERR_INVALID, "cbis_fill_normal_fast: null dst");
+  const uint64_t key = mix64(seed + kGolden);
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv((n + 1) / 2, 256), 1 << 20);
+  if (dtype == CBIS_F32)
+    fill_fast_kernel<float><<<blocks, 256, 0, (hipStream_t)stream>>>((float*)dst, n, (uint32_t)key,
+                                                                      (uint32_t)(key >> 32), stddev);
+  else if (dtype == CBIS_BF16)
+    fill_fast_kernel<uint16_t><<<blocks, 256, 0, (hipStream_t)stream>>>((uint16_t*)dst, n, (uint32_t)key,
+                                                                         (uint32_t)(key >> 32), stddev);
+  else
+    return fail(CBIS_ERR_UNSUPPORTED, "cbis_fill_normal_fast: dtype %d", dtype);
+  return check_launch("cbis_fill_normal_fast");
+}
+
+int cbis_convert_f32(void* dst, int dst_dtype, const float* src, int64_t n, cbis_stream_t stream) {
+  CBIS_REQUIRE(n >= 0, CBIS_ERR_INVALID, "cbis_convert_f32: n < 0");
+  if (n == 0) return CBIS_OK;
+  CBIS_REQUIRE(dst && src, CBIS_ERR_INVALID, "cbis_convert_f32: null pointer");
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(n, 256), 65536);
+  if (dst_dtype == CBIS_F32)
+    convert_kernel<float><<<blocks, 256, 0, (hipStream_t)stream>>>((float*)dst, src, n);
+  else if (dst_dtype == CBIS_BF16)
+    convert_kernel<uint16_t><<<blocks, 256, 0, (hipStream_t)stream>>>((uint16_t*)dst, src, n);
+  else
+    return fail(CBIS_ERR_UNSUPPORTED, "cbis_convert_f32: dtype %d", dst_dtype);
+  return check_launch("cbis_convert_f32");
+}
+
+int cbis_quantize_fp8_rows(uint8_t* codes, float* scale, const float* src, int N, int K, cbis_stream_t stream) {
+  CBIS_REQUIRE(N >= 0 && K > 0, CBIS_ERR_INVALID, "cbis_quantize_fp8_rows: bad sizes");
+  if (N == 0) return CBIS_OK;
+  CBIS_REQUIRE(codes && scale && src, CBIS_ERR_INVALID, "cbis_quantize_fp8_rows: null pointer");
+  quantize_fp8_rows_kernel<<<N, 256, 0, (hipStream_t)stream>>>(codes, scale, src, K);
+  return check_launch("cbis_quantize_fp8_rows");
+}
+
+// ----------------------------- reference signatures ------------------------
+
+int cbis_embed_lookup_add(const int* token_ids, const int* positions, const float* tok_emb, const float* pos_emb,
+                          float* out, int T, int d_model, cbis_stream_t stream) {
+  // The reference launcher has no vocab / table sizes; ids are trusted as
+  // there (kernels/elementwise.cu:7-17).
+  return cbis_embed(T, d_model, token_ids, positions, CBIS_F32, tok_emb, pos_emb, 0x7FFFFFFF, 0x7FFFFFFF, out,
+                    stream);
+}
+
+int cbis_layernorm_forward(const float* X, const float* gamma, const float* beta, float* Y, int T, int d_model,
+                           cbis_stream_t stream) {
+  return cbis_layernorm(T, d_model, X, d_model, gamma, beta, 1e-5f, CBIS_F32, Y, d_model, stream);
+}
+
+int cbis_gelu_forward(float* X, int T, int width, cbis_stream_t stream) {
+  CBIS_REQUIRE(T >= 0 && width >= 0, CBIS_ERR_INVALID, "cbis_gelu_forward: bad sizes");
+  const int64_t n = (int64_t)T * width;
+  if (n == 0) return CBIS_OK;
+  CBIS_REQUIRE(X, CBIS_ERR_INVALID, "cbis_gelu_forward: null pointer");
+  gelu_kernel<<<(unsigned)cdiv(n, 256), 256, 0, (hipStream_t)stream>>>(X, n);
+  return check_launch("cbis_gelu_forward");
+}
+
+int cbis_residual_add(float* X, const float* Y, int T, int width, cbis_stream_t stream) {
+  CBIS_REQUIRE(T >= 0 && width >= 0, CBIS_ERR_INVALID, "cbis_residual_add: bad sizes");
+  const int64_t n = (int64_t)T * width;
+  if (n == 0) return CBIS_OK;
+  CBIS_REQUIRE(X && Y, CBIS_ERR_INVALID, "cbis_residual_add: null pointer");
+  residual_kernel<<<(unsigned)cdiv(n, 256), 256, 0, (hipStream_t)stream>>>(X, Y, n);
+  return check_launch("cbis_residual_add");
+}
+
+int cbis_scatter_kv_to_cache(const float* K, const float* V, float* kp, float* vp, const int* wpage, const int* woff,
+                             int total_rows, int d_model, int page_size, int n_heads, int head_dim,
+                             cbis_stream_t stream) {
+  CBIS_REQUIRE(total_rows >= 0 && d_model == n_heads * head_dim && page_size > 0, CBIS_ERR_INVALID,
+               "cbis_scatter_kv_to_cache: d_model %d != n_heads %d * head_dim %d", d_model, n_heads, head_dim);
+  if (total_rows == 0) return CBIS_OK;
+  CBIS_REQUIRE(K && V && kp && vp && wpage && woff, CBIS_ERR_INVALID, "cbis_scatter_kv_to_cache: null pointer");
+  scatter_kv_kernel<<<(unsigned)cdiv(total_rows, 4), 256, 0, (hipStream_t)stream>>>(total_rows, d_model, K, V, kp,
+                                                                                     vp, wpage, woff, page_size);
+  return check_launch("cbis_scatter_kv_to_cache");
+}
+
+}  // extern "C"

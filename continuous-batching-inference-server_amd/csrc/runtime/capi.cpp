@@ -1,0 +1,237 @@
+// extern "C" wrappers of the C++ runtime (include/cbis_runtime.h).  C++
+// exceptions stop here: they become negative return codes (or NULL) with the
+// message in cbis_runtime_last_error().
+#include <cstring>
+
+#include "cbis_runtime.h"
+#include "runtime.hpp"
+
+using namespace cbis;
+
+struct cbis_cache {
+  std::unique_ptr<PagedKVCache> impl;
+};
+struct cbis_weights {
+  std::unique_ptr<ModelWeights> impl;
+};
+struct cbis_runner {
+  std::unique_ptr<TransformerRunner> impl;
+};
+
+namespace {
+thread_local std::string g_err;
+
+template <typename F>
+int guard(F&& f) {
+  try {
+    return f();
+  } catch (const std::out_of_range& e) {
+    g_err = std::string("out_of_range: ") + e.what();
+    return -2;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+template <typename T, typename F>
+T* guard_ptr(F&& f) {
+  try {
+    return f();
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return nullptr;
+  }
+}
+
+ModelConfig to_cfg(const cbis_model_config* c) {
+  if (!c) throw std::invalid_argument("null config");
+  ModelConfig m;
+  m.vocab = c->vocab; m.d_model = c->d_model; m.n_heads = c->n_heads; m.head_dim = c->head_dim;
+  m.n_layers = c->n_layers; m.mlp = c->mlp; m.max_seq = c->max_seq; m.page_size = c->page_size;
+  m.weight_dtype = c->weight_dtype; m.kv_dtype = c->kv_dtype;
+  m.validate();
+  return m;
+}
+}  // namespace
+
+extern "C" {
+
+const char* cbis_runtime_last_error(void) { return g_err.c_str(); }
+
+void cbis_default_config(cbis_model_config* c) {
+  ModelConfig m;
+  c->vocab = m.vocab; c->d_model = m.d_model; c->n_heads = m.n_heads; c->head_dim = m.head_dim;
+  c->n_layers = m.n_layers; c->mlp = m.mlp; c->max_seq = m.max_seq; c->page_size = m.page_size;
+  c->weight_dtype = m.weight_dtype; c->kv_dtype = m.kv_dtype;
+}
+
+cbis_cache* cbis_cache_create(int num_layers, int max_pages, int page_size, int n_heads, int head_dim, int kv_dtype,
+                              int pages_per_seq, int alloc_device) {
+  return guard_ptr<cbis_cache>([&] {
+    auto* c = new cbis_cache();
+    try {
+      c->impl.reset(new PagedKVCache(num_layers, max_pages, page_size, n_heads, head_dim, kv_dtype, pages_per_seq,
+                                     alloc_device != 0));
+    } catch (...) {
+      delete c;
+      throw;
+    }
+    return c;
+  });
+}
+
+void cbis_cache_destroy(cbis_cache* c) { delete c; }
+
+int cbis_cache_allocate_sequence(cbis_cache* c) { return guard([&] { return c->impl->allocate_sequence(); }); }
+
+void cbis_cache_free_sequence(cbis_cache* c, int seq_id) { c->impl->free_sequence(seq_id); }
+
+int cbis_cache_ensure_capacity(cbis_cache* c, int seq_id, int token_pos) {
+  return guard([&] { return c->impl->ensure_capacity(seq_id, token_pos) ? 1 : 0; });
+}
+
+int cbis_cache_resolve_slot(cbis_cache* c, int seq_id, int token_pos, int* page, int* offset) {
+  return guard([&] {
+    c->impl->resolve_slot(seq_id, token_pos, page, offset);
+    return 0;
+  });
+}
+
+int cbis_cache_page_table(cbis_cache* c, int seq_id, int* out, int capacity) {
+  return guard([&] {
+    const std::vector<int> t = c->impl->page_table(seq_id);
+    const int n = std::min<int>((int)t.size(), capacity);
+    std::memcpy(out, t.data(), (size_t)n * 4);
+    return n;
+  });
+}
+
+int cbis_cache_seq_pages(cbis_cache* c, int seq_id, int* out, int capacity) {
+  return guard([&] {
+    const auto& p = c->impl->pages(seq_id);
+    const int n = std::min<int>((int)p.size(), capacity);
+    if (n > 0) std::memcpy(out, p.data(), (size_t)n * 4);
+    return (int)p.size();
+  });
+}
+
+int cbis_cache_num_free_pages(cbis_cache* c) { return c->impl->num_free_pages(); }
+int cbis_cache_max_pages(cbis_cache* c) { return c->impl->max_pages(); }
+int cbis_cache_page_size(cbis_cache* c) { return c->impl->page_size(); }
+
+void* cbis_cache_k_base(cbis_cache* c, int layer) {
+  return guard_ptr<void>([&] { return c->impl->k_base(layer); });
+}
+
+void* cbis_cache_v_base(cbis_cache* c, int layer) {
+  return guard_ptr<void>([&] { return c->impl->v_base(layer); });
+}
+
+int cbis_cache_fill_normal(cbis_cache* c, uint64_t seed, float std) {
+  return guard([&] {
+    c->impl->fill_normal(seed, std, nullptr);
+    return 0;
+  });
+}
+
+cbis_weights* cbis_weights_synthetic(const cbis_model_config* cfg, uint64_t seed, float std) {
+  return guard_ptr<cbis_weights>([&] {
+    auto* w = new cbis_weights();
+    try {
+      w->impl = ModelWeights::synthetic(to_cfg(cfg), seed, std);
+    } catch (...) {
+      delete w;
+      throw;
+    }
+    return w;
+  });
+}
+
+cbis_weights* cbis_weights_load(const char* path, const cbis_model_config* cfg) {
+  return guard_ptr<cbis_weights>([&] {
+    auto* w = new cbis_weights();
+    try {
+      w->impl = ModelWeights::load(path ? path : "", to_cfg(cfg));
+    } catch (...) {
+      delete w;
+      throw;
+    }
+    return w;
+  });
+}
+
+void cbis_weights_destroy(cbis_weights* w) { delete w; }
+
+size_t cbis_weights_device_bytes(const cbis_weights* w) { return w->impl->device_bytes(); }
+
+void* cbis_weights_tensor(const cbis_weights* w, const char* name) {
+  return guard_ptr<void>([&] { return w->impl->tensor(name ? name : ""); });
+}
+
+cbis_runner* cbis_runner_create(const cbis_weights* w, cbis_cache* c, int max_total_rows) {
+  return guard_ptr<cbis_runner>([&] {
+    auto* r = new cbis_runner();
+    try {
+      r->impl.reset(new TransformerRunner(*w->impl, *c->impl, max_total_rows));
+    } catch (...) {
+      delete r;
+      throw;
+    }
+    return r;
+  });
+}
+
+void cbis_runner_destroy(cbis_runner* r) { delete r; }
+
+int cbis_runner_forward_step(cbis_runner* r, int n, const int* token_ids, const int* positions, const int* seq_ids,
+                             float* logits_out) {
+  return guard([&] {
+    if (n < 0) throw std::invalid_argument("forward_step: n < 0");
+    std::vector<int> t(token_ids, token_ids + n), p(positions, positions + n), s(seq_ids, seq_ids + n);
+    const std::vector<float> lg = r->impl->forward_step(t, p, s);
+    if (!lg.empty()) std::memcpy(logits_out, lg.data(), lg.size() * 4);
+    return 0;
+  });
+}
+
+int cbis_runner_forward_step_greedy(cbis_runner* r, int n, const int* token_ids, const int* positions,
+                                    const int* seq_ids, int* next_tokens) {
+  return guard([&] {
+    if (n < 0) throw std::invalid_argument("forward_step_greedy: n < 0");
+    std::vector<int> t(token_ids, token_ids + n), p(positions, positions + n), s(seq_ids, seq_ids + n);
+    const std::vector<int> nx = r->impl->forward_step_greedy(t, p, s);
+    if (!nx.empty()) std::memcpy(next_tokens, nx.data(), nx.size() * 4);
+    return 0;
+  });
+}
+
+const float* cbis_runner_logits_device(cbis_runner* r) { return r->impl->logits_device(); }
+
+void* cbis_runner_stream(cbis_runner* r) { return (void*)r->impl->stream(); }
+
+void cbis_runner_set_graphs(cbis_runner* r, int enable) { r->impl->set_graphs(enable != 0); }
+
+int cbis_run_continuous(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
+                        const int* prompt_tokens, const int* decode_lens, int max_slots, int* out_tokens,
+                        double* step_ms, int max_steps) {
+  return guard([&] {
+    std::vector<Request> reqs(n_requests);
+    size_t off = 0;
+    for (int i = 0; i < n_requests; ++i) {
+      reqs[i].prompt.assign(prompt_tokens + off, prompt_tokens + off + prompt_lens[i]);
+      off += prompt_lens[i];
+      reqs[i].decode_len = decode_lens[i];
+    }
+    const ContinuousResult res = run_continuous(*r->impl, *c->impl, reqs, max_slots);
+    size_t o = 0;
+    for (int i = 0; i < n_requests; ++i) {
+      for (int j = 0; j < decode_lens[i]; ++j) out_tokens[o++] = j < (int)res.tokens[i].size() ? res.tokens[i][j] : -1;
+    }
+    if (step_ms)
+      for (int i = 0; i < (int)res.step_ms.size() && i < max_steps; ++i) step_ms[i] = res.step_ms[i];
+    return (int)res.step_ms.size();
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,216 @@
+// Host runtime of the per-step forward, keeping the reference's C++ API:
+//   ModelConfig        runtime twin of cfg:: (include/config.hpp:4-25)
+//   PagedKVCache       include/paged_kv_cache.hpp:17-51
+//   ModelWeights       include/model_weights.hpp:7-25
+//   TransformerRunner  include/transformer.hpp:15-34
+//   run_continuous     src/bench_batching.cpp:98-179
+// Device work goes only through the kernels' C-ABI (cbis_kernels.h).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "cbis_kernels.h"
+
+namespace cbis {
+
+struct ModelConfig {
+  int vocab = 1000;
+  int d_model = 256;
+  int n_heads = 8;
+  int head_dim = 32;
+  int n_layers = 4;
+  int mlp = 1024;
+  int max_seq = 32768;
+  int page_size = 16;
+  int weight_dtype = CBIS_F32;
+  int kv_dtype = CBIS_F32;
+
+  int pages_per_seq() const { return max_seq / page_size; }
+  // GEMM input activations: fp32 for an fp32 model, bf16 otherwise.
+  int act_dtype() const { return weight_dtype == CBIS_F32 ? CBIS_F32 : CBIS_BF16; }
+  void validate() const;
+};
+
+size_t dtype_size(int dtype);
+void hip_check(hipError_t e, const char* what);
+void cbis_check(int rc, const char* what);
+
+// ---------------------------------------------------------------------------
+// Paged KV cache.  The bookkeeping reproduces src/paged_kv_cache.cpp:5-60
+// exactly (free list [P-1 .. 0] so pop_back hands out 0, 1, 2, ...; pages of
+// a freed sequence are pushed back in logical order; sequence ids are a
+// monotonic counter).  Device pools: one allocation holding, per layer, a K
+// pool then a V pool, each [max_pages][page_size][n_heads][head_dim].
+// ---------------------------------------------------------------------------
+class PagedKVCache {
+ public:
+  PagedKVCache(int num_layers, int max_pages, int page_size, int n_heads, int head_dim, int kv_dtype = CBIS_F32,
+               int pages_per_seq = 2048, bool alloc_device = true);
+  ~PagedKVCache();
+  PagedKVCache(const PagedKVCache&) = delete;
+  PagedKVCache& operator=(const PagedKVCache&) = delete;
+
+  int allocate_sequence();
+  void free_sequence(int seq_id);
+  bool ensure_capacity(int seq_id, int token_pos);
+  void resolve_slot(int seq_id, int token_pos, int* physical_page, int* offset) const;
+  std::vector<int> page_table(int seq_id) const;
+  const std::vector<int>& pages(int seq_id) const;  // throws std::out_of_range
+
+  void* k_base(int layer) const;
+  void* v_base(int layer) const;
+  int num_free_pages() const { return (int)free_pages_.size(); }
+  int max_pages() const { return max_pages_; }
+  int page_size() const { return page_size_; }
+  int n_heads() const { return n_heads_; }
+  int head_dim() const { return head_dim_; }
+  int num_layers() const { return num_layers_; }
+  int kv_dtype() const { return kv_dtype_; }
+  int pages_per_seq() const { return pages_per_seq_; }
+  size_t pool_bytes() const { return layer_bytes_; }
+  bool has_device() const { return base_ != nullptr; }
+  void fill_normal(uint64_t seed, float std, hipStream_t s);
+
+ private:
+  int num_layers_, max_pages_, page_size_, n_heads_, head_dim_, kv_dtype_, pages_per_seq_;
+  size_t layer_bytes_ = 0;
+  uint8_t* base_ = nullptr;
+  std::vector<int> free_pages_;
+  std::unordered_map<int, std::vector<int>> seq_pages_;
+  int next_seq_id_ = 0;
+};
+
+// ---------------------------------------------------------------------------
+// Weights.  Linear weights in the config's dtype (fp32 / bf16 / fp8 e4m3 with
+// a per-output-channel fp32 scale), Q/K/V fused to one [3d, d] matrix;
+// embeddings fp32 (fp32 model) or bf16; biases and LayerNorm fp32.  All
+// tensors live in one device arena.
+// ---------------------------------------------------------------------------
+struct LayerWeights {
+  float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
+  void* wqkv = nullptr;
+  float *bqkv = nullptr, *sqkv = nullptr;
+  void* wo = nullptr;
+  float *bo = nullptr, *so = nullptr;
+  void* w1 = nullptr;
+  float *b1 = nullptr, *s1 = nullptr;
+  void* w2 = nullptr;
+  float *b2 = nullptr, *s2 = nullptr;
+};
+
+class ModelWeights {
+ public:
+  ModelConfig cfg;
+  void* tok_emb = nullptr;
+  void* pos_emb = nullptr;
+  std::vector<LayerWeights> layers;
+  float *ln_f_w = nullptr, *ln_f_b = nullptr;
+  void* lm_head = nullptr;
+  float* lm_scale = nullptr;
+
+  static std::unique_ptr<ModelWeights> synthetic(const ModelConfig& cfg, uint64_t seed, float std = 0.02f);
+  static std::unique_ptr<ModelWeights> load(const std::string& path, const ModelConfig& cfg);
+  ~ModelWeights();
+  void free_all();
+  size_t device_bytes() const { return arena_bytes_; }
+  int emb_dtype() const { return cfg.weight_dtype == CBIS_F32 ? CBIS_F32 : CBIS_BF16; }
+  void* tensor(const std::string& name) const;
+
+ private:
+  ModelWeights() = default;
+  void plan();
+  uint8_t* arena_ = nullptr;
+  size_t arena_bytes_ = 0;
+  std::map<std::string, void*> named_;
+};
+
+// ---------------------------------------------------------------------------
+// One flattened continuous-batch step (src/transformer.cpp:44-99).
+// ---------------------------------------------------------------------------
+class TransformerRunner {
+ public:
+  TransformerRunner(const ModelWeights& weights, PagedKVCache& cache, int max_total_rows);
+  ~TransformerRunner();
+  TransformerRunner(const TransformerRunner&) = delete;
+  TransformerRunner& operator=(const TransformerRunner&) = delete;
+
+  // Returns row-major [rows, vocab] logits (the reference's contract).
+  std::vector<float> forward_step(const std::vector<int>& token_ids, const std::vector<int>& positions,
+                                  const std::vector<int>& seq_ids);
+  // Same step; returns the greedy next token of every row (device argmax).
+  std::vector<int> forward_step_greedy(const std::vector<int>& token_ids, const std::vector<int>& positions,
+                                       const std::vector<int>& seq_ids);
+  const float* logits_device() const { return d_logits_; }
+  hipStream_t stream() const { return stream_; }
+  void set_graphs(bool on) { use_graphs_ = on; }
+
+ private:
+  struct StepPlan;
+  void prepare(const int* tok, const int* pos, const int* seq, int M);
+  void enqueue_forward();
+  void run_step(bool greedy);
+
+  const ModelWeights& w_;
+  PagedKVCache& cache_;
+  ModelConfig cfg_;
+  int max_rows_;
+  hipStream_t stream_ = nullptr;
+  bool use_graphs_ = true;
+
+  // metadata staging (pinned host, one H2D per step)
+  uint8_t* h_meta_ = nullptr;
+  uint8_t* d_meta_ = nullptr;
+  size_t meta_cap_ = 0;
+
+  // activations
+  float* d_x_ = nullptr;
+  void* d_xn_ = nullptr;
+  float* d_q_ = nullptr;
+  void* d_attn_ = nullptr;
+  void* d_h_ = nullptr;
+  float* d_logits_ = nullptr;
+  int* d_next_ = nullptr;
+  void* d_ws_ = nullptr;
+  size_t ws_bytes_ = 0;
+
+  // current step
+  int M_ = 0;
+  int n_decode_ = 0, n_tiles_ = 0, n_seqs_ = 0, bt_width_ = 0, max_kv_ = 0;
+  size_t meta_bytes_ = 0;
+  int *d_tok_ = nullptr, *d_pos_ = nullptr, *d_wpage_ = nullptr, *d_woff_ = nullptr, *d_rowbt_ = nullptr,
+      *d_drows_ = nullptr, *d_tiles_ = nullptr, *d_bt_ = nullptr;
+
+  // graph cache: one executable graph per step shape signature
+  struct GraphEntry {
+    hipGraphExec_t exec = nullptr;
+  };
+  std::map<std::vector<int>, GraphEntry> graphs_;
+  std::vector<int> signature() const;
+};
+
+// ---------------------------------------------------------------------------
+// Continuous batching (src/bench_batching.cpp:98-179), all requests present
+// at t = 0.
+// ---------------------------------------------------------------------------
+struct Request {
+  std::vector<int> prompt;
+  int decode_len = 0;
+};
+
+struct ContinuousResult {
+  std::vector<std::vector<int>> tokens;  // generated tokens per request
+  std::vector<double> step_ms;           // wall time of each forward step
+};
+
+ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, const std::vector<Request>& reqs,
+                                int max_slots);
+
+}  // namespace cbis

@@ -1,0 +1,302 @@
+// TransformerRunner::forward_step -- one flattened continuous-batch step,
+// src/transformer.cpp:44-99, on the gfx950 kernels of cbis_kernels.h.
+//
+// Differences from the reference's step that keep its contract:
+//  * per-step metadata (token ids, positions, write slots, a compact block
+//    table per distinct sequence instead of a kPagesPerSeq-wide copy per row,
+//    decode-row list, prefill tiles) is packed into one pinned buffer and
+//    sent with a single H2D copy;
+//  * per layer: LayerNorm -> one fused QKV GEMM whose epilogue adds the bias
+//    and scatters K/V into their page slots (scatter-before-attention order
+//    of src/transformer.cpp:75-80 kept) -> split-KV decode attention for
+//    single rows and MFMA prefill attention for runs of consecutive rows of
+//    one sequence -> out-projection GEMM with bias + residual epilogue ->
+//    LayerNorm -> fc1 GEMM with bias + GELU -> fc2 GEMM with bias + residual;
+//  * steps whose shape repeats replay a captured HIP graph;
+//  * forward_step_greedy takes the argmax on the device.
+#include <algorithm>
+#include <cstring>
+#include <unordered_map>
+
+#include "runtime.hpp"
+
+namespace cbis {
+
+namespace {
+constexpr int kMinPrefillRun = 8;   // runs shorter than this use the decode kernel
+constexpr int kTileRows = 32;       // query rows per prefill tile
+constexpr size_t kMaxGraphs = 64;
+size_t align_ints(size_t n) { return (n + 3) & ~(size_t)3; }
+}  // namespace
+
+TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& cache, int max_total_rows)
+    : w_(weights), cache_(cache), cfg_(weights.cfg), max_rows_(max_total_rows) {
+  cfg_.validate();
+  if (max_total_rows <= 0) throw std::invalid_argument("TransformerRunner: max_total_rows must be > 0");
+  if (cache.num_layers() != cfg_.n_layers || cache.n_heads() != cfg_.n_heads || cache.head_dim() != cfg_.head_dim ||
+      cache.page_size() != cfg_.page_size || cache.kv_dtype() != cfg_.kv_dtype)
+    throw std::invalid_argument("TransformerRunner: cache geometry does not match the model config");
+  if (!cache.has_device()) throw std::invalid_argument("TransformerRunner: cache has no device pools");
+  hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  const size_t R = max_total_rows, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
+  const size_t ae = dtype_size(cfg_.act_dtype());
+  hip_check(hipMalloc((void**)&d_x_, R * D * 4), "hipMalloc x");
+  hip_check(hipMalloc(&d_xn_, R * D * ae), "hipMalloc xn");
+  hip_check(hipMalloc((void**)&d_q_, R * D * 4), "hipMalloc q");
+  hip_check(hipMalloc(&d_attn_, R * D * ae), "hipMalloc attn");
+  hip_check(hipMalloc(&d_h_, R * F * ae), "hipMalloc h");
+  hip_check(hipMalloc((void**)&d_logits_, R * V * 4), "hipMalloc logits");
+  hip_check(hipMalloc((void**)&d_next_, R * 4), "hipMalloc next");
+  // Split-KV partials: the automatic split keeps rows * splits <= 2048 + rows.
+  ws_bytes_ = (2048 + R) * (size_t)cfg_.n_heads * (cfg_.head_dim + 4) * 4;
+  hip_check(hipMalloc(&d_ws_, ws_bytes_), "hipMalloc attention workspace");
+}
+
+TransformerRunner::~TransformerRunner() {
+  for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
+  if (stream_) (void)hipStreamDestroy(stream_);
+  (void)hipFree(d_x_); (void)hipFree(d_xn_); (void)hipFree(d_q_); (void)hipFree(d_attn_);
+  (void)hipFree(d_h_); (void)hipFree(d_logits_); (void)hipFree(d_next_); (void)hipFree(d_ws_);
+  (void)hipFree(d_meta_);
+  if (h_meta_) (void)hipHostFree(h_meta_);
+}
+
+void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, int M) {
+  if (M > max_rows_) throw std::runtime_error("forward_step: total_rows exceeds max_total_rows");
+  for (int i = 0; i < M; ++i) {
+    if (tok[i] < 0 || tok[i] >= cfg_.vocab) throw std::out_of_range("forward_step: token id out of range");
+    if (pos[i] < 0 || pos[i] >= cfg_.max_seq) throw std::out_of_range("forward_step: position out of range");
+  }
+  std::vector<int> wpage(M), woff(M), rowbt(M);
+  std::unordered_map<int, int> index;
+  std::vector<int> seqs;
+  int width = 1;
+  for (int i = 0; i < M; ++i) {
+    cache_.resolve_slot(seq[i], pos[i], &wpage[i], &woff[i]);  // throws like the reference
+    auto it = index.find(seq[i]);
+    if (it == index.end()) {
+      it = index.emplace(seq[i], (int)seqs.size()).first;
+      seqs.push_back(seq[i]);
+      width = std::max(width, (int)cache_.pages(seq[i]).size());
+    }
+    rowbt[i] = it->second;
+  }
+  // Rows: runs of consecutive positions of one sequence go to the MFMA
+  // prefill kernel (bf16 K/V), everything else to the split-KV decode kernel.
+  const bool prefill_ok = cfg_.kv_dtype == CBIS_BF16 && cfg_.n_heads % 4 == 0;
+  std::vector<int> drows, tiles;
+  int max_kv = 1;
+  for (int i = 0; i < M;) {
+    int j = i + 1;
+    while (j < M && seq[j] == seq[i] && pos[j] == pos[j - 1] + 1) ++j;
+    if (prefill_ok && j - i >= kMinPrefillRun) {
+      for (int r = i; r < j; r += kTileRows) {
+        const int nv = std::min(kTileRows, j - r);
+        tiles.insert(tiles.end(), {r, nv, rowbt[r], pos[r]});
+      }
+    } else {
+      for (int r = i; r < j; ++r) {
+        drows.push_back(r);
+        max_kv = std::max(max_kv, pos[r] + 1);
+      }
+    }
+    i = j;
+  }
+  M_ = M;
+  n_decode_ = (int)drows.size();
+  n_tiles_ = (int)tiles.size() / 4;
+  n_seqs_ = (int)seqs.size();
+  bt_width_ = width;
+  max_kv_ = (max_kv + 255) / 256 * 256;  // coarse, so steps share split shapes (and graphs)
+
+  const size_t o_tok = 0, o_pos = o_tok + align_ints(M), o_wp = o_pos + align_ints(M), o_wo = o_wp + align_ints(M),
+               o_rb = o_wo + align_ints(M), o_dr = o_rb + align_ints(M), o_ti = o_dr + align_ints(drows.size()),
+               o_bt = o_ti + align_ints(tiles.size()), n_ints = o_bt + align_ints((size_t)n_seqs_ * width);
+  const size_t bytes = n_ints * 4;
+  if (bytes > meta_cap_) {
+    for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
+    graphs_.clear();
+    if (d_meta_) hip_check(hipFree(d_meta_), "hipFree meta");
+    if (h_meta_) hip_check(hipHostFree(h_meta_), "hipHostFree meta");
+    meta_cap_ = std::max(bytes, (size_t)1 << 20) * 2;
+    hip_check(hipMalloc((void**)&d_meta_, meta_cap_), "hipMalloc meta");
+    hip_check(hipHostMalloc((void**)&h_meta_, meta_cap_, 0), "hipHostMalloc meta");
+  }
+  int* h = (int*)h_meta_;
+  std::memcpy(h + o_tok, tok, M * 4);
+  std::memcpy(h + o_pos, pos, M * 4);
+  std::memcpy(h + o_wp, wpage.data(), M * 4);
+  std::memcpy(h + o_wo, woff.data(), M * 4);
+  std::memcpy(h + o_rb, rowbt.data(), M * 4);
+  if (!drows.empty()) std::memcpy(h + o_dr, drows.data(), drows.size() * 4);
+  if (!tiles.empty()) std::memcpy(h + o_ti, tiles.data(), tiles.size() * 4);
+  int* bt = h + o_bt;
+  std::memset(bt, 0, (size_t)n_seqs_ * width * 4);
+  for (int s = 0; s < n_seqs_; ++s) {
+    const auto& pg = cache_.pages(seqs[s]);
+    std::copy(pg.begin(), pg.end(), bt + (size_t)s * width);
+  }
+  int* d = (int*)d_meta_;
+  d_tok_ = d + o_tok; d_pos_ = d + o_pos; d_wpage_ = d + o_wp; d_woff_ = d + o_wo; d_rowbt_ = d + o_rb;
+  d_drows_ = d + o_dr; d_tiles_ = d + o_ti; d_bt_ = d + o_bt;
+  meta_bytes_ = bytes;
+  hip_check(hipMemcpyAsync(d_meta_, h_meta_, bytes, hipMemcpyHostToDevice, stream_), "H2D step metadata");
+}
+
+std::vector<int> TransformerRunner::signature() const {
+  return {M_, n_decode_, n_tiles_, n_seqs_, bt_width_, max_kv_};
+}
+
+void TransformerRunner::enqueue_forward() {
+  const int M = M_, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
+  const int act = cfg_.act_dtype(), wd = cfg_.weight_dtype;
+  hipStream_t s = stream_;
+  cbis_check(cbis_embed(M, D, d_tok_, d_pos_, w_.emb_dtype(), w_.tok_emb, w_.pos_emb, V, cfg_.max_seq, d_x_, s),
+             "embed");
+
+  cbis_gemm_desc g = {};
+  g.M = M;
+  g.x_dtype = act;
+  g.w_dtype = wd;
+
+  cbis_attn_desc a = {};
+  a.n_heads = cfg_.n_heads;
+  a.head_dim = cfg_.head_dim;
+  a.page_size = cfg_.page_size;
+  a.q_dtype = CBIS_F32;
+  a.q = d_q_;
+  a.ldq = D;
+  a.kv_dtype = cfg_.kv_dtype;
+  a.num_pages = cache_.max_pages();
+  a.block_table = d_bt_;
+  a.bt_stride = bt_width_;
+  a.row_bt = d_rowbt_;
+  a.row_pos = d_pos_;
+  a.out_dtype = act;
+  a.out = d_attn_;
+  a.ldo = D;
+  a.max_kv_len = max_kv_;
+  a.workspace = d_ws_;
+  a.workspace_bytes = ws_bytes_;
+
+  for (int l = 0; l < cfg_.n_layers; ++l) {
+    const LayerWeights& L = w_.layers[l];
+    cbis_check(cbis_layernorm(M, D, d_x_, D, L.ln1_w, L.ln1_b, 1e-5f, act, d_xn_, D, s), "ln1");
+    // QKV projection; K and V columns go straight to their page slots.
+    g = cbis_gemm_desc{};
+    g.M = M; g.N = 3 * D; g.K = D;
+    g.x_dtype = act; g.X = d_xn_; g.ldx = D;
+    g.w_dtype = wd; g.W = L.wqkv; g.ldw = D; g.w_scale = L.sqkv;
+    g.bias = L.bqkv;
+    g.y_dtype = CBIS_F32; g.Y = d_q_; g.ldy = D;
+    g.kv_col0 = D; g.kv_width = D; g.kv_dtype = cfg_.kv_dtype; g.page_size = cfg_.page_size;
+    g.k_pool = cache_.k_base(l); g.v_pool = cache_.v_base(l);
+    g.write_page = d_wpage_; g.write_offset = d_woff_;
+    cbis_check(cbis_gemm(&g, s), "qkv gemm");
+    a.k_pool = cache_.k_base(l);
+    a.v_pool = cache_.v_base(l);
+    if (n_decode_ > 0) {
+      a.n_rows = n_decode_;
+      a.rows = d_drows_;
+      cbis_check(cbis_paged_attention(&a, s), "decode attention");
+    }
+    if (n_tiles_ > 0) cbis_check(cbis_paged_prefill_attention(&a, n_tiles_, d_tiles_, s), "prefill attention");
+    // out-projection + bias + residual, in place on x
+    g = cbis_gemm_desc{};
+    g.M = M; g.N = D; g.K = D;
+    g.x_dtype = act; g.X = d_attn_; g.ldx = D;
+    g.w_dtype = wd; g.W = L.wo; g.ldw = D; g.w_scale = L.so;
+    g.bias = L.bo; g.residual = d_x_; g.ldr = D;
+    g.y_dtype = CBIS_F32; g.Y = d_x_; g.ldy = D;
+    cbis_check(cbis_gemm(&g, s), "out-proj gemm");
+    cbis_check(cbis_layernorm(M, D, d_x_, D, L.ln2_w, L.ln2_b, 1e-5f, act, d_xn_, D, s), "ln2");
+    g = cbis_gemm_desc{};
+    g.M = M; g.N = F; g.K = D;
+    g.x_dtype = act; g.X = d_xn_; g.ldx = D;
+    g.w_dtype = wd; g.W = L.w1; g.ldw = D; g.w_scale = L.s1;
+    g.bias = L.b1; g.epilogue = CBIS_EPI_GELU;
+    g.y_dtype = act; g.Y = d_h_; g.ldy = F;
+    cbis_check(cbis_gemm(&g, s), "fc1 gemm");
+    g = cbis_gemm_desc{};
+    g.M = M; g.N = D; g.K = F;
+    g.x_dtype = act; g.X = d_h_; g.ldx = F;
+    g.w_dtype = wd; g.W = L.w2; g.ldw = F; g.w_scale = L.s2;
+    g.bias = L.b2; g.residual = d_x_; g.ldr = D;
+    g.y_dtype = CBIS_F32; g.Y = d_x_; g.ldy = D;
+    cbis_check(cbis_gemm(&g, s), "fc2 gemm");
+  }
+  cbis_check(cbis_layernorm(M, D, d_x_, D, w_.ln_f_w, w_.ln_f_b, 1e-5f, act, d_xn_, D, s), "ln_f");
+  g = cbis_gemm_desc{};
+  g.M = M; g.N = V; g.K = D;
+  g.x_dtype = act; g.X = d_xn_; g.ldx = D;
+  g.w_dtype = wd; g.W = w_.lm_head; g.ldw = D; g.w_scale = w_.lm_scale;
+  g.y_dtype = CBIS_F32; g.Y = d_logits_; g.ldy = V;
+  cbis_check(cbis_gemm(&g, s), "lm_head gemm");
+}
+
+void TransformerRunner::run_step(bool greedy) {
+  auto body = [&]() {
+    enqueue_forward();
+    if (greedy) cbis_check(cbis_argmax_rows(M_, cfg_.vocab, d_logits_, cfg_.vocab, d_next_, stream_), "argmax");
+  };
+  if (!use_graphs_) {
+    body();
+    return;
+  }
+  std::vector<int> sig = signature();
+  sig.push_back(greedy ? 1 : 0);
+  auto it = graphs_.find(sig);
+  if (it == graphs_.end()) {
+    if (graphs_.size() >= kMaxGraphs) {
+      for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
+      graphs_.clear();
+    }
+    hipGraph_t graph = nullptr;
+    hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    try {
+      body();
+    } catch (...) {
+      (void)hipStreamEndCapture(stream_, &graph);
+      if (graph) (void)hipGraphDestroy(graph);
+      throw;
+    }
+    hip_check(hipStreamEndCapture(stream_, &graph), "hipStreamEndCapture");
+    GraphEntry e;
+    hipError_t rc = hipGraphInstantiate(&e.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    hip_check(rc, "hipGraphInstantiate");
+    it = graphs_.emplace(sig, e).first;
+  }
+  hip_check(hipGraphLaunch(it->second.exec, stream_), "hipGraphLaunch");
+}
+
+std::vector<float> TransformerRunner::forward_step(const std::vector<int>& token_ids, const std::vector<int>& positions,
+                                                   const std::vector<int>& seq_ids) {
+  const int M = (int)token_ids.size();
+  if (M == 0) return {};
+  if ((int)positions.size() != M || (int)seq_ids.size() != M)
+    throw std::invalid_argument("forward_step: token_ids/positions/seq_ids sizes differ");
+  prepare(token_ids.data(), positions.data(), seq_ids.data(), M);
+  run_step(false);
+  std::vector<float> logits((size_t)M * cfg_.vocab);
+  hip_check(hipMemcpyAsync(logits.data(), d_logits_, logits.size() * 4, hipMemcpyDeviceToHost, stream_), "D2H logits");
+  hip_check(hipStreamSynchronize(stream_), "forward_step sync");
+  return logits;
+}
+
+std::vector<int> TransformerRunner::forward_step_greedy(const std::vector<int>& token_ids,
+                                                        const std::vector<int>& positions,
+                                                        const std::vector<int>& seq_ids) {
+  const int M = (int)token_ids.size();
+  if (M == 0) return {};
+  if ((int)positions.size() != M || (int)seq_ids.size() != M)
+    throw std::invalid_argument("forward_step_greedy: token_ids/positions/seq_ids sizes differ");
+  prepare(token_ids.data(), positions.data(), seq_ids.data(), M);
+  run_step(true);
+  std::vector<int> next(M);
+  hip_check(hipMemcpyAsync(next.data(), d_next_, (size_t)M * 4, hipMemcpyDeviceToHost, stream_), "D2H tokens");
+  hip_check(hipStreamSynchronize(stream_), "forward_step_greedy sync");
+  return next;
+}
+
+}  // namespace cbis

@@ -1,0 +1,218 @@
+/*
+ * cbis_kernels.h -- C-ABI of the MI355X (gfx950) kernels behind the per-step
+ * transformer forward.
+ *
+ * This is the drop-in boundary.  In the reference the kernels sit behind
+ * seven C++ launchers taking raw device pointers, int dims and a stream:
+ *   include/linear.hpp:9-11       linear_forward          (cuBLAS SGEMM + bias)
+ *   include/elementwise.hpp:6-8   embed_lookup_add
+ *   include/elementwise.hpp:12-13 layernorm_forward
+ *   include/elementwise.hpp:15-18 gelu_forward
+ *   include/elementwise.hpp:20-21 residual_add
+ *   include/attention.hpp:8-12    scatter_kv_to_cache
+ *   include/attention.hpp:29-33   fused_paged_causal_attention
+ * Each has an extern "C" twin below with the same argument meaning (minus
+ * the cuBLAS handle).  Beside them are the descriptor entry points the
+ * runtime uses: the MFMA GEMM with fused epilogues (bias, GELU, residual,
+ * K/V page scatter; fp32, bf16 and fp8-e4m3 weights), split-KV paged decode
+ * attention with a caller-provided workspace, MFMA prefill attention over
+ * paged K/V, LayerNorm with a bf16 output, device argmax and synthetic fills.
+ *
+ * Conventions: every pointer argument is a device pointer unless stated;
+ * layouts are row-major; weights use nn.Linear's [out, in] layout
+ * (docs/gemm_layout.md:16-41); K/V pools are [pages][page_size][heads][head_dim].
+ * Entry points are stream-ordered, allocate nothing, and return 0 on success
+ * or a non-zero cbis_status; cbis_last_error() then holds a message (per
+ * thread).  They never exit() (the reference's CUDA_CHECK does,
+ * include/cuda_check.hpp:7-15).
+ */
+#ifndef CBIS_KERNELS_H
+#define CBIS_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* cbis_stream_t; /* a hipStream_t; NULL is the default stream */
+
+enum cbis_dtype { CBIS_F32 = 0, CBIS_BF16 = 1, CBIS_FP8E4M3 = 2 };
+
+enum cbis_status {
+  CBIS_OK = 0,
+  CBIS_ERR_INVALID = 1,     /* bad argument (null pointer, size, alignment) */
+  CBIS_ERR_UNSUPPORTED = 2, /* shape/dtype combination this build has no kernel for */
+  CBIS_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  CBIS_ERR_HIP = 4          /* the HIP runtime reported an error */
+};
+
+/* Message for the last non-zero status returned on this thread. */
+const char* cbis_last_error(void);
+
+/* ----------------------------------------------------------------------- */
+/* Reference-signature entry points (fp32 throughout).                      */
+/* ----------------------------------------------------------------------- */
+
+/* Y[T,out] = X[T,in] . W[out,in]^T + b (b may be NULL).
+ * Replaces linear_forward, include/linear.hpp:9-11 / kernels/linear.cu:15-34. */
+int cbis_linear_forward(const float* X, const float* W, const float* b, float* Y, int T,
+                        int in_features, int out_features, cbis_stream_t stream);
+
+/* out[r] = tok_emb[token_ids[r]] + pos_emb[positions[r]].
+ * Replaces embed_lookup_add, include/elementwise.hpp:6-8. */
+int cbis_embed_lookup_add(const int* token_ids, const int* positions, const float* tok_emb,
+                          const float* pos_emb, float* out, int T, int d_model, cbis_stream_t stream);
+
+/* Y = LayerNorm(X) * gamma + beta, eps 1e-5.
+ * Replaces layernorm_forward, include/elementwise.hpp:12-13. */
+int cbis_layernorm_forward(const float* X, const float* gamma, const float* beta, float* Y, int T,
+                           int d_model, cbis_stream_t stream);
+
+/* In-place exact-erf GELU.  Replaces gelu_forward, include/elementwise.hpp:15-18. */
+int cbis_gelu_forward(float* X, int T, int width, cbis_stream_t stream);
+
+/* X += Y.  Replaces residual_add, include/elementwise.hpp:20-21. */
+int cbis_residual_add(float* X, const float* Y, int T, int width, cbis_stream_t stream);
+
+/* Copies row r of K/V into slot (write_page[r], write_offset[r]) of the pools.
+ * Replaces scatter_kv_to_cache, include/attention.hpp:8-12. */
+int cbis_scatter_kv_to_cache(const float* K_proj, const float* V_proj, float* k_pages, float* v_pages,
+                             const int* write_page, const int* write_offset, int total_rows, int d_model,
+                             int page_size, int n_heads, int head_dim, cbis_stream_t stream);
+
+/* Causal paged attention with the reference's per-row page table
+ * row_page_table[total_rows, pages_per_seq]; kv_len = row_query_pos[r] + 1.
+ * Replaces fused_paged_causal_attention, include/attention.hpp:29-33
+ * (kernels/attention.cu:57-127).  Runs the wave64 decode kernel in a single
+ * pass per (row, head block): it needs no workspace.  Supported: head_dim 32,
+ * page_size 16, n_heads a multiple of 8. */
+int cbis_fused_paged_causal_attention(const float* Q_proj, const float* k_pages, const float* v_pages,
+                                      const int* row_page_table, const int* row_query_pos, float* attn_out,
+                                      int total_rows, int n_heads, int head_dim, int page_size,
+                                      int pages_per_seq, cbis_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* GEMM: Y = epilogue(X . W^T) on MFMA.                                     */
+/* ----------------------------------------------------------------------- */
+
+enum cbis_epilogue { CBIS_EPI_NONE = 0, CBIS_EPI_GELU = 1 };
+
+typedef struct cbis_gemm_desc {
+  int M, N, K;
+  int x_dtype;           /* CBIS_F32 or CBIS_BF16 */
+  const void* X;         /* [M, K], row stride ldx elements */
+  int64_t ldx;
+  int w_dtype;           /* CBIS_F32 (needs x F32), CBIS_BF16 or CBIS_FP8E4M3 (need x BF16) */
+  const void* W;         /* [N, K], row stride ldw elements */
+  int64_t ldw;
+  const float* w_scale;  /* [N] per-output-channel scale (fp8 only), else NULL */
+  const float* bias;     /* [N] or NULL */
+  int epilogue;          /* cbis_epilogue, applied after scale and bias */
+  const float* residual; /* [M, N] fp32 added last (may alias Y), or NULL */
+  int64_t ldr;
+  int y_dtype;           /* CBIS_F32 or CBIS_BF16 */
+  void* Y;               /* [M, N] (columns >= kv_col0 excluded when scattering) */
+  int64_t ldy;
+  /* Optional K/V page scatter (the fused form of scatter_kv_to_cache):
+   * columns [kv_col0, kv_col0 + kv_width) go to k_pool and the next kv_width
+   * to v_pool at slot (write_page[r], write_offset[r]).  kv_pool NULL = off. */
+  int kv_col0, kv_width, kv_dtype, page_size;
+  void* k_pool;
+  void* v_pool;
+  const int* write_page;
+  const int* write_offset;
+} cbis_gemm_desc;
+
+int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* Paged attention.                                                          */
+/* ----------------------------------------------------------------------- */
+
+typedef struct cbis_attn_desc {
+  int n_rows;              /* rows to process (entries of `rows`, or 0..n_rows-1) */
+  const int* rows;         /* [n_rows] row ids into q/out/row_pos/row_bt, or NULL */
+  int n_heads, head_dim, page_size;
+  int q_dtype;             /* CBIS_F32 or CBIS_BF16 */
+  const void* q;           /* [*, n_heads*head_dim], row stride ldq elements */
+  int64_t ldq;
+  int kv_dtype;            /* CBIS_F32 or CBIS_BF16 */
+  const void* k_pool;      /* [num_pages, page_size, n_heads, head_dim] */
+  const void* v_pool;
+  int num_pages;           /* pool size; page ids are clamped to it */
+  const int* block_table;  /* [*, bt_stride] physical page ids */
+  int64_t bt_stride;
+  const int* row_bt;       /* row -> block_table row, or NULL (row r uses row r) */
+  const int* row_pos;      /* row -> query position; kv_len = pos + 1 */
+  int out_dtype;           /* CBIS_F32 or CBIS_BF16 */
+  void* out;               /* [*, n_heads*head_dim], row stride ldo elements */
+  int64_t ldo;
+  int max_kv_len;          /* host upper bound of pos+1 over the rows */
+  int split_tokens;        /* tokens per split-KV chunk (multiple of page_size), 0 = auto */
+  void* workspace;         /* fp32 partials when a row needs more than one split */
+  size_t workspace_bytes;
+} cbis_attn_desc;
+
+/* Bytes of workspace cbis_paged_attention needs for this descriptor (0 when
+ * every row fits one split).  Resolves split_tokens = 0 the same way. */
+size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d);
+
+/* Split-KV decode attention: any set of rows, each with its own kv_len. */
+int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream);
+
+/* Prefill attention on MFMA for query tiles of <= 32 consecutive rows of one
+ * sequence.  tiles is a device array [n_tiles][4] of {first_row, n_valid_rows,
+ * block_table_row, first_position}; row i of a tile has position
+ * first_position + i and attends causally to keys [0, position].
+ * d->rows / row_bt / row_pos / max_kv_len / split_tokens / workspace are
+ * ignored.  Supports bf16 K/V, head_dim 32, page_size 16. */
+int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int* tiles,
+                                 cbis_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* Row ops.                                                                  */
+/* ----------------------------------------------------------------------- */
+
+/* out[r,:] = tok_emb[token_ids[r],:] + pos_emb[positions[r],:] (fp32 out);
+ * embeddings fp32 or bf16; ids are clamped to [0, vocab) and [0, max_pos). */
+int cbis_embed(int T, int d_model, const int* token_ids, const int* positions, int emb_dtype,
+               const void* tok_emb, const void* pos_emb, int vocab, int max_pos, float* out,
+               cbis_stream_t stream);
+
+/* Row LayerNorm of fp32 X into fp32 or bf16 Y. */
+int cbis_layernorm(int T, int d_model, const float* X, int64_t ldx, const float* gamma, const float* beta,
+                   float eps, int y_dtype, void* Y, int64_t ldy, cbis_stream_t stream);
+
+/* out[r] = first index of the maximum of logits[r, 0:N] (strict >), the
+ * greedy rule of src/bench_batching.cpp:66-73. */
+int cbis_argmax_rows(int T, int N, const float* logits, int64_t ld, int* out, cbis_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* Synthetic data.                                                           */
+/* ----------------------------------------------------------------------- */
+
+/* dst[i] = std * z(seed, stream_id, start + i), z the exact Irwin-Hall(12)
+ * variate of the counter-based splitmix64 generator; stored as fp32 or bf16
+ * (round to nearest even).  Bit-reproducible on the host. */
+int cbis_fill_normal_exact(void* dst, int dtype, int64_t n, uint64_t seed, uint64_t stream_id,
+                           uint64_t start, float std, cbis_stream_t stream);
+
+/* Fast N(0, std) fill for large synthetic activations / K/V pools:
+ * Box-Muller over a 32-bit hash of (seed, index), fp32 or bf16. */
+int cbis_fill_normal_fast(void* dst, int dtype, int64_t n, uint64_t seed, float std, cbis_stream_t stream);
+
+/* dst[i] = src[i] stored as fp32 or bf16 (round to nearest even). */
+int cbis_convert_f32(void* dst, int dst_dtype, const float* src, int64_t n, cbis_stream_t stream);
+
+/* Per-output-channel OCP fp8 e4m3 quantisation of an fp32 [N, K] weight:
+ * scale[n] = absmax(src[n,:]) / 448 (fp32; 1 for an all-zero row),
+ * codes[n,k] = RNE_e4m3(src[n,k] / scale[n]). */
+int cbis_quantize_fp8_rows(uint8_t* codes, float* scale, const float* src, int N, int K, cbis_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CBIS_KERNELS_H */

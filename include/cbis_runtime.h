@@ -1,0 +1,109 @@
+/*
+ * cbis_runtime.h -- C-ABI of the C++ host runtime (libcbis.so).
+ *
+ * The runtime keeps the reference's host API in C++
+ * (continuous-batching-inference-server_amd/csrc/runtime/runtime.hpp):
+ *   PagedKVCache        include/paged_kv_cache.hpp:17-51 (src/paged_kv_cache.cpp:5-60)
+ *   ModelWeights        include/model_weights.hpp:7-25  (src/model_weights.cpp:41-75)
+ *   TransformerRunner   include/transformer.hpp:15-34   (src/transformer.cpp:11-99)
+ *   run_continuous      src/bench_batching.cpp:98-179
+ * and reaches the GPU only through include/cbis_kernels.h.  The functions
+ * below wrap those classes for callers that bind C (ctypes, cgo, JNI...).
+ * C++ exceptions never cross this boundary: a failing call returns a
+ * negative status (or NULL) and cbis_runtime_last_error() says why.
+ */
+#ifndef CBIS_RUNTIME_H
+#define CBIS_RUNTIME_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct cbis_model_config {
+  int vocab, d_model, n_heads, head_dim, n_layers, mlp, max_seq, page_size;
+  int weight_dtype; /* CBIS_F32, CBIS_BF16 or CBIS_FP8E4M3 (linear weights) */
+  int kv_dtype;     /* CBIS_F32 or CBIS_BF16 (paged K/V pools) */
+} cbis_model_config;
+
+typedef struct cbis_cache cbis_cache;
+typedef struct cbis_weights cbis_weights;
+typedef struct cbis_runner cbis_runner;
+
+const char* cbis_runtime_last_error(void);
+
+/* The reference model's dimensions (include/config.hpp:4-25), fp32. */
+void cbis_default_config(cbis_model_config* cfg);
+
+/* ---- PagedKVCache (include/paged_kv_cache.hpp:17-51) -------------------- */
+/* alloc_device = 0 keeps only the bookkeeping (no HIP call at all). */
+cbis_cache* cbis_cache_create(int num_layers, int max_pages, int page_size, int n_heads, int head_dim, int kv_dtype,
+                              int pages_per_seq, int alloc_device);
+void cbis_cache_destroy(cbis_cache* c);
+int cbis_cache_allocate_sequence(cbis_cache* c);
+void cbis_cache_free_sequence(cbis_cache* c, int seq_id);
+/* 1: capacity ensured; 0: free list exhausted (reference returns false);
+ * negative: unknown sequence (reference throws std::out_of_range). */
+int cbis_cache_ensure_capacity(cbis_cache* c, int seq_id, int token_pos);
+/* 0 on success; negative when the slot is not allocated (reference throws). */
+int cbis_cache_resolve_slot(cbis_cache* c, int seq_id, int token_pos, int* physical_page, int* offset);
+/* Writes the zero-padded pages_per_seq-entry table; returns entries written or negative. */
+int cbis_cache_page_table(cbis_cache* c, int seq_id, int* out, int capacity);
+/* Physical pages owned by seq_id in logical order; returns the count (may exceed capacity). */
+int cbis_cache_seq_pages(cbis_cache* c, int seq_id, int* out, int capacity);
+int cbis_cache_num_free_pages(cbis_cache* c);
+int cbis_cache_max_pages(cbis_cache* c);
+int cbis_cache_page_size(cbis_cache* c);
+void* cbis_cache_k_base(cbis_cache* c, int layer);
+void* cbis_cache_v_base(cbis_cache* c, int layer);
+/* Fills every page of every pool with N(0, std) (cbis_fill_normal_fast). */
+int cbis_cache_fill_normal(cbis_cache* c, uint64_t seed, float std);
+
+/* ---- ModelWeights (include/model_weights.hpp:7-25) ---------------------- */
+/* Seeded synthetic weights: linear / embedding weights and linear biases
+ * N(0, std) from the exact counter-based generator, LayerNorm gamma 1 /
+ * beta 0; linear weights stored as cfg->weight_dtype. */
+cbis_weights* cbis_weights_synthetic(const cbis_model_config* cfg, uint64_t seed, float std);
+/* python/export_weights.py:42-66 layout (fp32), converted to cfg's dtypes. */
+cbis_weights* cbis_weights_load(const char* path, const cbis_model_config* cfg);
+void cbis_weights_destroy(cbis_weights* w);
+size_t cbis_weights_device_bytes(const cbis_weights* w);
+/* Device pointer of a named tensor ("tok_emb", "pos_emb", "lm_head",
+ * "lm_scale", "ln_f_w", "ln_f_b", or "l<i>.<name>" with name in wqkv, bqkv,
+ * sqkv, wo, bo, so, w1, b1, s1, w2, b2, s2, ln1_w, ln1_b, ln2_w, ln2_b). */
+void* cbis_weights_tensor(const cbis_weights* w, const char* name);
+
+/* ---- TransformerRunner (include/transformer.hpp:15-34) ------------------ */
+cbis_runner* cbis_runner_create(const cbis_weights* w, cbis_cache* c, int max_total_rows);
+void cbis_runner_destroy(cbis_runner* r);
+/* forward_step: row i is (token_ids[i], positions[i], seq_ids[i]); the caller
+ * ran ensure_capacity for every row.  logits_out: host [n, vocab] fp32. */
+int cbis_runner_forward_step(cbis_runner* r, int n, const int* token_ids, const int* positions,
+                             const int* seq_ids, float* logits_out);
+/* Same step with the greedy argmax of every row taken on the device;
+ * next_tokens: host [n]. */
+int cbis_runner_forward_step_greedy(cbis_runner* r, int n, const int* token_ids, const int* positions,
+                                    const int* seq_ids, int* next_tokens);
+/* Device pointer of the last step's [n, vocab] fp32 logits. */
+const float* cbis_runner_logits_device(cbis_runner* r);
+/* hipStream_t the runner launches on. */
+void* cbis_runner_stream(cbis_runner* r);
+/* Enable / disable HIP-graph replay of steps whose shape repeats. */
+void cbis_runner_set_graphs(cbis_runner* r, int enable);
+
+/* ---- continuous batching (src/bench_batching.cpp:98-179) ---------------- */
+/* All requests are present at t = 0.  prompt_tokens concatenates the
+ * prompts; out_tokens receives decode_lens[i] tokens per request,
+ * concatenated.  step_ms (optional, capacity max_steps) receives each
+ * step's wall time; returns the number of steps run, or negative. */
+int cbis_run_continuous(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
+                        const int* prompt_tokens, const int* decode_lens, int max_slots, int* out_tokens,
+                        double* step_ms, int max_steps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CBIS_RUNTIME_H */

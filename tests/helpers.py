@@ -1,0 +1,48 @@
+"""Shared helpers for the GPU parity tests (torch is used only for device
+memory and the stream handle)."""
+import numpy as np
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def bf16_dev(a_f32, dev):
+    """fp32 numpy -> device bf16 tensor (round to nearest even), plus the
+    exact fp32 values it holds."""
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a_f32, dtype=np.float32)).to(dev).to(torch.bfloat16)
+    return t, t.float().cpu().numpy()
+
+
+def bits_u16(t):
+    import torch
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def row_rel_err(got, ref):
+    """max over rows of ||got - ref||_inf / ||ref||_inf (the bf16/fp8 metric)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    num = np.abs(got - ref).max(axis=-1)
+    den = np.maximum(np.abs(ref).max(axis=-1), 1e-30)
+    return float((num / den).max())
+
+
+def rng(seed):
+    return np.random.default_rng(seed)

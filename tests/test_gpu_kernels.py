@@ -1,0 +1,491 @@
+"""Kernel-level parity of the HIP path (through the C-ABI) against the CPU
+oracle on the same seeded inputs.
+
+Tolerances (north_star): fp32 paths 1e-4 max-abs; bf16 / fp8 paths 2e-2
+relative (per row ||d||_inf / ||ref||_inf); integer / byte work bit-exact.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from helpers import bf16_dev, bits_u16, ptr, row_rel_err, rng, stream, sync, to_dev
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+LOWP_TOL = 2e-2
+
+
+def _gemm(cbis, M, N, K, X, x_dtype, W, w_dtype, Y, y_dtype, bias=None, w_scale=None, gelu=False, residual=None,
+          kv=None):
+    d = cbis.GemmDesc()
+    d.M, d.N, d.K = M, N, K
+    d.x_dtype, d.X, d.ldx = x_dtype, ptr(X), K
+    d.w_dtype, d.W, d.ldw = w_dtype, ptr(W), K
+    d.w_scale = ptr(w_scale)
+    d.bias = ptr(bias)
+    d.epilogue = cbis.EPI_GELU if gelu else cbis.EPI_NONE
+    d.residual, d.ldr = ptr(residual), N
+    d.y_dtype, d.Y, d.ldy = y_dtype, ptr(Y), (kv["ldy"] if kv else N)
+    if kv:
+        d.kv_col0, d.kv_width, d.kv_dtype, d.page_size = kv["col0"], kv["width"], kv["dtype"], 16
+        d.k_pool, d.v_pool = ptr(kv["k"]), ptr(kv["v"])
+        d.write_page, d.write_offset = ptr(kv["wpage"]), ptr(kv["woff"])
+    cbis.check(cbis.kernels().cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
+    sync()
+
+
+# --------------------------------------------------------------------------
+# synthetic data and number formats: bit-exact
+# --------------------------------------------------------------------------
+
+def test_fill_normal_exact_matches_oracle_prng(cbis, oracle, dev):
+    import torch
+    n = 200_003
+    out = torch.empty(n, dtype=torch.float32, device=dev)
+    cbis.check(cbis.kernels().cbis_fill_normal_exact(ptr(out), cbis.F32, n, 0, 105, 777, 0.02, stream()))
+    sync()
+    ref = oracle.normal(0, 105, n, 0.02, start=777)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    outb = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    cbis.check(cbis.kernels().cbis_fill_normal_exact(ptr(outb), cbis.BF16, n, 3, 2, 0, 1.0, stream()))
+    sync()
+    assert np.array_equal(bits_u16(outb), oracle.f32_to_bf16_bits(oracle.normal(3, 2, n, 1.0)))
+
+
+def test_convert_bf16_and_fp8_quantise_bit_exact(cbis, oracle, dev):
+    import torch
+    g = rng(1)
+    N, K = 96, 512
+    w = (g.standard_normal((N, K)) * 0.02).astype(np.float32)
+    # exact rounding ties and extremes for both codecs
+    w[0, :8] = np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.0 - 2 ** -8, 0.0, -0.0, 1e-30, 3e38, -3e38], np.float32)
+    w[1, :4] = np.array([448.0, -448.0, 300.0, 2 ** -10], np.float32) * 1e-3
+    w[2, :] = 0.0  # all-zero row: scale 1
+    src = to_dev(w, dev)
+    b = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    cbis.check(cbis.kernels().cbis_convert_f32(ptr(b), cbis.BF16, ptr(src), N * K, stream()))
+    codes = torch.empty((N, K), dtype=torch.uint8, device=dev)
+    scale = torch.empty(N, dtype=torch.float32, device=dev)
+    cbis.check(cbis.kernels().cbis_quantize_fp8_rows(ptr(codes), ptr(scale), ptr(src), N, K, stream()))
+    sync()
+    assert np.array_equal(bits_u16(b), oracle.f32_to_bf16_bits(w))
+    ref_codes, ref_scale = oracle.quantize_e4m3_rows(w)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint32), ref_scale.view(np.uint32))
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+
+
+# --------------------------------------------------------------------------
+# GEMM
+# --------------------------------------------------------------------------
+
+C2_SHAPES = [  # (name, N, K, bias, gelu, residual)
+    ("qkv", 768, 256, True, False, False),
+    ("out", 256, 256, True, False, False),
+    ("up", 1024, 256, True, True, False),
+    ("down", 256, 1024, True, False, True),
+]
+
+
+def _sample_rows(M, k, seed):
+    if M <= k:
+        return np.arange(M)
+    r = rng(seed).choice(M, size=k, replace=False)
+    r.sort()
+    return r
+
+
+@pytest.mark.parametrize("M", [64, 512, 4096])
+@pytest.mark.parametrize("shape", C2_SHAPES, ids=lambda s: s[0])
+def test_gemm_fp32_c2(cbis, oracle, dev, M, shape):
+    import torch
+    name, N, K, has_b, gelu, has_r = shape
+    x = oracle.normal(11, 1, M * K).reshape(M, K)
+    w = oracle.normal(11, 2, N * K, 0.02).reshape(N, K)
+    b = oracle.normal(11, 3, N, 0.02) if has_b else None
+    r = oracle.normal(11, 4, M * N).reshape(M, N) if has_r else None
+    X, W = to_dev(x, dev), to_dev(w, dev)
+    B = to_dev(b, dev) if has_b else None
+    Y = to_dev(r, dev) if has_r else torch.empty((M, N), dtype=torch.float32, device=dev)
+    _gemm(cbis, M, N, K, X, cbis.F32, W, cbis.F32, Y, cbis.F32, bias=B, gelu=gelu, residual=Y if has_r else None)
+    rows = _sample_rows(M, 512, M)
+    ref = oracle.gemm(x[rows], w, bias=b, gelu=gelu, residual=None if r is None else r[rows])
+    err = np.abs(Y.cpu().numpy()[rows] - ref).max()
+    assert err < FP32_TOL, err
+
+
+@pytest.mark.parametrize("M", [64, 512, 4096])
+@pytest.mark.parametrize("shape", C2_SHAPES, ids=lambda s: s[0])
+def test_gemm_bf16_c2(cbis, oracle, dev, M, shape):
+    import torch
+    name, N, K, has_b, gelu, has_r = shape
+    X, x = bf16_dev(oracle.normal(12, 1, M * K).reshape(M, K), dev)
+    W, w = bf16_dev(oracle.normal(12, 2, N * K, 0.02).reshape(N, K), dev)
+    b = oracle.normal(12, 3, N, 0.02) if has_b else None
+    r = oracle.normal(12, 4, M * N).reshape(M, N) if has_r else None
+    B = to_dev(b, dev) if has_b else None
+    R = to_dev(r, dev) if has_r else None
+    Y32 = torch.empty((M, N), dtype=torch.float32, device=dev)
+    Y16 = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    _gemm(cbis, M, N, K, X, cbis.BF16, W, cbis.BF16, Y32, cbis.F32, bias=B, gelu=gelu, residual=R)
+    _gemm(cbis, M, N, K, X, cbis.BF16, W, cbis.BF16, Y16, cbis.BF16, bias=B, gelu=gelu, residual=R)
+    rows = _sample_rows(M, 512, M + 1)
+    ref = oracle.gemm(x[rows], w, bias=b, gelu=gelu, residual=None if r is None else r[rows])
+    # fp32 output: only accumulation order differs from the fp64 oracle
+    assert np.abs(Y32.cpu().numpy()[rows] - ref).max() < FP32_TOL
+    assert row_rel_err(Y16.float().cpu().numpy()[rows], ref) < LOWP_TOL
+
+
+@pytest.mark.parametrize("N,K", [(6144, 2048), (2048, 2048), (8192, 2048), (2048, 8192), (32000, 2048)])
+def test_gemm_bf16_c4_shapes(cbis, oracle, dev, N, K):
+    """Config 4's per-layer GEMMs at M=1216 (checked on sampled rows)."""
+    import torch
+    M = 1216
+    X, x = bf16_dev(oracle.normal(13, 1, M * K).reshape(M, K), dev)
+    W, w = bf16_dev(oracle.normal(13, 2, N * K, 0.02).reshape(N, K), dev)
+    Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _gemm(cbis, M, N, K, X, cbis.BF16, W, cbis.BF16, Y, cbis.F32)
+    rows = _sample_rows(M, 24, N)
+    rows[-1] = M - 1  # include the ragged last M tile
+    ref = oracle.gemm(x[rows], w)
+    assert np.abs(Y.cpu().numpy()[rows] - ref).max() < FP32_TOL * 4
+
+
+@pytest.mark.parametrize("M", [16, 200])
+def test_gemm_fp8_weights(cbis, oracle, dev, M):
+    import torch
+    N, K = 1000, 2048
+    w = oracle.normal(14, 2, N * K, 0.02).reshape(N, K)
+    codes, sc = oracle.quantize_e4m3_rows(w)
+    wdq = oracle.e4m3_table()[codes]
+    X, x = bf16_dev(oracle.normal(14, 1, M * K).reshape(M, K), dev)
+    b = oracle.normal(14, 3, N, 0.02)
+    C, S, B = to_dev(codes, dev), to_dev(sc, dev), to_dev(b, dev)
+    Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _gemm(cbis, M, N, K, X, cbis.BF16, C, cbis.FP8E4M3, Y, cbis.F32, bias=B, w_scale=S)
+    ref = oracle.gemm(x, wdq, w_scale=sc, bias=b)
+    assert np.abs(Y.cpu().numpy() - ref).max() < FP32_TOL
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_gemm_qkv_scatter_epilogue(cbis, oracle, dev, kv_dtype):
+    """Fused QKV projection: Q to its buffer, K/V straight into page slots
+    (the fused form of scatter_kv_to_cache, kernels/attention.cu:7-19)."""
+    import torch
+    M, D, P = 77, 256, 40
+    dt = cbis.F32 if kv_dtype == "f32" else cbis.BF16
+    act = np.float32
+    x = oracle.normal(15, 1, M * D).reshape(M, D)
+    w = oracle.normal(15, 2, 3 * D * D, 0.02).reshape(3 * D, D)
+    b = oracle.normal(15, 3, 3 * D, 0.02)
+    if dt == cbis.F32:
+        X, W = to_dev(x, dev), to_dev(w, dev)
+        xv, wv = x, w
+        tdt = torch.float32
+    else:
+        X, xv = bf16_dev(x, dev)
+        W, wv = bf16_dev(w, dev)
+        tdt = torch.bfloat16
+    slots = rng(5).permutation(P * 16)[:M]
+    wpage, woff = (slots // 16).astype(np.int32), (slots % 16).astype(np.int32)
+    kp = torch.zeros((P, 16, D), dtype=tdt, device=dev)
+    vp = torch.zeros((P, 16, D), dtype=tdt, device=dev)
+    Q = torch.zeros((M, D), dtype=torch.float32, device=dev)
+    kv = {"col0": D, "width": D, "dtype": dt, "k": kp, "v": vp, "wpage": to_dev(wpage, dev),
+          "woff": to_dev(woff, dev), "ldy": D}
+    _gemm(cbis, M, 3 * D, D, X, dt, W, dt, Q, cbis.F32, bias=to_dev(b, dev), kv=kv)
+    ref = oracle.gemm(xv, wv, bias=b).astype(act)
+    assert np.abs(Q.cpu().numpy() - ref[:, :D]).max() < FP32_TOL
+    kh, vh = kp.float().cpu().numpy(), vp.float().cpu().numpy()
+    gk, gv = kh[wpage, woff], vh[wpage, woff]
+    if dt == cbis.F32:
+        assert np.abs(gk - ref[:, D:2 * D]).max() < FP32_TOL
+        assert np.abs(gv - ref[:, 2 * D:]).max() < FP32_TOL
+    else:
+        assert row_rel_err(gk, ref[:, D:2 * D]) < LOWP_TOL
+        assert row_rel_err(gv, ref[:, 2 * D:]) < LOWP_TOL
+    # untouched slots stay zero
+    mask = np.ones((P, 16), bool)
+    mask[wpage, woff] = False
+    assert not kh[mask].any() and not vh[mask].any()
+
+
+def test_gemm_rejects_bad_shapes(cbis):
+    d = cbis.GemmDesc()
+    d.M, d.N, d.K = 4, 8, 100  # K not a multiple of 64 for bf16
+    d.x_dtype = d.w_dtype = d.y_dtype = cbis.BF16
+    d.X = d.W = d.Y = 256
+    d.ldx = d.ldw = 100
+    d.ldy = 8
+    assert cbis.kernels().cbis_gemm(ctypes.byref(d), None) == 2
+
+
+# --------------------------------------------------------------------------
+# LayerNorm, embedding, argmax, reference elementwise launchers
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("D", [256, 2048])
+@pytest.mark.parametrize("ydt", ["f32", "bf16"])
+def test_layernorm(cbis, oracle, dev, D, ydt):
+    import torch
+    M = 300
+    x = (oracle.normal(16, 1, M * D).reshape(M, D) * 3 + 1.5).astype(np.float32)
+    g = (1 + oracle.normal(16, 2, D, 0.3)).astype(np.float32)
+    b = oracle.normal(16, 3, D, 0.3)
+    X, G, B = to_dev(x, dev), to_dev(g, dev), to_dev(b, dev)
+    tdt = torch.float32 if ydt == "f32" else torch.bfloat16
+    Y = torch.empty((M, D), dtype=tdt, device=dev)
+    cbis.check(cbis.kernels().cbis_layernorm(M, D, ptr(X), D, ptr(G), ptr(B), 1e-5, cbis.DTYPES[ydt], ptr(Y), D,
+                                             stream()))
+    sync()
+    ref = oracle.layernorm(x, g, b)
+    if ydt == "f32":
+        assert np.abs(Y.cpu().numpy() - ref).max() < 1e-5 * 10
+    else:
+        assert row_rel_err(Y.float().cpu().numpy(), ref) < LOWP_TOL
+
+
+@pytest.mark.parametrize("edt", ["f32", "bf16"])
+def test_embed(cbis, oracle, dev, edt):
+    import torch
+    V, S, D, M = 512, 100, 256, 50
+    te = oracle.normal(17, 1, V * D, 0.02).reshape(V, D)
+    pe = oracle.normal(17, 2, S * D, 0.02).reshape(S, D)
+    tok = oracle.uniform_int(17, 3, M, 0, V - 1)
+    pos = oracle.uniform_int(17, 4, M, 0, S - 1)
+    if edt == "f32":
+        TE, PE, tev, pev = to_dev(te, dev), to_dev(pe, dev), te, pe
+    else:
+        (TE, tev), (PE, pev) = bf16_dev(te, dev), bf16_dev(pe, dev)
+    out = torch.empty((M, D), dtype=torch.float32, device=dev)
+    cbis.check(cbis.kernels().cbis_embed(M, D, ptr(to_dev(tok, dev)), ptr(to_dev(pos, dev)), cbis.DTYPES[edt],
+                                         ptr(TE), ptr(PE), V, S, ptr(out), stream()))
+    sync()
+    ref = tev[tok].astype(np.float64) + pev[pos]
+    assert np.array_equal(out.cpu().numpy(), ref.astype(np.float32))
+
+
+def test_argmax_first_max_wins(cbis, oracle, dev):
+    import torch
+    M, N = 64, 32000
+    L = oracle.normal(18, 1, M * N).reshape(M, N)
+    L[0, :] = 1.0                   # all equal -> 0
+    L[1, 5] = L[1, 31999] = 99.0    # tie -> 5
+    L[2, :] = -np.inf               # -inf row -> 0
+    L[3, 31999] = 50.0              # last column
+    T = to_dev(L, dev)
+    out = torch.empty(M, dtype=torch.int32, device=dev)
+    cbis.check(cbis.kernels().cbis_argmax_rows(M, N, ptr(T), N, ptr(out), stream()))
+    sync()
+    assert np.array_equal(out.cpu().numpy(), oracle.argmax_rows(L))
+
+
+def test_reference_signature_elementwise(cbis, oracle, dev):
+    import torch
+    K = cbis.kernels()
+    T, D, V, S = 40, 256, 1000, 64
+    te = oracle.normal(19, 1, V * D, 0.02).reshape(V, D)
+    pe = oracle.normal(19, 2, S * D, 0.02).reshape(S, D)
+    tok = oracle.uniform_int(19, 3, T, 0, V - 1)
+    pos = np.arange(T, dtype=np.int32)
+    x = torch.empty((T, D), dtype=torch.float32, device=dev)
+    cbis.check(K.cbis_embed_lookup_add(ptr(to_dev(tok, dev)), ptr(to_dev(pos, dev)), ptr(to_dev(te, dev)),
+                                       ptr(to_dev(pe, dev)), ptr(x), T, D, stream()))
+    g = (1 + oracle.normal(19, 4, D, 0.1)).astype(np.float32)
+    b = oracle.normal(19, 5, D, 0.1)
+    y = torch.empty_like(x)
+    cbis.check(K.cbis_layernorm_forward(ptr(x), ptr(to_dev(g, dev)), ptr(to_dev(b, dev)), ptr(y), T, D, stream()))
+    w = oracle.normal(19, 6, 1024 * D, 0.02).reshape(1024, D)
+    bb = oracle.normal(19, 7, 1024, 0.02)
+    h = torch.empty((T, 1024), dtype=torch.float32, device=dev)
+    cbis.check(K.cbis_linear_forward(ptr(y), ptr(to_dev(w, dev)), ptr(to_dev(bb, dev)), ptr(h), T, D, 1024, stream()))
+    cbis.check(K.cbis_gelu_forward(ptr(h), T, 1024, stream()))
+    r = torch.ones((T, 1024), dtype=torch.float32, device=dev)
+    cbis.check(K.cbis_residual_add(ptr(r), ptr(h), T, 1024, stream()))
+    sync()
+    xe = te[tok].astype(np.float64) + pe[pos]
+    assert np.abs(x.cpu().numpy() - xe).max() < 1e-7
+    ye = oracle.layernorm(xe.astype(np.float32), g, b)
+    assert np.abs(y.cpu().numpy() - ye).max() < 1e-4
+    he = oracle.gemm(y.cpu().numpy(), w, bias=bb, gelu=True)
+    assert np.abs(r.cpu().numpy() - (1.0 + he)).max() < FP32_TOL
+
+
+# --------------------------------------------------------------------------
+# Paged attention
+# --------------------------------------------------------------------------
+
+def _attn_desc(cbis, n_rows, H, q, kp, vp, num_pages, bt, bt_stride, pos, out, kv_dtype, q_dtype=0, out_dtype=0,
+               rows=None, row_bt=None, max_kv=0, split=0, ws=None):
+    d = cbis.AttnDesc()
+    d.n_rows, d.rows, d.n_heads, d.head_dim, d.page_size = n_rows, ptr(rows), H, 32, 16
+    d.q_dtype, d.q, d.ldq = q_dtype, ptr(q), H * 32
+    d.kv_dtype, d.k_pool, d.v_pool, d.num_pages = kv_dtype, ptr(kp), ptr(vp), num_pages
+    d.block_table, d.bt_stride, d.row_bt, d.row_pos = ptr(bt), bt_stride, ptr(row_bt), ptr(pos)
+    d.out_dtype, d.out, d.ldo = out_dtype, ptr(out), H * 32
+    d.max_kv_len, d.split_tokens = max_kv, split
+    if ws is not None:
+        d.workspace, d.workspace_bytes = ptr(ws), ws.numel() * ws.element_size()
+    return d
+
+
+def _c3_inputs(oracle, n_seq=256, lo=128, hi=2048, pool=40000, seed=0):
+    """Config 3: kv_len U[lo, hi], one query per sequence at pos kv_len-1,
+    a random permutation of a pool of `pool` pages as the page table."""
+    kv = oracle.uniform_int(seed, 3001, n_seq, lo, hi)
+    npages = (kv + 15) // 16
+    perm = rng(seed).permutation(pool).astype(np.int32)
+    stride = int(npages.max())
+    bt = np.zeros((n_seq, stride), np.int32)
+    off = 0
+    for i in range(n_seq):
+        bt[i, : npages[i]] = perm[off: off + npages[i]]
+        off += npages[i]
+    assert off <= pool
+    return kv.astype(np.int32), bt
+
+
+def test_decode_attention_c3_full_size(cbis, oracle, dev):
+    """BASELINE config 3 at full size: 256 sequences, kv U[128, 2048], 8x32,
+    fp32 K/V in a 40,000-page pool with a permuted page table."""
+    import torch
+    H, P = 8, 40000
+    kv, bt = _c3_inputs(oracle)
+    n = kv.size
+    kp = torch.empty((P, 16, H, 32), dtype=torch.float32, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    for t, s in ((kp, 1), (vp, 2), (q, 3)):
+        cbis.check(K.cbis_fill_normal_fast(ptr(t), cbis.F32, t.numel(), s, 1.0, stream()))
+    pos = kv - 1
+    BT, POS = to_dev(bt, dev), to_dev(pos, dev)
+    out_split = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
+    d = _attn_desc(cbis, n, H, q, kp, vp, P, BT, bt.shape[1], POS, out_split, cbis.F32, max_kv=int(kv.max()))
+    need = K.cbis_paged_attention_workspace_size(ctypes.byref(d))
+    assert need > 0
+    ws = torch.empty(need // 4 + 1, dtype=torch.float32, device=dev)
+    d.workspace, d.workspace_bytes = ptr(ws), need
+    cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream()))
+    # the reference-signature entry point (single pass, no workspace) on a
+    # [rows, pages_per_seq] row page table
+    out_ref_api = torch.empty_like(out_split)
+    cbis.check(K.cbis_fused_paged_causal_attention(ptr(q), ptr(kp), ptr(vp), ptr(BT), ptr(POS), ptr(out_ref_api), n, H,
+                                                   32, 16, bt.shape[1], stream()))
+    sync()
+    ref = oracle.paged_attention(q.cpu().numpy(), kp.cpu().numpy(), vp.cpu().numpy(), bt, pos, H, 32, 16)
+    assert np.abs(out_split.cpu().numpy() - ref).max() < FP32_TOL
+    assert np.abs(out_ref_api.cpu().numpy() - ref).max() < FP32_TOL
+
+
+@pytest.mark.parametrize("out_dtype", ["f32", "bf16"])
+def test_decode_attention_bf16_rows_subset(cbis, oracle, dev, out_dtype):
+    """bf16 pools with 64 heads, a row subset (rows list + row->table map),
+    kv lengths that end mid-page and a forced small split."""
+    import torch
+    H, P, S = 64, 3000, 12
+    kv = np.array([1, 15, 16, 17, 33, 100, 255, 256, 257, 1000, 2049, 4096], np.int32)
+    npages = (kv + 15) // 16
+    perm = rng(2).permutation(P).astype(np.int32)
+    bt = np.zeros((S, int(npages.max())), np.int32)
+    off = 0
+    for i in range(S):
+        bt[i, : npages[i]] = perm[off: off + npages[i]]
+        off += npages[i]
+    M = 20  # rows; row r belongs to sequence row_bt[r]
+    row_bt = rng(3).integers(0, S, M).astype(np.int32)
+    pos = np.array([rng(4 + r).integers(0, kv[row_bt[r]]) for r in range(M)], np.int32)
+    rows = np.array(sorted(rng(5).choice(M, 15, replace=False)), np.int32)
+    kp = torch.empty((P, 16, H, 32), dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((M, H * 32), dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    for t, s, dt in ((kp, 11, cbis.BF16), (vp, 12, cbis.BF16), (q, 13, cbis.F32)):
+        cbis.check(K.cbis_fill_normal_fast(ptr(t), dt, t.numel(), s, 1.0, stream()))
+    odt = torch.float32 if out_dtype == "f32" else torch.bfloat16
+    ref = oracle.paged_attention(q.cpu().numpy()[rows], bits_u16(kp), bits_u16(vp), bt, pos[rows], H, 32, 16,
+                                 row_bt=row_bt[rows], kv_dtype=1)
+    for split in (0, 64, 1 << 20):
+        out = torch.full((M, H * 32), 7.0, dtype=odt, device=dev)
+        d = _attn_desc(cbis, len(rows), H, q, kp, vp, P, to_dev(bt, dev), bt.shape[1], to_dev(pos, dev), out,
+                       cbis.BF16, out_dtype=cbis.DTYPES[out_dtype], rows=to_dev(rows, dev),
+                       row_bt=to_dev(row_bt, dev), max_kv=int(kv.max()), split=split)
+        need = K.cbis_paged_attention_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+        d.workspace, d.workspace_bytes = ptr(ws), need
+        cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream()))
+        sync()
+        got = out.float().cpu().numpy()
+        if out_dtype == "f32":
+            assert np.abs(got[rows] - ref).max() < FP32_TOL, split
+        else:
+            assert row_rel_err(got[rows], ref) < LOWP_TOL, split
+        others = np.setdiff1d(np.arange(M), rows)
+        assert (got[others] == 7.0).all()  # rows outside the list untouched
+
+
+def test_decode_attention_closed_forms(cbis, oracle, dev):
+    """kv_len = 1 gives v0 exactly; identical keys give the mean of V."""
+    import torch
+    H, P = 8, 64
+    kp = torch.zeros((P, 16, H, 32), dtype=torch.float32, device=dev)
+    vp = torch.empty_like(kp)
+    K = cbis.kernels()
+    cbis.check(K.cbis_fill_normal_fast(ptr(vp), cbis.F32, vp.numel(), 21, 1.0, stream()))
+    q = torch.empty((2, H * 32), dtype=torch.float32, device=dev)
+    cbis.check(K.cbis_fill_normal_fast(ptr(q), cbis.F32, q.numel(), 22, 1.0, stream()))
+    bt = np.array([[5, 9, 2, 0], [7, 1, 3, 4]], np.int32)
+    pos = np.array([0, 50], np.int32)   # kv_len 1 and 51 (all keys zero -> equal scores)
+    out = torch.empty((2, H * 32), dtype=torch.float32, device=dev)
+    d = _attn_desc(cbis, 2, H, q, kp, vp, P, to_dev(bt, dev), 4, to_dev(pos, dev), out, cbis.F32)
+    cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream()))
+    sync()
+    v = vp.cpu().numpy()
+    o = out.cpu().numpy().reshape(2, H, 32)
+    assert np.array_equal(o[0], v[5, 0])
+    keys = [v[bt[1, j // 16], j % 16] for j in range(51)]
+    assert np.abs(o[1] - np.mean(keys, axis=0)).max() < 1e-5
+
+
+def test_decode_attention_rejects_unsupported(cbis):
+    d = cbis.AttnDesc()
+    d.n_rows, d.n_heads, d.head_dim, d.page_size = 4, 8, 64, 16
+    d.q = d.k_pool = d.v_pool = d.block_table = d.out = d.row_pos = 256
+    d.num_pages, d.bt_stride = 10, 4
+    assert cbis.kernels().cbis_paged_attention(ctypes.byref(d), None) == 2
+    d.head_dim = 32
+    d.max_kv_len, d.split_tokens = 4096, 64  # needs a workspace
+    assert cbis.kernels().cbis_paged_attention(ctypes.byref(d), None) == 3
+
+
+@pytest.mark.parametrize("cached,n_rows", [(0, 100), (37, 64), (512, 512)])
+def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows):
+    """A chunk of n_rows consecutive positions after `cached` cached tokens
+    (config 4's chunks are (0, 512) and (512, 512))."""
+    import torch
+    H, P = 64, 200
+    total = cached + n_rows
+    npages = (total + 15) // 16
+    bt = rng(7).permutation(P)[:npages].astype(np.int32)[None, :]
+    kp = torch.empty((P, 16, H, 32), dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((n_rows, H * 32), dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    for t, s, dt in ((kp, 31, cbis.BF16), (vp, 32, cbis.BF16), (q, 33, cbis.F32)):
+        cbis.check(K.cbis_fill_normal_fast(ptr(t), dt, t.numel(), s, 1.0, stream()))
+    pos = (cached + np.arange(n_rows)).astype(np.int32)
+    tiles = []
+    for r in range(0, n_rows, 32):
+        tiles += [r, min(32, n_rows - r), 0, cached + r]
+    T = to_dev(np.array(tiles, np.int32), dev)
+    out = torch.empty((n_rows, H * 32), dtype=torch.bfloat16, device=dev)
+    d = _attn_desc(cbis, n_rows, H, q, kp, vp, P, to_dev(bt, dev), bt.shape[1], None, out, cbis.BF16,
+                   out_dtype=cbis.BF16)
+    cbis.check(K.cbis_paged_prefill_attention(ctypes.byref(d), len(tiles) // 4, ptr(T), stream()))
+    sync()
+    ref = oracle.paged_attention(q.cpu().numpy(), bits_u16(kp), bits_u16(vp), np.repeat(bt, n_rows, 0), pos, H, 32,
+                                 16, kv_dtype=1)
+    got = out.float().cpu().numpy()
+    assert row_rel_err(got.reshape(n_rows * H, 32), ref.reshape(n_rows * H, 32)) < LOWP_TOL * 2
+    assert np.abs(got - ref).mean() < 2e-3
