@@ -1,0 +1,317 @@
+#!/usr/bin/env python3
+"""Benchmark of the per-step forward on one MI355X.
+
+Default workload: the mid-size GPT (16 layers, d 2048,
+64x32 heads, MLP 8192, vocab 32000, bf16 weights with fp32 accumulation, bf16
+paged K/V) running one mixed continuous-batch step of 192 decode rows
+(kv_len U[256, 4096] over synthetic cached K/V) plus two 512-row prefill
+chunks (a fresh sequence at positions 0..511 and a sequence with 512 cached
+tokens at positions 512..1023): M = 1216 rows.  The physical page table is
+shuffled (single-page sequences freed in a random order before admission).
+A step is TransformerRunner::forward_step_greedy (every layer, lm_head over
+all 1216 rows, device argmax); metric = decode tokens/s = 192 / step time.
+
+Also measured live with HIP events on the runner's stream:
+  * the dominant kernel, split-KV paged decode attention of one layer over the
+    step's 192 decode rows (roofline: HBM, algorithmic bytes / duration);
+  * the step's bf16 GEMMs at M = 1216 (MFMA roofline, reported beside).
+cpu_baseline: the C oracle (a scalar-per-row fp64 restatement, OpenMP) timed
+on the host on one layer of the same step plus lm_head, scaled to 16 layers.
+
+Other modes: --config c1 (tiny fp32 GPT greedy continuous batching),
+--config c3 (paged decode attention alone), --config c5 (long-context fp8
+decode); --copy-calib (a plain device copy for PMC byte calibration).
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def _log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _cbis():
+    import __graft_entry__ as ge
+    return ge._import_cbis()
+
+
+class Events:
+    """HIP events on an explicit stream (the runner's), via torch's wrappers."""
+
+    def __init__(self, stream_handle):
+        import torch
+        self.torch = torch
+        self.stream = torch.cuda.ExternalStream(stream_handle) if stream_handle else torch.cuda.current_stream()
+
+    def time(self, fn, iters):
+        torch = self.torch
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(self.stream):
+            s.record(self.stream)
+            for _ in range(iters):
+                fn()
+            e.record(self.stream)
+        e.synchronize()
+        return s.elapsed_time(e) / iters  # ms
+
+
+def shuffled_cache(cbis, cache, n_pages, seed):
+    """Hands the allocator a shuffled free list using only the reference API:
+    n_pages one-page sequences take pages 0..n-1, then are freed in a random
+    order (free_sequence pushes their page back), so later allocations pop
+    physical pages in random order."""
+    rng = np.random.default_rng(seed)
+    dummies = []
+    for _ in range(n_pages):
+        s = cache.allocate_sequence()
+        assert cache.ensure_capacity(s, 0)
+        dummies.append(s)
+    for i in rng.permutation(n_pages):
+        cache.free_sequence(dummies[i])
+
+
+def c4_setup(cbis, oracle, n_layers=16, seed=0):
+    cfg = cbis.ModelConfig.make(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=n_layers, mlp=8192,
+                                max_seq=32768, weight_dtype="bf16", kv_dtype="bf16")
+    kv = oracle.uniform_int(seed, 5001, 192, 256, 4096)
+    pages_needed = int(((kv + 15) // 16).sum()) + 32 + 64
+    max_pages = pages_needed + 64
+    t0 = time.time()
+    w = cbis.ModelWeights.synthetic(cfg, seed=seed)
+    cache = cbis.PagedKVCache(n_layers, max_pages, 16, 64, 32, "bf16", pages_per_seq=2048)
+    cache.fill_normal(seed=seed + 1, std=1.0)
+    shuffled_cache(cbis, cache, max_pages, seed)
+    runner = cbis.TransformerRunner(w, cache, 1216)
+    toks = oracle.uniform_int(seed, 5002, 1216, 0, 31999)
+    tok, pos, sid, dec_seqs = [], [], [], []
+    for i in range(192):
+        s = cache.allocate_sequence()
+        assert cache.ensure_capacity(s, int(kv[i]) - 1)  # grows the page list to cover 0..kv-1
+        tok.append(int(toks[i])); pos.append(int(kv[i]) - 1); sid.append(s); dec_seqs.append(s)
+    for start in (0, 512):
+        s = cache.allocate_sequence()
+        assert cache.ensure_capacity(s, start + 511)
+        for p in range(start, start + 512):
+            tok.append(int(toks[len(tok)])); pos.append(p); sid.append(s)
+    _log(f"c4 setup {time.time() - t0:.1f}s: weights {w.device_bytes() / 1e9:.2f} GB, "
+         f"kv pool {max_pages} pages x {n_layers} layers")
+    return dict(cfg=cfg, w=w, cache=cache, runner=runner, tok=tok, pos=pos, sid=sid, kv=kv, dec_seqs=dec_seqs)
+
+
+def decode_attention_timing(cbis, st, iters):
+    """Times one layer's split-KV decode attention over the step's 192 decode
+    rows (the dominant kernel) on the runner's stream."""
+    import torch
+    cache, kv = st["cache"], st["kv"]
+    n, H = 192, 64
+    tables = [cache.pages(s) for s in st["dec_seqs"]]
+    width = max(len(t) for t in tables)
+    bt = np.zeros((n, width), np.int32)
+    for i, t in enumerate(tables):
+        bt[i, : len(t)] = t
+    dev = torch.device("cuda:0")
+    BT = torch.from_numpy(bt).to(dev)
+    POS = torch.from_numpy((kv - 1).astype(np.int32)).to(dev)
+    q = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
+    cbis.check(cbis.kernels().cbis_fill_normal_fast(q.data_ptr(), cbis.F32, q.numel(), 7, 1.0, None))
+    out = torch.empty((n, H * 32), dtype=torch.bfloat16, device=dev)
+    d = cbis.AttnDesc()
+    d.n_rows, d.n_heads, d.head_dim, d.page_size = n, H, 32, 16
+    d.q_dtype, d.q, d.ldq = cbis.F32, q.data_ptr(), H * 32
+    d.kv_dtype, d.k_pool, d.v_pool, d.num_pages = cbis.BF16, cache.k_base(0), cache.v_base(0), cache.max_pages()
+    d.block_table, d.bt_stride, d.row_pos = BT.data_ptr(), width, POS.data_ptr()
+    d.out_dtype, d.out, d.ldo = cbis.BF16, out.data_ptr(), H * 32
+    d.max_kv_len = int(kv.max())
+    need = cbis.kernels().cbis_paged_attention_workspace_size(ctypes.byref(d))
+    ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+    d.workspace, d.workspace_bytes = ws.data_ptr(), need
+    torch.cuda.synchronize()
+    ev = Events(st["runner"].stream())
+    stream = st["runner"].stream()
+    fn = lambda: cbis.check(cbis.kernels().cbis_paged_attention(ctypes.byref(d), stream))
+    ev.time(fn, 3)
+    ms = ev.time(fn, iters)
+    kvsum = int(kv.sum())
+    alg_bytes = kvsum * H * 32 * 2 * 2 + int(((kv + 15) // 16).sum()) * 4 + n * H * 32 * 4 + n * H * 32 * 2
+    return ms, alg_bytes
+
+
+def gemm_timing(cbis, st, iters):
+    """Times the step's bf16 GEMM shapes at M = 1216 (layer 0 weights)."""
+    import torch
+    w = st["w"]
+    dev = torch.device("cuda:0")
+    M = 1216
+    shapes = [("qkv", 6144, 2048, "l0.wqkv"), ("out", 2048, 2048, "l0.wo"), ("fc1", 8192, 2048, "l0.w1"),
+              ("fc2", 2048, 8192, "l0.w2"), ("lm_head", 32000, 2048, "lm_head")]
+    X = torch.empty((M, 8192), dtype=torch.bfloat16, device=dev)
+    cbis.check(cbis.kernels().cbis_fill_normal_fast(X.data_ptr(), cbis.BF16, X.numel(), 9, 1.0, None))
+    Y = torch.empty((M, 32000), dtype=torch.float32, device=dev)
+    ev = Events(st["runner"].stream())
+    stream = st["runner"].stream()
+    res = {}
+    tot_flops = tot_ms = 0.0
+    for name, N, K, wname in shapes:
+        d = cbis.GemmDesc()
+        d.M, d.N, d.K = M, N, K
+        d.x_dtype, d.X, d.ldx = cbis.BF16, X.data_ptr(), K
+        d.w_dtype, d.W, d.ldw = cbis.BF16, w.tensor(wname), K
+        d.y_dtype, d.Y, d.ldy = cbis.F32, Y.data_ptr(), N
+        fn = lambda d=d: cbis.check(cbis.kernels().cbis_gemm(ctypes.byref(d), stream))
+        ev.time(fn, 2)
+        ms = ev.time(fn, iters)
+        fl = 2.0 * M * N * K
+        # per layer the four projections run once; lm_head once per step
+        mult = 1 if name == "lm_head" else st["cfg"].n_layers
+        tot_flops += fl * mult
+        tot_ms += ms * mult
+        res[name] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 1)}
+    return res, tot_flops, tot_ms
+
+
+def cpu_baseline_c4(oracle, st, cbis):
+    """The C oracle on one layer of the same step + lm_head, scaled to 16
+    layers: a bounded sample (~10-30 s of CPU work)."""
+    spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
+                            max_seq=32768, weight_dtype="bf16", kv_dtype="bf16")
+    w = oracle.synthetic_weights(spec, seed=0, pos_rows=1024)
+    cache = st["cache"]
+    om = oracle.OracleModel(w, max_pages=1)
+    om.kpools = [np.empty((cache.max_pages(), 16, 64, 32), np.uint16)]
+    om.vpools = [np.empty((cache.max_pages(), 16, 64, 32), np.uint16)]
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    for dst, src in ((om.kpools[0], cache.k_base(0)), (om.vpools[0], cache.v_base(0))):
+        assert hip.hipMemcpy(dst.ctypes.data, src, dst.nbytes, 2) == 0
+    om._kp = (ctypes.c_void_p * 1)(om.kpools[0].ctypes.data)
+    om._vp = (ctypes.c_void_p * 1)(om.vpools[0].ctypes.data)
+    tok, pos, sid = st["tok"], st["pos"], st["sid"]
+    M = len(tok)
+    wpage = np.empty(M, np.int32)
+    woff = np.empty(M, np.int32)
+    uniq, row_bt = {}, np.empty(M, np.int32)
+    for i in range(M):
+        wpage[i], woff[i] = cache.resolve_slot(sid[i], pos[i])
+        row_bt[i] = uniq.setdefault(sid[i], len(uniq))
+    tables = {s: cache.pages(s) for s in uniq}
+    width = max(len(t) for t in tables.values())
+    bt = np.zeros((len(uniq), width), np.int32)
+    for s, j in uniq.items():
+        bt[j, : len(tables[s])] = tables[s]
+    t0 = time.time()
+    om.forward_step(tok, pos, wpage, woff, bt, row_bt)
+    t_layer_plus_head = time.time() - t0
+    # separate the lm_head share with a 0-layer pass (embed + ln_f + lm_head)
+    om._mdl.n_layers = 0
+    t1 = time.time()
+    om.forward_step(tok, pos, wpage, woff, bt, row_bt)
+    t_head = time.time() - t1
+    t_step = (t_layer_plus_head - t_head) * 16 + t_head
+    return {"value": round(192.0 / t_step, 3), "unit": "decode tokens/s", "cores": oracle.lib().orc_num_threads(),
+            "kind": "port",
+            "sample": f"oracle fp64 forward of config 4's 1216-row step, 1 of 16 layers ({t_layer_plus_head - t_head:.1f}s)"
+                      f" + lm_head ({t_head:.1f}s), scaled to 16 layers; step {t_step:.1f}s"}
+
+
+def run_c4(args, cbis, oracle):
+    st = c4_setup(cbis, oracle)
+    runner = st["runner"]
+    import torch
+    step = lambda: runner.forward_step_greedy(st["tok"], st["pos"], st["sid"])
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_step = dt * 1000.0 / args.steps
+    value = 192.0 * args.steps / dt
+    _log(f"c4 step {ms_step:.3f} ms -> {value:.1f} decode tok/s ({1216 * args.steps / dt:.0f} rows/s)")
+    att_ms, att_bytes = decode_attention_timing(cbis, st, max(10, args.steps))
+    att_gbs = att_bytes / att_ms / 1e6
+    _log(f"decode attention (1 layer): {att_ms:.4f} ms, {att_bytes / 1e9:.3f} GB -> {att_gbs:.0f} GB/s")
+    gem, gflops, gms = gemm_timing(cbis, st, max(10, args.steps))
+    gemm_tflops = gflops / gms / 1e9
+    _log(f"gemms: {json.dumps(gem)}; step total {gemm_tflops:.0f} TFLOP/s")
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_c4(oracle, st, cbis)
+        _log(f"cpu baseline: {cpu}")
+    return {
+        "metric": "decode tokens/s (config 4 mixed continuous-batch step, mid-size GPT)",
+        "value": round(value, 2),
+        "unit": "decode tokens/s",
+        "ms_per_step": round(ms_step, 4),
+        "dtype": "bf16",
+        "data": "synthetic (seeded weights N(0,0.02); K/V cache N(0,1); random token ids)",
+        "config": {"workload": "c4_mixed_step", "model": "gpt-mid L16 d2048 h64x32 mlp8192 V32000",
+                   "decode_rows": 192, "decode_kv_len": "U[256,4096]", "prefill_chunks": "2x512 (pos 0, 512)",
+                   "rows_per_step": 1216, "page_size": 16, "page_table": "shuffled", "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "paged_decode_kernel<bf16> + split merge, one layer",
+                     "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": att_bytes, "ms": round(att_ms, 4)},
+        "gemm_roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": BF16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4), "shapes": gem},
+        "cpu_baseline": cpu,
+    }
+
+
+def run_copy_calib(args):
+    """A plain device-to-device copy of known size for PMC byte calibration."""
+    import torch
+    n = 1 << 28  # 1 GiB of fp32
+    a = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"metric": "copy calibration", "value": float(n * 4), "unit": "bytes read per launch"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c4", choices=["c4"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calib", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box here has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calib:
+        print(json.dumps(run_copy_calib(args)))
+        return
+    cbis = _cbis()
+    import oracle
+    res = run_c4(args, cbis, oracle)
+    line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": res["dtype"], "data": res["data"], "config": res["config"],
+            "roofline": res["roofline"], "gemm_roofline": res["gemm_roofline"], "cpu_baseline": res["cpu_baseline"]}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

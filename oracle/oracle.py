@@ -110,8 +110,10 @@ def _i32(a):
 # --------------------------------------------------------------------------
 
 def normal(seed: int, stream: int, n: int, std: float = 1.0, start: int = 0) -> np.ndarray:
+    """std is an fp32 value (the product's C-ABI takes it as float); the
+    variate is scaled by it in fp64 and rounded once to fp32."""
     out = np.empty(n, dtype=np.float32)
-    lib().orc_normal_f32(seed, stream, start, n, std, _ptr(out))
+    lib().orc_normal_f32(seed, stream, start, n, float(np.float32(std)), _ptr(out))
     return out
 
 

@@ -259,8 +259,9 @@ def test_embed(cbis, oracle, dev, edt):
     else:
         (TE, tev), (PE, pev) = bf16_dev(te, dev), bf16_dev(pe, dev)
     out = torch.empty((M, D), dtype=torch.float32, device=dev)
-    cbis.check(cbis.kernels().cbis_embed(M, D, ptr(to_dev(tok, dev)), ptr(to_dev(pos, dev)), cbis.DTYPES[edt],
-                                         ptr(TE), ptr(PE), V, S, ptr(out), stream()))
+    TOK, POS = to_dev(tok, dev), to_dev(pos, dev)  # keep the device copies alive until the launch completes
+    cbis.check(cbis.kernels().cbis_embed(M, D, ptr(TOK), ptr(POS), cbis.DTYPES[edt], ptr(TE), ptr(PE), V, S,
+                                         ptr(out), stream()))
     sync()
     ref = tev[tok].astype(np.float64) + pev[pos]
     assert np.array_equal(out.cpu().numpy(), ref.astype(np.float32))
@@ -290,16 +291,19 @@ def test_reference_signature_elementwise(cbis, oracle, dev):
     tok = oracle.uniform_int(19, 3, T, 0, V - 1)
     pos = np.arange(T, dtype=np.int32)
     x = torch.empty((T, D), dtype=torch.float32, device=dev)
-    cbis.check(K.cbis_embed_lookup_add(ptr(to_dev(tok, dev)), ptr(to_dev(pos, dev)), ptr(to_dev(te, dev)),
-                                       ptr(to_dev(pe, dev)), ptr(x), T, D, stream()))
+    # device copies are bound to names so they outlive the asynchronous launches
+    TOK, POS, TE, PE = to_dev(tok, dev), to_dev(pos, dev), to_dev(te, dev), to_dev(pe, dev)
+    cbis.check(K.cbis_embed_lookup_add(ptr(TOK), ptr(POS), ptr(TE), ptr(PE), ptr(x), T, D, stream()))
     g = (1 + oracle.normal(19, 4, D, 0.1)).astype(np.float32)
     b = oracle.normal(19, 5, D, 0.1)
     y = torch.empty_like(x)
-    cbis.check(K.cbis_layernorm_forward(ptr(x), ptr(to_dev(g, dev)), ptr(to_dev(b, dev)), ptr(y), T, D, stream()))
+    G, B = to_dev(g, dev), to_dev(b, dev)
+    cbis.check(K.cbis_layernorm_forward(ptr(x), ptr(G), ptr(B), ptr(y), T, D, stream()))
     w = oracle.normal(19, 6, 1024 * D, 0.02).reshape(1024, D)
     bb = oracle.normal(19, 7, 1024, 0.02)
     h = torch.empty((T, 1024), dtype=torch.float32, device=dev)
-    cbis.check(K.cbis_linear_forward(ptr(y), ptr(to_dev(w, dev)), ptr(to_dev(bb, dev)), ptr(h), T, D, 1024, stream()))
+    W, BB = to_dev(w, dev), to_dev(bb, dev)
+    cbis.check(K.cbis_linear_forward(ptr(y), ptr(W), ptr(BB), ptr(h), T, D, 1024, stream()))
     cbis.check(K.cbis_gelu_forward(ptr(h), T, 1024, stream()))
     r = torch.ones((T, 1024), dtype=torch.float32, device=dev)
     cbis.check(K.cbis_residual_add(ptr(r), ptr(h), T, 1024, stream()))
