@@ -99,7 +99,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
   const int t0 = split * a.split_tokens;
   if (kv_len <= 0 || t0 >= kv_len) return;
   const int t1 = min(kv_len, t0 + a.split_tokens);
-  const int nsplit_row = (kv_len + a.split_tokens - 1) / a.split_tokens;
+  // A row whose kv_len exceeds the host's max_kv_len bound keeps its first
+  // n_splits splits (the grid and workspace cover no more).
+  const int nsplit_row = min((kv_len + a.split_tokens - 1) / a.split_tokens, a.n_splits);
   const int* bt = a.bt + (int64_t)(a.row_bt ? a.row_bt[row] : row) * a.bt_stride;
 
   const int head = hb * HPB + lane / G;
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArg
   const int row = a.rows ? a.rows[ridx] : ridx;
   const int kv_len = min(a.row_pos[row] + 1, a.max_kv);
   if (kv_len <= 0) return;
-  const int ns = (kv_len + a.split_tokens - 1) / a.split_tokens;
+  const int ns = min((kv_len + a.split_tokens - 1) / a.split_tokens, a.n_splits);
   if (ns <= 1) return;
   const float* w = a.ws + ((int64_t)ridx * a.n_splits * a.n_heads + head) * kWS;
   const int64_t sstride = (int64_t)a.n_heads * kWS;
