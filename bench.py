@@ -227,6 +227,21 @@ def cpu_baseline_c4(oracle, st, cbis):
                       f" + lm_head ({t_head:.1f}s), scaled to 16 layers; step {t_step:.1f}s"}
 
 
+def recorded_traffic(name):
+    """HBM bytes per launch of the dominant kernel, as recorded from the two
+    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE, copy-calibrated) in
+    profiles/<name>; None when no such record exists."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def run_c4(args, cbis, oracle):
     st = c4_setup(cbis, oracle)
     runner = st["runner"]
@@ -265,7 +280,8 @@ def run_c4(args, cbis, oracle):
                    "rows_per_step": 1216, "page_size": 16, "page_table": "shuffled", "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": "paged_decode_kernel<bf16> + split merge, one layer",
                      "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(att_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": recorded_traffic("paged_decode_c4_hbm_traffic.md"),
                      "algorithmic_bytes": att_bytes, "ms": round(att_ms, 4)},
         "gemm_roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": BF16_PEAK_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4), "shapes": gem},

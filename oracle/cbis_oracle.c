@@ -30,7 +30,7 @@
  * e4m3 codecs are this build's own specification, restated independently of
  * the product so tests can compare the two bit for bit.
  *
- * Pins (what checks this file; see tests/test_oracle.py):
+ * Pins (what checks this file; tests/test_cpu_oracle.py):
  *   - end-to-end logits against golden vectors written by importing the
  *     reference's python/model.py (tests/golden/gen_golden.py);
  *   - GEMM against numpy matmul and exact small-integer products;
