@@ -171,6 +171,9 @@ def gemm_timing(cbis, st, iters):
         d.x_dtype, d.X, d.ldx = cbis.BF16, X.data_ptr(), K
         d.w_dtype, d.W, d.ldw = cbis.BF16, w.tensor(wname), K
         d.y_dtype, d.Y, d.ldy = cbis.F32, Y.data_ptr(), N
+        need = cbis.kernels().cbis_gemm_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+        d.workspace, d.workspace_bytes = ws.data_ptr(), need
         fn = lambda d=d: cbis.check(cbis.kernels().cbis_gemm(ctypes.byref(d), stream))
         ev.time(fn, 2)
         ms = ev.time(fn, iters)
@@ -179,7 +182,7 @@ def gemm_timing(cbis, st, iters):
         mult = 1 if name == "lm_head" else st["cfg"].n_layers
         tot_flops += fl * mult
         tot_ms += ms * mult
-        res[name] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 1)}
+        res[name] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 1), "split_k_workspace": need}
     return res, tot_flops, tot_ms
 
 

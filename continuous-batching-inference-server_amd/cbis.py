@@ -42,7 +42,8 @@ class GemmDesc(ctypes.Structure):
                 ("residual", _P), ("ldr", _I64),
                 ("y_dtype", _I), ("Y", _P), ("ldy", _I64),
                 ("kv_col0", _I), ("kv_width", _I), ("kv_dtype", _I), ("page_size", _I),
-                ("k_pool", _P), ("v_pool", _P), ("write_page", _P), ("write_offset", _P)]
+                ("k_pool", _P), ("v_pool", _P), ("write_page", _P), ("write_offset", _P),
+                ("workspace", _P), ("workspace_bytes", _SZ)]
 
 
 class AttnDesc(ctypes.Structure):
@@ -77,6 +78,7 @@ KERNEL_SYMBOLS = {
     "cbis_scatter_kv_to_cache": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "cbis_fused_paged_causal_attention": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "cbis_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
+    "cbis_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "cbis_paged_attention_workspace_size": (_SZ, [ctypes.POINTER(AttnDesc)]),
     "cbis_paged_attention": (_I, [ctypes.POINTER(AttnDesc), _P]),
     "cbis_paged_prefill_attention": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),

@@ -10,8 +10,8 @@
 //
 // Tiling.  Both operands are K-contiguous, so A (X) and B (W) tiles are
 // staged the same way: rows of 128 bytes of K (64 bf16 / 32 fp32) in LDS,
-// with the 16-byte chunk index XOR-swizzled by (row & 7) so the
-// ds_read_b128 fragment loads of 8 consecutive rows hit distinct banks.
+// with the 16-byte chunk index XOR-swizzled by ((row >> 1) & 7) so the
+// ds_read_b128 fragment loads of 16 consecutive rows hit distinct banks.
 // Two LDS buffers; the next K tile is fetched into registers while the
 // current one feeds the MFMAs (one barrier per K step).  Each wave owns a
 // (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks:
@@ -107,7 +107,13 @@ struct WLoad<uint8_t> {
   }
 };
 
-__device__ inline int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+// LDS image of a 128-byte tile row: 16-byte chunk c of row r sits in slot
+// c ^ ((r >> 1) & 7).  gfx950 serves a ds_read_b128 16 lanes (256 bytes, all
+// 64 banks) per cycle; the 16 lanes of a fragment load read one chunk of 16
+// consecutive rows, i.e. 8 even rows in bytes 0-127 and 8 odd rows in bytes
+// 128-255 of the 64 banks, each set in 8 distinct slots: no bank conflicts.
+__device__ inline int swz_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+__device__ inline int swz(int row, int chunk) { return row * 128 + (swz_slot(row, chunk) << 4); }
 
 template <int BM, int BN, int WM, int WN, typename XT, typename WT>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
@@ -261,6 +267,227 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs g) {
   epilogue_store(g, (int)(idx / g.N), (int)(idx % g.N), v);
 }
 
+// ---------------------------------------------------------------------------
+// bf16 x bf16 on a multi-stage LDS ring fed by direct-to-LDS loads.
+//
+// Each global_load_lds_dwordx4 moves 16 bytes per lane straight from global
+// memory into LDS at M0 + 16 * lane (no VGPRs, no ds_write): one wave
+// instruction fills 1 KiB = eight 128-byte tile rows.  The chunk swizzle
+// (swz_slot) is applied on the global side -- lane i of an instruction
+// covering rows 8g..8g+7 fetches the chunk that belongs in slot i & 7 of row
+// 8g + (i >> 3) -- so the LDS image is the swizzled layout the ds_read_b128
+// fragment loads expect.
+//
+// STAGES K tiles are in flight: iteration kt waits (s_waitcnt vmcnt) for its
+// own tile only, then one barrier, then issues the loads of tile
+// kt + STAGES - 1 into the slot that iteration kt - 1 finished reading.
+// The loads are issued with inline assembly and waited for explicitly: the
+// compiler's own tracking of LDS DMA either waits for every load in flight
+// (with a fenced barrier) or misses the wait (with a bare one).  No other
+// vector-memory instruction is issued inside the main loop, so the vmcnt
+// immediates count exactly the DMA loads of the younger tiles.
+// ---------------------------------------------------------------------------
+__device__ inline void lds_dma16(const void* gptr, uint32_t lds_addr) {
+  // M0 is reserved by the compiler (it never keeps a value there across
+  // ordinary code), so it is set right before the load that reads it.
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory");
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmArgs g) {
+  constexpr int NWAVES = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int ROWS = BM + BN;                 // tile rows per stage (A then B)
+  constexpr int GROUPS = ROWS / 8;              // 1 KiB DMA instructions per stage
+  constexpr int LPW = GROUPS / NWAVES;          // per wave
+  constexpr int STAGE_BYTES = ROWS * 128;
+  static_assert(LPW * NWAVES == GROUPS && BM % 8 == 0 && BN % 8 == 0, "tile / wave mismatch");
+  static_assert(LPW * (STAGES - 1) < 64, "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
+
+  const int mt = (g.M + BM - 1) / BM;
+  const int nwg = gridDim.x;
+  int bid = blockIdx.x;
+  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  const int tm = bid % mt, tn = bid / mt;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kz = blockIdx.z;
+  const int kbeg = kz * g.k_per;
+  const int KT = min(g.k_per, g.K - kbeg) / 64;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int half = lane >> 5, l32 = lane & 31;
+
+  // Per-lane source pointers of this wave's DMA instructions (k tile 0).
+  const uint16_t* src[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int grp = wave * LPW + j;
+    const int rr = grp * 8 + (lane >> 3);
+    const int chunk = swz_slot(rr, lane & 7);  // the chunk that belongs in slot lane & 7 of row rr
+    if (rr < BM) {
+      const int r = min(m0 + rr, g.M - 1);
+      src[j] = (const uint16_t*)g.X + (int64_t)r * g.ldx + kbeg + chunk * 8;
+    } else {
+      const int r = min(n0 + rr - BM, g.N - 1);
+      src[j] = (const uint16_t*)g.W + (int64_t)r * g.ldw + kbeg + chunk * 8;
+    }
+  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds0 + wave * LPW * 1024);
+
+  auto issue = [&](int kt) {
+    const uint32_t base = wave_lds + (uint32_t)((kt % STAGES) * STAGE_BYTES);
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) lds_dma16(src[j] + kt * 64, base + j * 1024);
+  };
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragment byte offsets inside a stage: swz(row, kc); every fragment row
+  // this lane reads is l32 plus a multiple of 32, so its swizzle key is l32's.
+  const int a_row0 = (wm * TM + l32) * 128;
+  const int b_row0 = (BM + wn * TN + l32) * 128;
+  const int sw = (l32 >> 1) & 7;
+  bf16x8_t af[2][FM], bf[2][FN];
+  auto load_frags = [&](int slot, int ks, int fb) {
+    const uint8_t* st = smem + slot * STAGE_BYTES;
+    const int kc = ((2 * ks + half) ^ sw) << 4;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[fb][i] = *(const bf16x8_t*)(st + a_row0 + i * 32 * 128 + kc);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[fb][j] = *(const bf16x8_t*)(st + b_row0 + j * 32 * 128 + kc);
+  };
+  // Waits until k tile t has landed in LDS for every wave: at most
+  // (last - t) * LPW of this wave's DMA loads may remain (tiles t+1..last are
+  // the younger ones in flight), then a barrier.  The lgkmcnt wait makes
+  // every wave's earlier ds_reads complete before any wave refills the slot
+  // they read.
+  auto await_tile = [&](int t, int last) {
+    const int younger = last - t;
+    if constexpr (STAGES >= 4) {
+      if (younger >= 3) wait_vmcnt<3 * LPW>();
+      else if (younger == 2) wait_vmcnt<2 * LPW>();
+      else if (younger == 1) wait_vmcnt<LPW>();
+      else wait_vmcnt<0>();
+    } else {
+      if (younger >= 2) wait_vmcnt<2 * LPW>();
+      else if (younger == 1) wait_vmcnt<LPW>();
+      else wait_vmcnt<0>();
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+  };
+
+  // Tiles 0..STAGES-1 in flight, one per slot.
+#pragma unroll
+  for (int t = 0; t < STAGES; ++t)
+    if (t < KT) issue(t);
+  await_tile(0, min(KT - 1, STAGES - 1));
+  load_frags(0, 0, 0);
+
+  // The fragments of sub-step ks+1 are read while sub-step ks's MFMAs run;
+  // across a tile boundary the barrier sits between the last sub-step's
+  // fragment reads and its MFMAs, and the freed slot is refilled with tile
+  // kt + STAGES right after it.
+  for (int kt = 0; kt < KT; ++kt) {
+    const int slot = kt % STAGES;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int fb = ks & 1;
+      if (ks < 3) {
+        load_frags(slot, ks + 1, fb ^ 1);
+      } else if (kt + 1 < KT) {
+        await_tile(kt + 1, min(KT - 1, kt + STAGES - 1));
+        if (kt + STAGES < KT) issue(kt + STAGES);
+        load_frags((kt + 1) % STAGES, 0, fb ^ 1);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fb][i], bf[fb][j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + wn * TN + j * 32 + l32;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+        if (col < g.N && row < g.M) {
+          if (g.ksplit > 1) g.partial[((int64_t)kz * g.M + row) * g.N + col] = acc[i][j][e];
+          else epilogue_store(g, row, col, acc[i][j][e]);
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+int launch_dma(const GemmArgs& g, hipStream_t s) {
+  const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
+  gemm_bf16_dma_kernel<BM, BN, WM, WN, STAGES><<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, 0, s>>>(g);
+  int rc = check_launch("cbis_gemm(bf16)");
+  if (rc || g.ksplit <= 1) return rc;
+  splitk_reduce_kernel<<<(unsigned)cdiv((int64_t)g.M * g.N, 256), 256, 0, s>>>(g);
+  return check_launch("cbis_gemm(split-k reduce)");
+}
+
+// Tile of the bf16 direct-to-LDS path and its split-K plan.  The tile is
+// 128 x 128 on 8 waves (2 x 4, each 64 x 32) with a 2-stage 64 KiB ring, so
+// two workgroups share a CU.  When the output tiles cannot occupy the 256 CUs
+// and K is long enough, K is split so about 2 workgroups per CU run; each
+// split keeps at least 16 K tiles (shorter splits lose more to the partial
+// round trip than they gain in occupancy).
+constexpr int kDmaBM = 128, kDmaBN = 128;
+constexpr int kCUs = 256;
+
+struct SplitPlan {
+  int ksplit = 1;
+  int k_per = 0;
+};
+
+SplitPlan plan_dma_split(int M, int N, int K) {
+  SplitPlan p;
+  p.k_per = K;
+  const int64_t tiles = cdiv(M, kDmaBM) * cdiv(N, kDmaBN);
+  const int kt = K / 64;
+  if (tiles >= kCUs || kt < 16) return p;
+  int ks = (int)std::max<int64_t>(2, std::min<int64_t>(4, (2 * kCUs) / tiles));
+  ks = std::min(ks, kt / 16);
+  if (ks <= 1) return p;
+  const int per = (kt + ks - 1) / ks;
+  p.ksplit = (kt + per - 1) / per;
+  p.k_per = per * 64;
+  return p;
+}
+
+bool dma_eligible(const cbis_gemm_desc* d) {
+  return d->x_dtype == CBIS_BF16 && d->w_dtype == CBIS_BF16 && ((uintptr_t)d->W & 15u) == 0 &&
+         (d->ldw * 2) % 16 == 0;
+}
+
 template <int BM, int BN, int WM, int WN, typename XT, typename WT>
 int launch(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
@@ -301,9 +528,6 @@ using namespace cbis;
 
 extern "C" {
 
-// Bytes of split-K workspace cbis_gemm would use for this problem if given;
-// 0 when it runs without split-K.  (Exposed for callers that want to give a
-// workspace; cbis_gemm runs without one.)
 int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
   CBIS_REQUIRE(d, CBIS_ERR_INVALID, "cbis_gemm: null descriptor");
   CBIS_REQUIRE(d->M >= 0 && d->N > 0 && d->K > 0, CBIS_ERR_INVALID, "cbis_gemm: bad M/N/K %d/%d/%d", d->M, d->N, d->K);
@@ -353,8 +577,27 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
 
   hipStream_t s = (hipStream_t)stream;
   if (f32) return dispatch<float, float>(g, s);
-  if (d->w_dtype == CBIS_BF16) return dispatch<uint16_t, uint16_t>(g, s);
+  if (d->w_dtype == CBIS_BF16) {
+    // The direct-to-LDS path needs 16-byte aligned rows of both operands.
+    if (dma_eligible(d)) {
+      const SplitPlan p = plan_dma_split(d->M, d->N, d->K);
+      const size_t need = (size_t)p.ksplit * d->M * d->N * sizeof(float);
+      if (p.ksplit > 1 && d->workspace && d->workspace_bytes >= need) {
+        g.ksplit = p.ksplit;
+        g.k_per = p.k_per;
+        g.partial = (float*)d->workspace;
+      }
+      return launch_dma<kDmaBM, kDmaBN, 2, 4, 2>(g, s);
+    }
+    return dispatch<uint16_t, uint16_t>(g, s);
+  }
   return dispatch<uint16_t, uint8_t>(g, s);
+}
+
+size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {
+  if (!d || d->M <= 0 || d->N <= 0 || d->K <= 0 || !dma_eligible(d) || d->K % 64) return 0;
+  const SplitPlan p = plan_dma_split(d->M, d->N, d->K);
+  return p.ksplit > 1 ? (size_t)p.ksplit * d->M * d->N * sizeof(float) : 0;
 }
 
 int cbis_linear_forward(const float* X, const float* W, const float* b, float* Y, int T, int in_features,

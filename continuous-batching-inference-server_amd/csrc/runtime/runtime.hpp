@@ -180,6 +180,8 @@ class TransformerRunner {
   int* d_next_ = nullptr;
   void* d_ws_ = nullptr;
   size_t ws_bytes_ = 0;
+  void* d_gemm_ws_ = nullptr;
+  size_t gemm_ws_bytes_ = 0;
 
   // current step
   int M_ = 0;

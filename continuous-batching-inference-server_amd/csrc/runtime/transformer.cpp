@@ -50,6 +50,19 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   // Split-KV partials: the automatic split keeps rows * splits <= 2048 + rows.
   ws_bytes_ = (2048 + R) * (size_t)cfg_.n_heads * (cfg_.head_dim + 4) * 4;
   hip_check(hipMalloc(&d_ws_, ws_bytes_), "hipMalloc attention workspace");
+  // Split-K workspace: the largest any of the step's GEMM shapes asks for at
+  // any row count up to max_total_rows.
+  const int shapes[5][2] = {{3 * (int)D, (int)D}, {(int)D, (int)D}, {(int)F, (int)D}, {(int)D, (int)F}, {(int)V, (int)D}};
+  cbis_gemm_desc q = {};
+  q.x_dtype = cfg_.act_dtype();
+  q.w_dtype = cfg_.weight_dtype;
+  q.W = w_.lm_head;  // any weight pointer of the arena: only its alignment is inspected
+  for (int m = 1; m <= max_total_rows; ++m)
+    for (const auto& sh : shapes) {
+      q.M = m; q.N = sh[0]; q.K = sh[1]; q.ldw = sh[1];
+      gemm_ws_bytes_ = std::max(gemm_ws_bytes_, cbis_gemm_workspace_size(&q));
+    }
+  if (gemm_ws_bytes_) hip_check(hipMalloc(&d_gemm_ws_, gemm_ws_bytes_), "hipMalloc gemm workspace");
 }
 
 TransformerRunner::~TransformerRunner() {
@@ -57,6 +70,7 @@ TransformerRunner::~TransformerRunner() {
   if (stream_) (void)hipStreamDestroy(stream_);
   (void)hipFree(d_x_); (void)hipFree(d_xn_); (void)hipFree(d_q_); (void)hipFree(d_attn_);
   (void)hipFree(d_h_); (void)hipFree(d_logits_); (void)hipFree(d_next_); (void)hipFree(d_ws_);
+  if (d_gemm_ws_) (void)hipFree(d_gemm_ws_);
   (void)hipFree(d_meta_);
   if (h_meta_) (void)hipHostFree(h_meta_);
 }
@@ -184,6 +198,7 @@ void TransformerRunner::enqueue_forward() {
     cbis_check(cbis_layernorm(M, D, d_x_, D, L.ln1_w, L.ln1_b, 1e-5f, act, d_xn_, D, s), "ln1");
     // QKV projection; K and V columns go straight to their page slots.
     g = cbis_gemm_desc{};
+    g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
     g.M = M; g.N = 3 * D; g.K = D;
     g.x_dtype = act; g.X = d_xn_; g.ldx = D;
     g.w_dtype = wd; g.W = L.wqkv; g.ldw = D; g.w_scale = L.sqkv;
@@ -203,6 +218,7 @@ void TransformerRunner::enqueue_forward() {
     if (n_tiles_ > 0) cbis_check(cbis_paged_prefill_attention(&a, n_tiles_, d_tiles_, s), "prefill attention");
     // out-projection + bias + residual, in place on x
     g = cbis_gemm_desc{};
+    g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
     g.M = M; g.N = D; g.K = D;
     g.x_dtype = act; g.X = d_attn_; g.ldx = D;
     g.w_dtype = wd; g.W = L.wo; g.ldw = D; g.w_scale = L.so;
@@ -211,6 +227,7 @@ void TransformerRunner::enqueue_forward() {
     cbis_check(cbis_gemm(&g, s), "out-proj gemm");
     cbis_check(cbis_layernorm(M, D, d_x_, D, L.ln2_w, L.ln2_b, 1e-5f, act, d_xn_, D, s), "ln2");
     g = cbis_gemm_desc{};
+    g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
     g.M = M; g.N = F; g.K = D;
     g.x_dtype = act; g.X = d_xn_; g.ldx = D;
     g.w_dtype = wd; g.W = L.w1; g.ldw = D; g.w_scale = L.s1;
@@ -218,6 +235,7 @@ void TransformerRunner::enqueue_forward() {
     g.y_dtype = act; g.Y = d_h_; g.ldy = F;
     cbis_check(cbis_gemm(&g, s), "fc1 gemm");
     g = cbis_gemm_desc{};
+    g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
     g.M = M; g.N = D; g.K = F;
     g.x_dtype = act; g.X = d_h_; g.ldx = F;
     g.w_dtype = wd; g.W = L.w2; g.ldw = F; g.w_scale = L.s2;
@@ -227,6 +245,7 @@ void TransformerRunner::enqueue_forward() {
   }
   cbis_check(cbis_layernorm(M, D, d_x_, D, w_.ln_f_w, w_.ln_f_b, 1e-5f, act, d_xn_, D, s), "ln_f");
   g = cbis_gemm_desc{};
+  g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
   g.M = M; g.N = V; g.K = D;
   g.x_dtype = act; g.X = d_xn_; g.ldx = D;
   g.w_dtype = wd; g.W = w_.lm_head; g.ldw = D; g.w_scale = w_.lm_scale;

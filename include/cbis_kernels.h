@@ -123,7 +123,16 @@ typedef struct cbis_gemm_desc {
   void* v_pool;
   const int* write_page;
   const int* write_offset;
+  /* Optional split-K workspace (fp32 partials).  With enough of it the
+   * library splits K for problems whose output tiles alone cannot fill the
+   * GPU; NULL / too small runs without splitting. */
+  void* workspace;
+  size_t workspace_bytes;
 } cbis_gemm_desc;
+
+/* Bytes of workspace that let cbis_gemm use its preferred split-K for this
+ * descriptor (0 when it does not split). */
+size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d);
 
 int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream);
 

@@ -18,7 +18,7 @@ LOWP_TOL = 2e-2
 
 
 def _gemm(cbis, M, N, K, X, x_dtype, W, w_dtype, Y, y_dtype, bias=None, w_scale=None, gelu=False, residual=None,
-          kv=None):
+          kv=None, workspace=False):
     d = cbis.GemmDesc()
     d.M, d.N, d.K = M, N, K
     d.x_dtype, d.X, d.ldx = x_dtype, ptr(X), K
@@ -32,8 +32,15 @@ def _gemm(cbis, M, N, K, X, x_dtype, W, w_dtype, Y, y_dtype, bias=None, w_scale=
         d.kv_col0, d.kv_width, d.kv_dtype, d.page_size = kv["col0"], kv["width"], kv["dtype"], 16
         d.k_pool, d.v_pool = ptr(kv["k"]), ptr(kv["v"])
         d.write_page, d.write_offset = ptr(kv["wpage"]), ptr(kv["woff"])
+    ws = None
+    if workspace:
+        import torch
+        need = cbis.kernels().cbis_gemm_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=Y.device)
+        d.workspace, d.workspace_bytes = ptr(ws), need
     cbis.check(cbis.kernels().cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
     sync()
+    return d.workspace_bytes
 
 
 # --------------------------------------------------------------------------
@@ -149,6 +156,28 @@ def test_gemm_bf16_c4_shapes(cbis, oracle, dev, N, K):
     rows = _sample_rows(M, 24, N)
     rows[-1] = M - 1  # include the ragged last M tile
     ref = oracle.gemm(x[rows], w)
+    assert np.abs(Y.cpu().numpy()[rows] - ref).max() < FP32_TOL * 4
+
+
+@pytest.mark.parametrize("M", [192, 1216])
+@pytest.mark.parametrize("N,K,gelu", [(2048, 2048, False), (2048, 8192, False), (1024, 4096, True)])
+def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
+    """Split-K (fp32 partials in a caller workspace, reduce + epilogue) on the
+    shapes whose output tiles cannot fill the GPU: bias, GELU, and a residual
+    that aliases Y, against the fp64 oracle; the split must engage."""
+    import torch
+    X, x = bf16_dev(oracle.normal(15, 1, M * K).reshape(M, K), dev)
+    W, w = bf16_dev(oracle.normal(15, 2, N * K, 0.02).reshape(N, K), dev)
+    b = oracle.normal(15, 3, N, 0.02)
+    r = None if gelu else oracle.normal(15, 4, M * N).reshape(M, N)
+    B = to_dev(b, dev)
+    Y = to_dev(r, dev) if r is not None else torch.empty((M, N), dtype=torch.float32, device=dev)
+    used = _gemm(cbis, M, N, K, X, cbis.BF16, W, cbis.BF16, Y, cbis.F32, bias=B, gelu=gelu,
+                 residual=Y if r is not None else None, workspace=True)
+    assert used > 0
+    rows = _sample_rows(M, 48, N + K)
+    rows[-1] = M - 1
+    ref = oracle.gemm(x[rows], w, bias=b, gelu=gelu, residual=None if r is None else r[rows])
     assert np.abs(Y.cpu().numpy()[rows] - ref).max() < FP32_TOL * 4
 
 
