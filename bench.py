@@ -292,6 +292,79 @@ def run_c4(args, cbis, oracle):
     }
 
 
+def c3_inputs(oracle, n_seq=256, lo=128, hi=2048, pool=40000, seed=0):
+    """Config 3: kv_len U[lo, hi], one query per sequence at pos kv_len-1, a
+    random permutation of a pool of `pool` pages as the page table."""
+    kv = oracle.uniform_int(seed, 3001, n_seq, lo, hi)
+    npages = (kv + 15) // 16
+    perm = np.random.default_rng(seed).permutation(pool).astype(np.int32)
+    bt = np.zeros((n_seq, int(npages.max())), np.int32)
+    off = 0
+    for i in range(n_seq):
+        bt[i, : npages[i]] = perm[off: off + npages[i]]
+        off += npages[i]
+    return kv, bt
+
+
+def run_c3(args, cbis, oracle):
+    """Config 3: paged decode attention alone (fp32 K/V, 8x32 heads, 256
+    sequences, kv U[128, 2048], 40,000-page pool, permuted page table)."""
+    import torch
+    H, P = 8, 40000
+    kv, bt = c3_inputs(oracle)
+    n = kv.size
+    dev = torch.device("cuda:0")
+    K = cbis.kernels()
+    kp = torch.empty((P, 16, H, 32), dtype=torch.float32, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
+    for t, sd in ((kp, 1), (vp, 2), (q, 3)):
+        cbis.check(K.cbis_fill_normal_fast(t.data_ptr(), cbis.F32, t.numel(), sd, 1.0, None))
+    BT = torch.from_numpy(bt).to(dev)
+    POS = torch.from_numpy((kv - 1).astype(np.int32)).to(dev)
+    out = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
+    d = cbis.AttnDesc()
+    d.n_rows, d.n_heads, d.head_dim, d.page_size = n, H, 32, 16
+    d.q_dtype, d.q, d.ldq = cbis.F32, q.data_ptr(), H * 32
+    d.kv_dtype, d.k_pool, d.v_pool, d.num_pages = cbis.F32, kp.data_ptr(), vp.data_ptr(), P
+    d.block_table, d.bt_stride, d.row_pos = BT.data_ptr(), bt.shape[1], POS.data_ptr()
+    d.out_dtype, d.out, d.ldo = cbis.F32, out.data_ptr(), H * 32
+    d.max_kv_len = int(kv.max())
+    need = K.cbis_paged_attention_workspace_size(ctypes.byref(d))
+    ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+    d.workspace, d.workspace_bytes = ws.data_ptr(), need
+    torch.cuda.synchronize()
+    ev = Events(None)
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lambda: cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream))
+    ev.time(fn, args.warmup)
+    ms = ev.time(fn, args.steps)
+    alg = int(kv.sum()) * H * 32 * 4 * 2 + int(((kv + 15) // 16).sum()) * 4 + 2 * n * H * 32 * 4
+    gbs = alg / ms / 1e6
+    _log(f"c3 decode attention: {ms:.4f} ms, {alg / 1e6:.1f} MB -> {gbs:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu:
+        qh, kh, vh = q.cpu().numpy(), kp.cpu().numpy(), vp.cpu().numpy()
+        t0 = time.time()
+        reps = 0
+        while time.time() - t0 < 10.0:
+            oracle.paged_attention(qh, kh, vh, bt, kv - 1, H, 32, 16)
+            reps += 1
+        cpu_ms = (time.time() - t0) * 1000.0 / reps
+        cpu = {"value": round(alg / cpu_ms / 1e6, 2), "unit": "GB/s", "cores": oracle.lib().orc_num_threads(),
+               "kind": "port", "sample": f"oracle fp64 paged attention over the full config-3 call, {reps} reps "
+                                          f"({cpu_ms:.1f} ms each)"}
+    return {"metric": "paged decode attention HBM GB/s (config 3)", "value": round(gbs, 1), "unit": "GB/s",
+            "ms_per_step": round(ms, 4), "dtype": "f32",
+            "data": "synthetic (Q/K/V N(0,1); permuted page table)",
+            "config": {"workload": "c3_paged_decode_attention", "rows": n, "heads": "8x32", "kv_len": "U[128,2048]",
+                       "pool_pages": P, "page_size": 16},
+            "roofline": {"bound": "hbm", "kernel": "paged_decode_kernel<f32> + split merge", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": alg, "ms": round(ms, 4)},
+            "cpu_baseline": cpu}
+
+
 def run_copy_calib(args):
     """A plain device-to-device copy of known size for PMC byte calibration."""
     import torch
@@ -309,7 +382,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c4", choices=["c4"])
+    ap.add_argument("--config", default="c4", choices=["c4", "c3"],
+                    help="c4: the bench line (default); c3: paged decode attention alone")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
@@ -324,6 +398,14 @@ def main():
         return
     cbis = _cbis()
     import oracle
+    if args.config == "c3":
+        res = run_c3(args, cbis, oracle)
+        line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
+                "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"], "data": res["data"],
+                "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
+        print(json.dumps(line), flush=True)
+        return
     res = run_c4(args, cbis, oracle)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",

@@ -200,7 +200,13 @@ class PagedKVCache:
             runtime().cbis_cache_destroy(self._h)
             self._h = None
 
-    __del__ = close
+    def __del__(self):
+        # At interpreter exit the module globals may already be gone; the
+        # process teardown releases the device memory then.
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def allocate_sequence(self) -> int:
         return _rt_check(runtime().cbis_cache_allocate_sequence(self._h), "allocate_sequence")
@@ -273,7 +279,13 @@ class ModelWeights:
             runtime().cbis_weights_destroy(self._h)
             self._h = None
 
-    __del__ = close
+    def __del__(self):
+        # At interpreter exit the module globals may already be gone; the
+        # process teardown releases the device memory then.
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class TransformerRunner:
@@ -289,7 +301,13 @@ class TransformerRunner:
             runtime().cbis_runner_destroy(self._h)
             self._h = None
 
-    __del__ = close
+    def __del__(self):
+        # At interpreter exit the module globals may already be gone; the
+        # process teardown releases the device memory then.
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def forward_step(self, token_ids, positions, seq_ids):
         """Returns [rows, vocab] fp32 logits as a flat list-backed ctypes array -> numpy via caller."""
