@@ -365,6 +365,103 @@ def run_c3(args, cbis, oracle):
             "cpu_baseline": cpu}
 
 
+def run_c1(args, cbis, oracle):
+    """Config 1: tiny fp32 GPT (V=512, d=256, 8x32, L=4, MLP 1024), 8 prompts
+    U[16,64], 32 greedy tokens each through the C++ continuous-batching
+    scheduler (1 prefill step + 31 decode steps of 8 rows).  value = decode
+    tokens / decode-step wall time (median of `steps` runs)."""
+    reqs = oracle.c1_requests()
+    cfg = cbis.ModelConfig.make(vocab=512, n_layers=4)
+    w = cbis.ModelWeights.synthetic(cfg, seed=0)
+    cache = cbis.PagedKVCache(4, 128, 16, 8, 32, "f32")
+    runner = cbis.TransformerRunner(w, cache, 512)
+    prompts = [r.prompt for r in reqs]
+    dl = [r.decode_len for r in reqs]
+    for _ in range(max(1, args.warmup)):
+        cbis.run_continuous(runner, cache, prompts, dl)
+    dec, tot, toks = [], [], None
+    for _ in range(args.steps):
+        toks, ms = cbis.run_continuous(runner, cache, prompts, dl)
+        dec.append(sum(ms[1:]))
+        tot.append(sum(ms))
+    n_dec = sum(d - 1 for d in dl)
+    n_prompt = sum(len(p) for p in prompts)
+    dec_ms, tot_ms = float(np.median(dec)), float(np.median(tot))
+    value = n_dec / dec_ms * 1000.0
+    _log(f"c1: decode {dec_ms:.3f} ms for {n_dec} tokens -> {value:.0f} tok/s; whole run {tot_ms:.3f} ms "
+         f"({(n_prompt + sum(dl)) / tot_ms * 1000.0:.0f} prompt+generated tok/s)")
+    cpu = None
+    if not args.no_cpu:
+        spec = oracle.ModelSpec(vocab=512, n_layers=4, max_seq=128)
+        om = oracle.OracleModel(oracle.synthetic_weights(spec, seed=0, pos_rows=128), max_pages=128)
+        t0 = time.time()
+        gen, _ = oracle.run_continuous(om, oracle.PagedKVCacheOracle(128), reqs)
+        cpu_s = time.time() - t0
+        assert gen == toks, "CPU oracle and GPU greedy tokens differ"
+        cpu = {"value": round((n_prompt + sum(dl)) / cpu_s, 2), "unit": "prompt+generated tok/s",
+               "cores": oracle.lib().orc_num_threads(), "kind": "port",
+               "sample": f"oracle fp64 run_continuous of the whole config-1 workload ({cpu_s:.1f} s); "
+                         f"greedy tokens identical to the GPU run"}
+    return {"metric": "decode tokens/s (config 1 tiny GPT continuous batching)", "value": round(value, 1),
+            "unit": "decode tokens/s", "ms_per_step": round(dec_ms / (len(dl) and 31), 4), "dtype": "f32",
+            "data": "synthetic (seeded weights N(0,0.02); prompt ids U[0,511])",
+            "config": {"workload": "c1_tiny_gpt_greedy", "requests": len(dl), "prompt_len": "U[16,64]",
+                       "decode_len": 32, "whole_run_ms": round(tot_ms, 3)},
+            "cpu_baseline": cpu}
+
+
+def run_c5(args, cbis, oracle):
+    """Config 5: the mid-size GPT with fp8-e4m3 linear weights (per-channel
+    fp32 scales) and a bf16 paged K/V cache; 16 sequences whose caches hold
+    32704 synthetic tokens greedy-decode 64 tokens each at positions
+    32704..32767 (the last one is kMaxSeqLen - 1).  A step is 16 rows;
+    value = 16 * 64 / wall time of the 64 steps (median over `steps` runs)."""
+    import torch
+    n_seq, ctx, gen = 16, 32768 - 64, 64
+    cfg = cbis.ModelConfig.make(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=16, mlp=8192,
+                                max_seq=32768, weight_dtype="fp8", kv_dtype="bf16")
+    pages = n_seq * 2048 + 64
+    t0 = time.time()
+    w = cbis.ModelWeights.synthetic(cfg, seed=0)
+    cache = cbis.PagedKVCache(16, pages, 16, 64, 32, "bf16", pages_per_seq=2048)
+    cache.fill_normal(seed=5, std=1.0)
+    shuffled_cache(cbis, cache, pages, 5)
+    runner = cbis.TransformerRunner(w, cache, 64)
+    seqs = []
+    for _ in range(n_seq):
+        sid = cache.allocate_sequence()
+        assert cache.ensure_capacity(sid, 32767)
+        seqs.append(sid)
+    _log(f"c5 setup {time.time() - t0:.1f}s: weights {w.device_bytes() / 1e9:.2f} GB, "
+         f"kv {pages} pages x 16 layers ({cache.max_pages() * 16 * 2048 * 2 * 2 * 16 / 1e9:.1f} GB)")
+    first = [int(t) for t in oracle.uniform_int(0, 5003, n_seq, 0, 31999)]
+
+    def run():
+        toks = first
+        for i in range(gen):
+            toks = runner.forward_step_greedy(toks, [ctx + i] * n_seq, seqs)
+        return toks
+
+    for _ in range(max(1, args.warmup)):
+        run()
+    times = []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        run()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t1)
+    dt = float(np.median(times))
+    value = n_seq * gen / dt
+    _log(f"c5: {gen} steps in {dt * 1000:.2f} ms -> {value:.1f} tok/s ({dt * 1000 / gen:.3f} ms/step)")
+    return {"metric": "decode tokens/s (config 5 long-context fp8 decode)", "value": round(value, 2),
+            "unit": "decode tokens/s", "ms_per_step": round(dt * 1000 / gen, 4), "dtype": "bf16 x fp8-e4m3",
+            "data": "synthetic (fp8 weights absmax-quantised from N(0,0.02); K/V cache N(0,1))",
+            "config": {"workload": "c5_long_context_fp8_decode", "sequences": n_seq, "kv_len": "32704..32767",
+                       "decode_tokens": gen, "kv_cache_gb": round(16 * n_seq * 32768 * 2048 * 2 * 2 / 1e9, 1)},
+            "cpu_baseline": None}
+
+
 def run_copy_calib(args):
     """A plain device-to-device copy of known size for PMC byte calibration."""
     import torch
@@ -382,8 +479,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c4", choices=["c4", "c3"],
-                    help="c4: the bench line (default); c3: paged decode attention alone")
+    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c3", "c5"],
+                    help="c4: the bench line (default); c1 / c3 / c5: the other BASELINE configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
@@ -398,12 +495,12 @@ def main():
         return
     cbis = _cbis()
     import oracle
-    if args.config == "c3":
-        res = run_c3(args, cbis, oracle)
+    if args.config != "c4":
+        res = {"c1": run_c1, "c3": run_c3, "c5": run_c5}[args.config](args, cbis, oracle)
         line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
                 "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
                 "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"], "data": res["data"],
-                "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
+                "config": res["config"], "roofline": res.get("roofline"), "cpu_baseline": res["cpu_baseline"]}
         print(json.dumps(line), flush=True)
         return
     res = run_c4(args, cbis, oracle)

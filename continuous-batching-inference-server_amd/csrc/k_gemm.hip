@@ -24,6 +24,8 @@
 // workgroups sharing a W column block share one L2.
 // Optional split-K (gridDim.z) writes fp32 partials to a caller workspace
 // and a second kernel reduces them and applies the epilogue.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace cbis {
@@ -454,6 +456,149 @@ int launch_dma(const GemmArgs& g, hipStream_t s) {
   return check_launch("cbis_gemm(split-k reduce)");
 }
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM for M <= 64 rows (decode steps): weight-streaming on MFMA.
+//
+// A workgroup of 8 waves owns 16 output columns; the waves split K into 8
+// contiguous ranges and each streams its W slice straight into MFMA B
+// operands (no LDS staging: every W element is used by all M rows of one
+// MFMA), with the X fragments coming from L2.  The 8 partial 16-column
+// tiles are summed through LDS and wave 0 applies the epilogue.
+//   bf16 X:  v_mfma_f32_16x16x32_bf16, lane l holds 8 consecutive k of row
+//            (or W row) l % 16 at k offset 8 * (l / 16); fp8 W is widened
+//            to bf16 with v_cvt_scalef32_pk_bf16_fp8 (scale 1: exact, every
+//            e4m3 value is a bf16 value), the channel scale is applied in
+//            the epilogue;
+//   fp32 X:  v_mfma_f32_16x16x4_f32, lane l holds k = 4 * (l / 16) + e of a
+//            16-k block in element e of a float4, one MFMA per e.
+// C fragment: lane l holds rows 4 * (l / 16) + i, column l % 16.
+// ---------------------------------------------------------------------------
+template <typename WT>
+struct SkinnyW;
+template <>
+struct SkinnyW<uint16_t> {  // bf16: 8 elements = 16 bytes
+  __device__ static inline bf16x8_t load(const uint16_t* p) { return *(const bf16x8_t*)p; }
+};
+template <>
+struct SkinnyW<uint8_t> {  // fp8 e4m3: 8 elements = 8 bytes
+  __device__ static inline bf16x8_t load(const uint8_t* p) {
+    const uint2 r = *(const uint2*)p;
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.x, 1.0f, false);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.x, 1.0f, true);
+    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.y, 1.0f, false);
+    const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.y, 1.0f, true);
+    uint4 u;
+    u.x = __builtin_bit_cast(uint32_t, a);
+    u.y = __builtin_bit_cast(uint32_t, b);
+    u.z = __builtin_bit_cast(uint32_t, c);
+    u.w = __builtin_bit_cast(uint32_t, d);
+    return __builtin_bit_cast(bf16x8_t, u);
+  }
+};
+
+constexpr int kSkinnyWaves = 8;
+
+template <typename XT, typename WT, int MB>
+__global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const GemmArgs g) {
+  constexpr bool F32 = sizeof(XT) == 4;
+  constexpr int KB = F32 ? 16 : 32;  // k per MFMA step
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int n = min(n0 + c16, g.N - 1);
+  const int nkb = g.K / KB;
+  const int kb0 = (nkb * wave) / kSkinnyWaves, kb1 = (nkb * (wave + 1)) / kSkinnyWaves;
+
+  f32x4_t acc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  int xrow[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) xrow[i] = min(i * 16 + c16, g.M - 1);
+
+  if constexpr (F32) {
+    const float* wp = (const float*)g.W + (int64_t)n * g.ldw + 4 * q;
+    const float* xp[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) xp[i] = (const float*)g.X + (int64_t)xrow[i] * g.ldx + 4 * q;
+    // Four k blocks per round: all their loads are issued before the MFMAs.
+    auto step = [&](int kb, auto U) {
+      constexpr int NU = decltype(U)::value;
+      f32x4_t w[NU], x[NU][MB];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        w[u] = *(const f32x4_t*)(wp + (kb + u) * KB);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) x[u][i] = *(const f32x4_t*)(xp[i] + (kb + u) * KB);
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u][i][e], w[u][e], acc[i], 0, 0, 0);
+    };
+    int kb = kb0;
+    for (; kb + 4 <= kb1; kb += 4) step(kb, std::integral_constant<int, 4>());
+    for (; kb < kb1; ++kb) step(kb, std::integral_constant<int, 1>());
+  } else {
+    const WT* wp = (const WT*)g.W + (int64_t)n * g.ldw + 8 * q;
+    const uint16_t* xp[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) xp[i] = (const uint16_t*)g.X + (int64_t)xrow[i] * g.ldx + 8 * q;
+    auto step = [&](int kb, auto U) {
+      constexpr int NU = decltype(U)::value;
+      bf16x8_t w[NU], x[NU][MB];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        w[u] = SkinnyW<WT>::load(wp + (kb + u) * KB);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) x[u][i] = *(const bf16x8_t*)(xp[i] + (kb + u) * KB);
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int i = 0; i < MB; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[u][i], w[u], acc[i], 0, 0, 0);
+    };
+    int kb = kb0;
+    for (; kb + 4 <= kb1; kb += 4) step(kb, std::integral_constant<int, 4>());
+    for (; kb < kb1; ++kb) step(kb, std::integral_constant<int, 1>());
+  }
+
+  // Sum the 8 waves' partial tiles (fixed order: deterministic).
+  __shared__ f32x4_t part[kSkinnyWaves][MB][64];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) part[wave][i][lane] = acc[i];
+  __syncthreads();
+  if (wave != 0) return;
+  const int col = n0 + c16;
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    f32x4_t v = part[0][i][lane];
+#pragma unroll
+    for (int w = 1; w < kSkinnyWaves; ++w) v += part[w][i][lane];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = i * 16 + 4 * q + e;
+      if (row < g.M && col < g.N) epilogue_store(g, row, col, v[e]);
+    }
+  }
+}
+
+template <typename XT, typename WT>
+int launch_skinny(const GemmArgs& g, hipStream_t s) {
+  const unsigned grid = (unsigned)cdiv(g.N, 16);
+  if (g.M <= 16) gemm_skinny_kernel<XT, WT, 1><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
+  else if (g.M <= 32) gemm_skinny_kernel<XT, WT, 2><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
+  else gemm_skinny_kernel<XT, WT, 4><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
+  return check_launch("cbis_gemm(skinny)");
+}
+
+constexpr int kSkinnyMaxM = 64;
+
 // Tile of the bf16 direct-to-LDS path and its split-K plan.  The tile is
 // 128 x 128 on 8 waves (2 x 4, each 64 x 32) with a 2-stage 64 KiB ring, so
 // two workgroups share a CU.  When the output tiles cannot occupy the 256 CUs
@@ -576,6 +721,16 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
   g.partial = nullptr;
 
   hipStream_t s = (hipStream_t)stream;
+  // Decode-sized M: weight streaming (K a multiple of 32 for bf16 / fp8 --
+  // already required -- and of 16 for fp32, W rows 16-byte aligned for fp32
+  // and bf16, 8-byte for fp8).
+  const bool w_al = ((uintptr_t)d->W & (d->w_dtype == CBIS_FP8E4M3 ? 7u : 15u)) == 0 &&
+                    (d->ldw * we) % (d->w_dtype == CBIS_FP8E4M3 ? 8 : 16) == 0;
+  if (d->M <= kSkinnyMaxM && w_al && d->K % 32 == 0) {
+    if (f32) return launch_skinny<float, float>(g, s);
+    if (d->w_dtype == CBIS_BF16) return launch_skinny<uint16_t, uint16_t>(g, s);
+    return launch_skinny<uint16_t, uint8_t>(g, s);
+  }
   if (f32) return dispatch<float, float>(g, s);
   if (d->w_dtype == CBIS_BF16) {
     // The direct-to-LDS path needs 16-byte aligned rows of both operands.

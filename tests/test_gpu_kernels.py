@@ -197,6 +197,67 @@ def test_gemm_fp8_weights(cbis, oracle, dev, M):
     assert np.abs(Y.cpu().numpy() - ref).max() < FP32_TOL
 
 
+def test_gemm_fp8_decode_every_code(cbis, oracle, dev):
+    """Every OCP e4m3 code through the decode-sized (skinny) GEMM: row n of W
+    holds code n at k = 0 and zeros elsewhere, X = e_0, scale 1, so
+    Y[0, n] is the decoded code itself -- exactly the oracle's table value
+    (NaN codes 0x7F / 0xFF must decode to NaN)."""
+    import torch
+    N, K = 256, 64
+    codes = np.zeros((N, K), np.uint8)
+    codes[:, 0] = np.arange(256, dtype=np.uint8)
+    x = np.zeros((1, K), np.float32)
+    x[0, 0] = 1.0
+    X, _ = bf16_dev(x, dev)
+    C, S = to_dev(codes, dev), to_dev(np.ones(N, np.float32), dev)
+    Y = torch.empty((1, N), dtype=torch.float32, device=dev)
+    _gemm(cbis, 1, N, K, X, cbis.BF16, C, cbis.FP8E4M3, Y, cbis.F32, w_scale=S)
+    got = Y.cpu().numpy()[0]
+    ref = oracle.e4m3_table()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    # exact equality of every value (the accumulator turns 1 * -0 into +0,
+    # so code 0x80 compares equal to 0 rather than bit for bit)
+    bad = [hex(c) for c in range(256) if not nan[c] and got[c] != ref[c]]
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("M", [1, 8, 16, 33, 64])
+@pytest.mark.parametrize("wdt", ["f32", "bf16", "fp8"])
+def test_gemm_skinny_decode_rows(cbis, oracle, dev, M, wdt):
+    """Decode-sized M (weight-streaming kernel) for every weight dtype, with
+    bias + GELU and with bias + a residual aliasing Y, against the oracle."""
+    import torch
+    N, K = 1040, 1024  # N not a multiple of the 16-column tile
+    w = oracle.normal(16, 2, N * K, 0.02).reshape(N, K)
+    xf = oracle.normal(16, 1, M * K).reshape(M, K)
+    b = oracle.normal(16, 3, N, 0.02)
+    r = oracle.normal(16, 4, M * N).reshape(M, N)
+    sc = None
+    if wdt == "f32":
+        X, x = to_dev(xf, dev), xf
+        W, wq, xdt, wdt_c = to_dev(w, dev), w, cbis.F32, cbis.F32
+    else:
+        X, x = bf16_dev(xf, dev)
+        xdt = cbis.BF16
+        if wdt == "bf16":
+            W, wq = bf16_dev(w, dev)
+            wdt_c = cbis.BF16
+        else:
+            codes, sc = oracle.quantize_e4m3_rows(w)
+            W, wq, wdt_c = to_dev(codes, dev), oracle.e4m3_table()[codes], cbis.FP8E4M3
+    S = to_dev(sc, dev) if sc is not None else None
+    B = to_dev(b, dev)
+    Yg = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _gemm(cbis, M, N, K, X, xdt, W, wdt_c, Yg, cbis.F32, bias=B, w_scale=S, gelu=True)
+    Yr = to_dev(r, dev)
+    _gemm(cbis, M, N, K, X, xdt, W, wdt_c, Yr, cbis.F32, bias=B, w_scale=S, residual=Yr)
+    ref_g = oracle.gemm(x, wq, w_scale=sc, bias=b, gelu=True)
+    ref_r = oracle.gemm(x, wq, w_scale=sc, bias=b, residual=r)
+    assert np.abs(Yg.cpu().numpy() - ref_g).max() < FP32_TOL
+    assert np.abs(Yr.cpu().numpy() - ref_r).max() < FP32_TOL
+
+
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 def test_gemm_qkv_scatter_epilogue(cbis, oracle, dev, kv_dtype):
     """Fused QKV projection: Q to its buffer, K/V straight into page slots
