@@ -126,11 +126,14 @@ def decode_attention_timing(cbis, st, iters):
     dev = torch.device("cuda:0")
     BT = torch.from_numpy(bt).to(dev)
     POS = torch.from_numpy((kv - 1).astype(np.int32)).to(dev)
+    # rows in the order TransformerRunner passes them: longest first
+    ROWS = torch.from_numpy(np.argsort(-kv, kind="stable").astype(np.int32)).to(dev)
     q = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
     cbis.check(cbis.kernels().cbis_fill_normal_fast(q.data_ptr(), cbis.F32, q.numel(), 7, 1.0, None))
     out = torch.empty((n, H * 32), dtype=torch.bfloat16, device=dev)
     d = cbis.AttnDesc()
     d.n_rows, d.n_heads, d.head_dim, d.page_size = n, H, 32, 16
+    d.rows = ROWS.data_ptr()
     d.q_dtype, d.q, d.ldq = cbis.F32, q.data_ptr(), H * 32
     d.kv_dtype, d.k_pool, d.v_pool, d.num_pages = cbis.BF16, cache.k_base(0), cache.v_base(0), cache.max_pages()
     d.block_table, d.bt_stride, d.row_pos = BT.data_ptr(), width, POS.data_ptr()
@@ -322,9 +325,11 @@ def run_c3(args, cbis, oracle):
         cbis.check(K.cbis_fill_normal_fast(t.data_ptr(), cbis.F32, t.numel(), sd, 1.0, None))
     BT = torch.from_numpy(bt).to(dev)
     POS = torch.from_numpy((kv - 1).astype(np.int32)).to(dev)
+    ROWS = torch.from_numpy(np.argsort(-kv, kind="stable").astype(np.int32)).to(dev)  # longest first
     out = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
     d = cbis.AttnDesc()
     d.n_rows, d.n_heads, d.head_dim, d.page_size = n, H, 32, 16
+    d.rows = ROWS.data_ptr()
     d.q_dtype, d.q, d.ldq = cbis.F32, q.data_ptr(), H * 32
     d.kv_dtype, d.k_pool, d.v_pool, d.num_pages = cbis.F32, kp.data_ptr(), vp.data_ptr(), P
     d.block_table, d.bt_stride, d.row_pos = BT.data_ptr(), bt.shape[1], POS.data_ptr()

@@ -33,6 +33,7 @@ namespace {
 constexpr int kHD = 32;  // head_dim supported by these kernels
 constexpr int kPS = 16;  // page_size supported by these kernels
 constexpr int kWS = kHD + 4;  // floats per split partial: acc[32], m, l, pad
+constexpr int kResidentWaves = 256 * 32;  // decode waves resident on the 256 CUs (64 VGPRs each)
 
 struct DecodeArgs {
   const int* rows;
@@ -440,12 +441,20 @@ int resolve_split(const cbis_attn_desc* d, int hblocks, int* n_splits) {
     if (d->max_kv_len <= 0) {
       split = 1 << 30;  // single pass
     } else {
-      // Aim for >= 2048 workgroups across the chip.
       const int64_t units = (int64_t)std::max(1, d->n_rows) * hblocks;
-      const int64_t want = std::max<int64_t>(1, cdiv(2048, units));
-      int64_t s = cdiv(max_kv, want);
-      s = std::max<int64_t>(64, cdiv(s, 64) * 64);
-      split = (int)std::min<int64_t>(s, 1 << 30);
+      const int64_t pages = units * cdiv(max_kv, kPS);  // upper bound of the call's page loads
+      if (pages <= 8 * kResidentWaves) {
+        // Small call (a few pages per resident wave): one round of fat
+        // workgroups, 6 pages per wave; per-workgroup setup, partial writes
+        // and the merge weigh more than the tail here.
+        split = (int)std::min<int64_t>(max_kv, 8 * 6 * kPS);
+      } else {
+        // Aim for >= 2048 workgroups across the chip.
+        const int64_t want = std::max<int64_t>(1, cdiv(2048, units));
+        int64_t s = cdiv(max_kv, want);
+        s = std::max<int64_t>(64, cdiv(s, 64) * 64);
+        split = (int)std::min<int64_t>(s, 1 << 30);
+      }
     }
   }
   *n_splits = (int)cdiv(max_kv, split);

@@ -116,6 +116,10 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
     }
     i = j;
   }
+  // Longest rows first: the decode kernel's workgroups are dispatched in row
+  // order, so the long rows' splits start early and the short ones fill the
+  // tail.
+  std::stable_sort(drows.begin(), drows.end(), [&](int x, int y) { return pos[x] > pos[y]; });
   M_ = M;
   n_decode_ = (int)drows.size();
   n_tiles_ = (int)tiles.size() / 4;
