@@ -30,19 +30,30 @@ int check_launch(const char* what);
 // ---------------------------------------------------------------------------
 __host__ __device__ inline float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-// Round to nearest even; NaN stays a quiet NaN.
+// Round to nearest even; NaN stays a quiet NaN.  On the device this is
+// gfx950's v_cvt_pk_bf16_f32 (round to nearest even); the host restates it.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __host__ __device__ inline uint16_t f32_to_bf16(float f) {
+#ifdef __HIP_DEVICE_COMPILE__
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
   u += 0x7FFFu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
+#endif
 }
 
 __device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
 __host__ __device__ inline uint32_t pack_bf16x2(float a, float b) {
+#ifdef __HIP_DEVICE_COMPILE__
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+#else
   return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+#endif
 }
 
 // OCP e4m3 -> bf16 bits, exact for every finite code (e4m3 values are a

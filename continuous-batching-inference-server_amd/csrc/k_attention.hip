@@ -18,8 +18,8 @@
 // log2(e) folded into q), merge through LDS, and either write the output
 // (single split) or fp32 partials (m, l, acc) that a merge kernel combines.
 //
-// Prefill kernel (MFMA).  One wave per (32-row query tile, head); four heads
-// per workgroup.  S^T = K Q^T on v_mfma_f32_32x32x16_bf16 with K read straight
+// Prefill kernel (MFMA).  One workgroup per (32-row query tile, head); its
+// four waves take the key blocks round-robin and merge at the end.  S^T = K Q^T on v_mfma_f32_32x32x16_bf16 with K read straight
 // from the pages in the A-operand layout, online softmax per query column,
 // O^T = V^T P^T with P taken from the S^T accumulators in registers (their
 // lane layout is the B-operand layout up to a fixed permutation of the key
@@ -277,13 +277,22 @@ struct PrefillArgs {
   float qscale;  // log2(e) / sqrt(head_dim), applied to S in fp32
 };
 
-// Wave tile: 32 queries x one head.  Workgroup: 4 heads of the same tile.
-__global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a) {
+// Workgroup: one 32-query tile x HPW adjacent heads, 4 waves per head; a
+// head's 4 waves take its key blocks round-robin (block b goes to wave
+// b % 4) and merge their softmax states through LDS at the end.  A key's
+// head_dim slice is 64 bytes, so adjacent heads of one workgroup read the
+// same 128-byte lines at about the same time.
+constexpr int kPrefillWaves = 4;  // waves per head
+
+template <int HPW>
+__global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel(const PrefillArgs a) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int n_hgroups = a.n_heads / 4;
-  const int tile = blockIdx.x / n_hgroups;
-  const int head = (blockIdx.x % n_hgroups) * 4 + wave;
+  const int wave_id = threadIdx.x >> 6;
+  const int wave = wave_id % kPrefillWaves;  // key-block lane of this head
+  const int hsub = wave_id / kPrefillWaves;
+  const int n_hg = a.n_heads / HPW;
+  const int tile = blockIdx.x / n_hg;
+  const int head = (blockIdx.x % n_hg) * HPW + hsub;
   const int4 td = *(const int4*)(a.tiles + 4 * (int64_t)tile);
   const int row0 = td.x, nvalid = td.y, pos0 = td.w;
   const int* bt = a.bt + (int64_t)td.z * a.bt_stride;
@@ -321,7 +330,8 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
   const int qpos = pos0 + min(col, nvalid - 1);  // this lane's query position
   const int kv_end = min(pos0 + nvalid, a.max_kv);  // keys [0, kv_end) needed by the tile
 
-  __shared__ uint16_t vt[4][32][kHD + 2];  // per-wave V tile [key][dim], padded
+  __shared__ uint16_t vt_all[HPW * kPrefillWaves][32][kHD + 2];  // per-wave V tile [key][dim], padded
+  auto& vt_w = vt_all[wave_id];
   f32x16_t o;
 #pragma unroll
   for (int i = 0; i < 16; ++i) o[i] = 0.f;
@@ -354,7 +364,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
   auto compute_block = [&](int j0, const KV& r) {
     // V tile into LDS: lane (key=col, half) holds dims half*16 .. +15.
     {
-      uint32_t* dst = (uint32_t*)&vt[wave][col][half * 16];
+      uint32_t* dst = (uint32_t*)&vt_w[col][half * 16];
       dst[0] = r.v0.x; dst[1] = r.v0.y; dst[2] = r.v0.z; dst[3] = r.v0.w;
       dst[4] = r.v1.x; dst[5] = r.v1.y; dst[6] = r.v1.z; dst[7] = r.v1.w;
     }
@@ -363,27 +373,44 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
     for (int i = 0; i < 16; ++i) s[i] = 0.f;
     s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k0, qb0, s, 0, 0, 0);
     s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k1, qb1, s, 0, 0, 0);
-    // s[i]: key j0 + 8*(i/4) + 4*half + (i%4), query col.
-    float mloc = -INFINITY;
+    // s[i]: key j0 + 8*(i/4) + 4*half + (i%4), query col; raw q.k (the
+    // scale log2(e)/sqrt(hd) > 0 is applied in the exponent).  Only blocks
+    // reaching past the tile's first query position or past kv_end need the
+    // causal mask (uniform test).
+    if (j0 + 31 > pos0 || j0 + 31 >= kv_end) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kj = j0 + 8 * (i >> 2) + 4 * half + (i & 3);
-      s[i] = (kj <= qpos && kj < kv_end) ? s[i] * a.qscale : -INFINITY;
-      mloc = fmaxf(mloc, s[i]);
+      for (int i = 0; i < 16; ++i) {
+        const int kj = j0 + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (kj > qpos || kj >= kv_end) s[i] = -INFINITY;
+      }
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    // Block 0 always holds key 0 <= qpos, so m is finite from the first
-    // block on and a fully masked later block leaves it unchanged.
+    float smax = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) smax = fmaxf(smax, s[i]);
+    smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+    const float mloc = smax * a.qscale;
+    // A wave's first blocks may hold no key <= qpos for some queries (it
+    // does not start at key 0): while m and mloc are both -inf, the
+    // exponents are taken against 0 so p = 0 and the (empty) state stays 0.
     const float mn = fmaxf(m, mloc);
-    const float corr = fast_exp2(m - mn);
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float corr = fast_exp2(m - mref);
     float lsum = 0.f;
-    bf16x8_t pb0, pb1;
+    float pf[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float p = fast_exp2(s[i] - mn);
-      lsum += p;
-      if (i < 8) pb0[i] = (short)f32_to_bf16(p);
-      else pb1[i - 8] = (short)f32_to_bf16(p);
+      pf[i] = fast_exp2(fmaf(s[i], a.qscale, -mref));
+      lsum += pf[i];
+    }
+    bf16x8_t pb0, pb1;
+    {
+      uint4 u0, u1;
+      u0.x = pack_bf16x2(pf[0], pf[1]);   u0.y = pack_bf16x2(pf[2], pf[3]);
+      u0.z = pack_bf16x2(pf[4], pf[5]);   u0.w = pack_bf16x2(pf[6], pf[7]);
+      u1.x = pack_bf16x2(pf[8], pf[9]);   u1.y = pack_bf16x2(pf[10], pf[11]);
+      u1.z = pack_bf16x2(pf[12], pf[13]); u1.w = pack_bf16x2(pf[14], pf[15]);
+      pb0 = __builtin_bit_cast(bf16x8_t, u0);
+      pb1 = __builtin_bit_cast(bf16x8_t, u1);
     }
     lsum += __shfl_xor(lsum, 32, 64);
     l = l * corr + lsum;
@@ -391,35 +418,71 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const PrefillArgs a)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[i] *= corr;
     // V^T as the A operand: lane = dim (col), k-slot e of MFMA b holds key
-    // 16*b + 8*(e/4) + 4*half + (e%4), matching P's register order.
-    __syncthreads();
+    // 16*b + 8*(e/4) + 4*half + (e%4), matching P's register order.  The V
+    // tile is this wave's own: its LDS writes are complete (lgkmcnt) before
+    // its lanes read each other's entries.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
     bf16x8_t va0, va1;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int kk = 8 * (e >> 2) + 4 * half + (e & 3);
-      va0[e] = (short)vt[wave][kk][col];
-      va1[e] = (short)vt[wave][16 + kk][col];
+      va0[e] = (short)vt_w[kk][col];
+      va1[e] = (short)vt_w[16 + kk][col];
     }
     o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va0, pb0, o, 0, 0, 0);
     o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va1, pb1, o, 0, 0, 0);
-    __syncthreads();
+    // The next block's V writes come after these reads in program order.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
   };
 
-  // Key blocks stream through a 4-entry register ring: block b + 3 is in
-  // flight while block b is computed.  The trip count is the same for the
-  // four waves (one query tile), so the barriers inside stay uniform.
+  // This wave's key blocks (wave, wave + 4, ...) stream through a 4-entry
+  // register ring: its block i + 3 is in flight while block i is computed.
   // Loads past the last block are clamped to key kv_end - 1 (in bounds) and
   // left unused.
   const int nblk = (kv_end + 31) / 32;
+  const int nmine = nblk > wave ? (nblk - wave + kPrefillWaves - 1) / kPrefillWaves : 0;
+  auto key0 = [&](int i) { return 32 * (wave + kPrefillWaves * i); };
   KV ring[4];
 #pragma unroll
-  for (int u = 0; u < 3; ++u) load_block(32 * u, ring[u]);
-  for (int b0 = 0; b0 < nblk; b0 += 4) {
+  for (int u = 0; u < 3; ++u) load_block(key0(u), ring[u]);
+  for (int i0 = 0; i0 < nmine; i0 += 4) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      load_block(32 * (b0 + u + 3), ring[(u + 3) & 3]);
-      if (b0 + u < nblk) compute_block(32 * (b0 + u), ring[u]);
+      load_block(key0(i0 + u + 3), ring[(u + 3) & 3]);
+      if (i0 + u < nmine) compute_block(key0(i0 + u), ring[u]);
     }
+  }
+
+  // Merge the waves' (m, l, o) per query column; a wave without blocks has
+  // m = -inf and contributes nothing.  Wave 0 always holds key 0.
+  __shared__ float pm_all[HPW][kPrefillWaves][64], pl_all[HPW][kPrefillWaves][64];
+  __shared__ f32x16_t po_all[HPW][kPrefillWaves][64];
+  auto& pm = pm_all[hsub];
+  auto& pl = pl_all[hsub];
+  auto& po = po_all[hsub];
+  pm[wave][lane] = m;
+  pl[wave][lane] = l;
+  po[wave][lane] = o;
+  __syncthreads();
+  if (wave != 0) return;
+  float M = m;
+#pragma unroll
+  for (int w = 1; w < kPrefillWaves; ++w) M = fmaxf(M, pm[w][lane]);
+  {
+    const float c0 = fast_exp2(m - M);
+    l *= c0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] *= c0;
+  }
+#pragma unroll
+  for (int w = 1; w < kPrefillWaves; ++w) {
+    const float c = fast_exp2(pm[w][lane] - M);
+    l += pl[w][lane] * c;
+    const f32x16_t ow = po[w][lane];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] += ow[i] * c;
   }
   // o[i]: dim 8*(i/4) + 4*half + (i%4) of query col.
   if (col < nvalid) {
@@ -548,7 +611,7 @@ int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int
   int rc = validate(d, "cbis_paged_prefill_attention");
   if (rc) return rc;
   CBIS_REQUIRE(d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_paged_prefill_attention: needs bf16 K/V");
-  CBIS_REQUIRE(d->n_heads % 4 == 0, CBIS_ERR_UNSUPPORTED, "cbis_paged_prefill_attention: n_heads %% 4");
+
   CBIS_REQUIRE(n_tiles >= 0, CBIS_ERR_INVALID, "cbis_paged_prefill_attention: n_tiles < 0");
   if (n_tiles == 0) return CBIS_OK;
   CBIS_REQUIRE(tiles && ((uintptr_t)tiles & 15u) == 0, CBIS_ERR_INVALID,
@@ -569,8 +632,12 @@ int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int
   a.n_heads = d->n_heads;
   a.max_kv = (int)std::min<int64_t>(d->bt_stride * kPS, 1 << 30);
   a.qscale = kLog2e / sqrtf((float)kHD);
-  const int64_t grid = (int64_t)n_tiles * (d->n_heads / 4);
-  paged_prefill_kernel<<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>(a);
+  // Two heads per workgroup measured best (C4 chunks: 36.7 us vs 42.2 with
+  // one head and 41.7 with four).
+  const int hpw = d->n_heads % 2 == 0 ? 2 : 1;
+  const int64_t grid = (int64_t)n_tiles * (d->n_heads / hpw);
+  if (hpw == 2) paged_prefill_kernel<2><<<(unsigned)grid, 2 * kPrefillWaves * 64, 0, (hipStream_t)stream>>>(a);
+  else paged_prefill_kernel<1><<<(unsigned)grid, kPrefillWaves * 64, 0, (hipStream_t)stream>>>(a);
   return check_launch("cbis_paged_prefill_attention");
 }
 

@@ -260,13 +260,35 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
   }
 }
 
+// Sums the split-K partials (fixed order) and applies the epilogue; four
+// consecutive columns per thread (16-byte partial loads) when N % 4 == 0.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs g) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t MN = (int64_t)g.M * g.N;
+  if ((g.N & 3) == 0) {
+    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (idx >= MN) return;
+    float4 v = *(const float4*)(g.partial + idx);
+    for (int z = 1; z < g.ksplit; ++z) {
+      const float4 p = *(const float4*)(g.partial + z * MN + idx);
+      v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    }
+    const int row = (int)(idx / g.N), col = (int)(idx % g.N);
+    epilogue_store(g, row, col, v.x);
+    epilogue_store(g, row, col + 1, v.y);
+    epilogue_store(g, row, col + 2, v.z);
+    epilogue_store(g, row, col + 3, v.w);
+    return;
+  }
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= MN) return;
   float v = 0.f;
   for (int z = 0; z < g.ksplit; ++z) v += g.partial[z * MN + idx];
   epilogue_store(g, (int)(idx / g.N), (int)(idx % g.N), v);
+}
+
+inline unsigned splitk_reduce_blocks(const GemmArgs& g) {
+  const int64_t MN = (int64_t)g.M * g.N;
+  return (unsigned)cdiv((g.N & 3) == 0 ? cdiv(MN, 4) : MN, 256);
 }
 
 // ---------------------------------------------------------------------------
@@ -452,7 +474,7 @@ int launch_dma(const GemmArgs& g, hipStream_t s) {
   gemm_bf16_dma_kernel<BM, BN, WM, WN, STAGES><<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, 0, s>>>(g);
   int rc = check_launch("cbis_gemm(bf16)");
   if (rc || g.ksplit <= 1) return rc;
-  splitk_reduce_kernel<<<(unsigned)cdiv((int64_t)g.M * g.N, 256), 256, 0, s>>>(g);
+  splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
   return check_launch("cbis_gemm(split-k reduce)");
 }
 
@@ -602,9 +624,9 @@ constexpr int kSkinnyMaxM = 64;
 // Tile of the bf16 direct-to-LDS path and its split-K plan.  The tile is
 // 128 x 128 on 8 waves (2 x 4, each 64 x 32) with a 2-stage 64 KiB ring, so
 // two workgroups share a CU.  When the output tiles cannot occupy the 256 CUs
-// and K is long enough, K is split so about 2 workgroups per CU run; each
-// split keeps at least 16 K tiles (shorter splits lose more to the partial
-// round trip than they gain in occupancy).
+// and K has at least 64 tiles, K is split so about 2 workgroups per CU run;
+// each split keeps at least 16 K tiles.  (Measured: at K = 2048 the partial
+// round trip costs more than the occupancy gains.)
 constexpr int kDmaBM = 128, kDmaBN = 128;
 constexpr int kCUs = 256;
 
@@ -618,7 +640,7 @@ SplitPlan plan_dma_split(int M, int N, int K) {
   p.k_per = K;
   const int64_t tiles = cdiv(M, kDmaBM) * cdiv(N, kDmaBN);
   const int kt = K / 64;
-  if (tiles >= kCUs || kt < 16) return p;
+  if (tiles >= kCUs || kt < 64) return p;
   int ks = (int)std::max<int64_t>(2, std::min<int64_t>(4, (2 * kCUs) / tiles));
   ks = std::min(ks, kt / 16);
   if (ks <= 1) return p;
@@ -646,7 +668,7 @@ int launch(const GemmArgs& g, hipStream_t s) {
   k<<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, lds, s>>>(g);
   int rc = check_launch("cbis_gemm");
   if (rc || g.ksplit <= 1) return rc;
-  splitk_reduce_kernel<<<(unsigned)cdiv((int64_t)g.M * g.N, 256), 256, 0, s>>>(g);
+  splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
   return check_launch("cbis_gemm(split-k reduce)");
 }
 

@@ -97,7 +97,7 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   }
   // Rows: runs of consecutive positions of one sequence go to the MFMA
   // prefill kernel (bf16 K/V), everything else to the split-KV decode kernel.
-  const bool prefill_ok = cfg_.kv_dtype == CBIS_BF16 && cfg_.n_heads % 4 == 0;
+  const bool prefill_ok = cfg_.kv_dtype == CBIS_BF16;
   std::vector<int> drows, tiles;
   int max_kv = 1;
   for (int i = 0; i < M;) {
