@@ -19,8 +19,9 @@ cpu_baseline: the C oracle (a scalar-per-row fp64 restatement, OpenMP) timed
 on the host on one layer of the same step plus lm_head, scaled to 16 layers.
 
 Other modes: --config c1 (tiny fp32 GPT greedy continuous batching),
---config c3 (paged decode attention alone), --config c5 (long-context fp8
-decode); --copy-calib (a plain device copy for PMC byte calibration).
+--config c2 (the isolated linear layers), --config c3 (paged decode
+attention alone), --config c5 (long-context fp8 decode); --copy-calib (a
+plain device copy for PMC byte calibration).
 """
 import argparse
 import ctypes
@@ -56,6 +57,31 @@ class Events:
         import torch
         self.torch = torch
         self.stream = torch.cuda.ExternalStream(stream_handle) if stream_handle else torch.cuda.current_stream()
+
+    def time_graph(self, fn, iters, reps=5):
+        """Per-call device time of `fn` with the host taken out: `iters`
+        calls captured in one graph on a side stream, the graph replayed
+        `reps` times between events (kernels that are a few microseconds
+        long are otherwise bound by the Python launch rate)."""
+        torch = self.torch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            fn()  # warm (lazy loads happen outside the capture)
+            side.synchronize()
+            with torch.cuda.graph(g, stream=side):
+                for _ in range(iters):
+                    fn()
+        g.replay()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            g.replay()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / (reps * iters)
 
     def time(self, fn, iters):
         torch = self.torch
@@ -189,23 +215,21 @@ def gemm_timing(cbis, st, iters):
     return res, tot_flops, tot_ms
 
 
-def cpu_baseline_c4(oracle, st, cbis):
-    """The C oracle on one layer of the same step + lm_head, scaled to 16
-    layers: a bounded sample (~10-30 s of CPU work)."""
-    spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
-                            max_seq=32768, weight_dtype="bf16", kv_dtype="bf16")
-    w = oracle.synthetic_weights(spec, seed=0, pos_rows=1024)
-    cache = st["cache"]
+def cpu_step_sample(oracle, spec, cache, tok, pos, sid):
+    """Times the C oracle (fp64, OpenMP) on one layer of a forward step over
+    the GPU cache's layer-0 K/V (copied to the host), and separately the
+    0-layer remainder (embedding + ln_f + lm_head).  Returns (t_layer, t_head)."""
+    w = oracle.synthetic_weights(spec, seed=0, pos_rows=max(pos) + 1)
     om = oracle.OracleModel(w, max_pages=1)
-    om.kpools = [np.empty((cache.max_pages(), 16, 64, 32), np.uint16)]
-    om.vpools = [np.empty((cache.max_pages(), 16, 64, 32), np.uint16)]
+    P = cache.max_pages()
+    om.kpools = [np.empty((P, 16, spec.n_heads, spec.head_dim), np.uint16)]
+    om.vpools = [np.empty((P, 16, spec.n_heads, spec.head_dim), np.uint16)]
     hip = ctypes.CDLL("libamdhip64.so")
     hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
     for dst, src in ((om.kpools[0], cache.k_base(0)), (om.vpools[0], cache.v_base(0))):
         assert hip.hipMemcpy(dst.ctypes.data, src, dst.nbytes, 2) == 0
     om._kp = (ctypes.c_void_p * 1)(om.kpools[0].ctypes.data)
     om._vp = (ctypes.c_void_p * 1)(om.vpools[0].ctypes.data)
-    tok, pos, sid = st["tok"], st["pos"], st["sid"]
     M = len(tok)
     wpage = np.empty(M, np.int32)
     woff = np.empty(M, np.int32)
@@ -213,23 +237,31 @@ def cpu_baseline_c4(oracle, st, cbis):
     for i in range(M):
         wpage[i], woff[i] = cache.resolve_slot(sid[i], pos[i])
         row_bt[i] = uniq.setdefault(sid[i], len(uniq))
-    tables = {s: cache.pages(s) for s in uniq}
+    tables = {q: cache.pages(q) for q in uniq}
     width = max(len(t) for t in tables.values())
     bt = np.zeros((len(uniq), width), np.int32)
-    for s, j in uniq.items():
-        bt[j, : len(tables[s])] = tables[s]
+    for q, j in uniq.items():
+        bt[j, : len(tables[q])] = tables[q]
     t0 = time.time()
     om.forward_step(tok, pos, wpage, woff, bt, row_bt)
     t_layer_plus_head = time.time() - t0
-    # separate the lm_head share with a 0-layer pass (embed + ln_f + lm_head)
     om._mdl.n_layers = 0
     t1 = time.time()
     om.forward_step(tok, pos, wpage, woff, bt, row_bt)
     t_head = time.time() - t1
-    t_step = (t_layer_plus_head - t_head) * 16 + t_head
+    return t_layer_plus_head - t_head, t_head
+
+
+def cpu_baseline_c4(oracle, st, cbis):
+    """The C oracle on one layer of the same step + lm_head, scaled to 16
+    layers: a bounded sample (~10-30 s of CPU work)."""
+    spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
+                            max_seq=32768, weight_dtype="bf16", kv_dtype="bf16")
+    t_layer, t_head = cpu_step_sample(oracle, spec, st["cache"], st["tok"], st["pos"], st["sid"])
+    t_step = t_layer * 16 + t_head
     return {"value": round(192.0 / t_step, 3), "unit": "decode tokens/s", "cores": oracle.lib().orc_num_threads(),
             "kind": "port",
-            "sample": f"oracle fp64 forward of config 4's 1216-row step, 1 of 16 layers ({t_layer_plus_head - t_head:.1f}s)"
+            "sample": f"oracle fp64 forward of config 4's 1216-row step, 1 of 16 layers ({t_layer:.1f}s)"
                       f" + lm_head ({t_head:.1f}s), scaled to 16 layers; step {t_step:.1f}s"}
 
 
@@ -459,12 +491,95 @@ def run_c5(args, cbis, oracle):
     dt = float(np.median(times))
     value = n_seq * gen / dt
     _log(f"c5: {gen} steps in {dt * 1000:.2f} ms -> {value:.1f} tok/s ({dt * 1000 / gen:.3f} ms/step)")
+    cpu = None
+    if not args.no_cpu:
+        spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
+                                max_seq=32768, weight_dtype="fp8", kv_dtype="bf16")
+        t_layer, t_head = cpu_step_sample(oracle, spec, cache, first, [ctx] * n_seq, seqs)
+        t_step = t_layer * 16 + t_head
+        cpu = {"value": round(n_seq / t_step, 4), "unit": "decode tokens/s", "cores": oracle.lib().orc_num_threads(),
+               "kind": "port",
+               "sample": f"oracle fp64 forward of one 16-row config-5 step (kv 32704), 1 of 16 layers "
+                         f"({t_layer:.1f}s) + lm_head ({t_head:.1f}s), scaled to 16 layers; step {t_step:.1f}s"}
     return {"metric": "decode tokens/s (config 5 long-context fp8 decode)", "value": round(value, 2),
             "unit": "decode tokens/s", "ms_per_step": round(dt * 1000 / gen, 4), "dtype": "bf16 x fp8-e4m3",
             "data": "synthetic (fp8 weights absmax-quantised from N(0,0.02); K/V cache N(0,1))",
             "config": {"workload": "c5_long_context_fp8_decode", "sequences": n_seq, "kv_len": "32704..32767",
                        "decode_tokens": gen, "kv_cache_gb": round(16 * n_seq * 32768 * 2048 * 2 * 2 / 1e9, 1)},
-            "cpu_baseline": None}
+            "cpu_baseline": cpu}
+
+
+def run_c2(args, cbis, oracle):
+    """Config 2: the isolated flattened-batch linear layers of the reference
+    model (d_model 256): QKV 256->768 (+bias), out-proj 256->256 (+bias),
+    MLP up 256->1024 (+bias, GELU), MLP down 1024->256 (+bias, residual), at
+    M in {64, 512, 4096}, fp32 and bf16 (fp32 accumulate).  Device time per
+    call from a replayed graph of `steps` calls.  value = total flops of the
+    24 GEMMs / their summed time; each shape is reported with
+    its TFLOP/s, bytes moved and roofline fraction (fp32: MFMA-bound against
+    157.3 TFLOP/s; bf16: min(2.5 PFLOP/s, AI x 8 TB/s))."""
+    import torch
+    dev = torch.device("cuda:0")
+    K_ = cbis.kernels()
+    ev = Events(None)
+    shapes = [("qkv", 768, 256, True, False, False), ("out", 256, 256, True, False, False),
+              ("up", 1024, 256, True, True, False), ("down", 256, 1024, True, False, True)]
+    rows, tot_fl, tot_ms = [], 0.0, 0.0
+    cpu_fl = cpu_s = 0.0
+    for dt in ("f32", "bf16"):
+        for M in (64, 512, 4096):
+            for name, N, K, has_b, gelu, has_r in shapes:
+                x = torch.randn(M, K, device=dev)
+                w = torch.randn(N, K, device=dev) * 0.02
+                b = torch.randn(N, device=dev) * 0.02
+                Y = torch.randn(M, N, device=dev)
+                X = x if dt == "f32" else x.to(torch.bfloat16)
+                W = w if dt == "f32" else w.to(torch.bfloat16)
+                d = cbis.GemmDesc()
+                d.M, d.N, d.K = M, N, K
+                d.x_dtype = d.w_dtype = cbis.F32 if dt == "f32" else cbis.BF16
+                d.X, d.ldx, d.W, d.ldw = X.data_ptr(), K, W.data_ptr(), K
+                d.bias = b.data_ptr()
+                d.epilogue = cbis.EPI_GELU if gelu else cbis.EPI_NONE
+                if has_r:
+                    d.residual, d.ldr = Y.data_ptr(), N
+                d.y_dtype, d.Y, d.ldy = cbis.F32, Y.data_ptr(), N
+                fn = lambda d=d: cbis.check(K_.cbis_gemm(ctypes.byref(d), torch.cuda.current_stream().cuda_stream))
+                ms = ev.time_graph(fn, max(5, args.steps))
+                fl = 2.0 * M * N * K
+                es = 4 if dt == "f32" else 2
+                nbytes = (M * K + N * K) * es + (N + M * N) * 4 + (M * N * 4 if has_r else 0)
+                tf = fl / ms / 1e9
+                if dt == "f32":
+                    peak = FP32_PEAK_TFLOPS
+                    bound = "mfma"
+                else:
+                    peak = min(BF16_PEAK_TFLOPS, fl / nbytes * HBM_PEAK_GBS / 1e3)
+                    bound = "mfma" if peak == BF16_PEAK_TFLOPS else "hbm"
+                rows.append({"dtype": dt, "M": M, "shape": name, "N": N, "K": K, "us": round(ms * 1000, 2),
+                             "tflops": round(tf, 1), "gbs": round(nbytes / ms / 1e6, 1), "bound": bound,
+                             "roofline_frac": round(tf / peak, 4)})
+                tot_fl += fl
+                tot_ms += ms
+                if not args.no_cpu and M == 512:
+                    xh, wh, bh = x.cpu().numpy(), w.cpu().numpy(), b.cpu().numpy()
+                    t0 = time.time()
+                    oracle.gemm(xh, wh, bias=bh, gelu=gelu)
+                    cpu_s += time.time() - t0
+                    cpu_fl += fl
+    for r in rows:
+        _log(f"c2 {r['dtype']:>4} M={r['M']:>4} {r['shape']:>4}: {r['us']:8.2f} us {r['tflops']:7.1f} TFLOP/s "
+             f"{r['gbs']:7.1f} GB/s  {r['bound']} frac {r['roofline_frac']:.3f}")
+    value = tot_fl / tot_ms / 1e9
+    cpu = None
+    if cpu_s > 0:
+        cpu = {"value": round(cpu_fl / cpu_s / 1e9, 3), "unit": "GFLOP/s", "cores": oracle.lib().orc_num_threads(),
+               "kind": "port", "sample": f"oracle fp64 GEMM (+bias/GELU) of the 8 M=512 shapes ({cpu_s:.1f} s)"}
+    return {"metric": "flattened-batch linear layers TFLOP/s (config 2)", "value": round(value, 2), "unit": "TFLOP/s",
+            "ms_per_step": round(tot_ms, 4), "dtype": "f32 and bf16 (fp32 accumulate)",
+            "data": "synthetic (X N(0,1), W and bias N(0,0.02))",
+            "config": {"workload": "c2_linear_layers", "d_model": 256, "M": [64, 512, 4096], "shapes": rows},
+            "cpu_baseline": cpu}
 
 
 def run_copy_calib(args):
@@ -484,7 +599,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c3", "c5"],
+    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c2", "c3", "c5"],
                     help="c4: the bench line (default); c1 / c3 / c5: the other BASELINE configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calib", action="store_true")
@@ -501,7 +616,7 @@ def main():
     cbis = _cbis()
     import oracle
     if args.config != "c4":
-        res = {"c1": run_c1, "c3": run_c3, "c5": run_c5}[args.config](args, cbis, oracle)
+        res = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c5": run_c5}[args.config](args, cbis, oracle)
         line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
                 "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
                 "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"], "data": res["data"],
