@@ -242,13 +242,18 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArg
   if (ns <= 1) return;
   const float* w = a.ws + ((int64_t)ridx * a.n_splits * a.n_heads + head) * kWS;
   const int64_t sstride = (int64_t)a.n_heads * kWS;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, w[s * sstride + kHD]);
-  float L = 0.f, O = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const float c = fast_exp2(w[s * sstride + kHD] - M);
-    L += w[s * sstride + kHD + 1] * c;
-    O += w[s * sstride + d] * c;
+  // One pass with a running maximum; the loads of later splits do not depend
+  // on the running state, so they are issued ahead.  Split 0 always exists
+  // and holds a finite maximum.
+  float M = w[kHD], L = w[kHD + 1], O = w[d];
+#pragma unroll 4
+  for (int s = 1; s < ns; ++s) {
+    const float ms = w[s * sstride + kHD], ls = w[s * sstride + kHD + 1], os = w[s * sstride + d];
+    const float Mn = fmaxf(M, ms);
+    const float c0 = fast_exp2(M - Mn), c1 = fast_exp2(ms - Mn);
+    L = L * c0 + ls * c1;
+    O = O * c0 + os * c1;
+    M = Mn;
   }
   const float r = O / L;
   const int64_t o = (int64_t)row * a.ldo + head * kHD + d;

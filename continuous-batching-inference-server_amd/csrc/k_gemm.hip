@@ -505,11 +505,14 @@ template <>
 struct SkinnyW<uint8_t> {  // fp8 e4m3: 8 elements = 8 bytes
   __device__ static inline bf16x8_t load(const uint8_t* p) {
     const uint2 r = *(const uint2*)p;
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.x, 1.0f, false);
-    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.x, 1.0f, true);
-    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.y, 1.0f, false);
-    const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.y, 1.0f, true);
+    return load_pair(r.x, r.y);
+  }
+  // 8 e4m3 codes (two dwords, lowest byte first) -> 8 bf16.
+  __device__ static inline bf16x8_t load_pair(uint32_t lo, uint32_t hi) {
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+    const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
     uint4 u;
     u.x = __builtin_bit_cast(uint32_t, a);
     u.y = __builtin_bit_cast(uint32_t, b);
@@ -566,6 +569,44 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
     int kb = kb0;
     for (; kb + 4 <= kb1; kb += 4) step(kb, std::integral_constant<int, 4>());
     for (; kb < kb1; ++kb) step(kb, std::integral_constant<int, 1>());
+  } else if constexpr (sizeof(WT) == 1) {
+    // fp8: 16 bytes of W per lane and load feed two MFMAs.  Within a 64-wide
+    // k step lane quarter q holds k = 16 q + 0..7 for the first MFMA and
+    // 16 q + 8..15 for the second, for W and X alike, so every product pairs
+    // the same k.
+    const uint8_t* wp = (const uint8_t*)g.W + (int64_t)n * g.ldw + 16 * q;
+    const uint16_t* xp[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) xp[i] = (const uint16_t*)g.X + (int64_t)xrow[i] * g.ldx + 16 * q;
+    const int nk2 = g.K / 64;
+    const int k0 = (nk2 * wave) / kSkinnyWaves, k1 = (nk2 * (wave + 1)) / kSkinnyWaves;
+    auto step2 = [&](int kb, auto U) {
+      constexpr int NU = decltype(U)::value;
+      uint4 wr[NU];
+      bf16x8_t x[NU][MB][2];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        wr[u] = *(const uint4*)(wp + (kb + u) * 64);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          x[u][i][0] = *(const bf16x8_t*)(xp[i] + (kb + u) * 64);
+          x[u][i][1] = *(const bf16x8_t*)(xp[i] + (kb + u) * 64 + 8);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const bf16x8_t w0 = SkinnyW<uint8_t>::load_pair(wr[u].x, wr[u].y);
+        const bf16x8_t w1 = SkinnyW<uint8_t>::load_pair(wr[u].z, wr[u].w);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[u][i][0], w0, acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[u][i][1], w1, acc[i], 0, 0, 0);
+        }
+      }
+    };
+    int kb = k0;
+    for (; kb + 4 <= k1; kb += 4) step2(kb, std::integral_constant<int, 4>());
+    for (; kb < k1; ++kb) step2(kb, std::integral_constant<int, 1>());
   } else {
     const WT* wp = (const WT*)g.W + (int64_t)n * g.ldw + 8 * q;
     const uint16_t* xp[MB];
@@ -743,12 +784,10 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
   g.partial = nullptr;
 
   hipStream_t s = (hipStream_t)stream;
-  // Decode-sized M: weight streaming (K a multiple of 32 for bf16 / fp8 --
-  // already required -- and of 16 for fp32, W rows 16-byte aligned for fp32
-  // and bf16, 8-byte for fp8).
-  const bool w_al = ((uintptr_t)d->W & (d->w_dtype == CBIS_FP8E4M3 ? 7u : 15u)) == 0 &&
-                    (d->ldw * we) % (d->w_dtype == CBIS_FP8E4M3 ? 8 : 16) == 0;
-  if (d->M <= kSkinnyMaxM && w_al && d->K % 32 == 0) {
+  // Decode-sized M: weight streaming (K a multiple of 32 for bf16 and fp32,
+  // of 64 for fp8; W rows 16-byte aligned).
+  const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * we) % 16 == 0;
+  if (d->M <= kSkinnyMaxM && w_al && d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0) {
     if (f32) return launch_skinny<float, float>(g, s);
     if (d->w_dtype == CBIS_BF16) return launch_skinny<uint16_t, uint16_t>(g, s);
     return launch_skinny<uint16_t, uint8_t>(g, s);
