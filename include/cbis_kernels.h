@@ -23,7 +23,10 @@
  * (docs/gemm_layout.md:16-41); K/V pools are [pages][page_size][heads][head_dim].
  * Entry points are stream-ordered, allocate nothing, and return 0 on success
  * or a non-zero cbis_status; cbis_last_error() then holds a message (per
- * thread).  They never exit() (the reference's CUDA_CHECK does,
+ * thread).  Every buffer a call (or a descriptor it reads) points to -- row
+ * lists, page tables, workspaces included -- must stay allocated and
+ * unmodified by other work until the launched kernels finish on the stream:
+ * the kernels read them asynchronously.  They never exit() (the reference's CUDA_CHECK does,
  * include/cuda_check.hpp:7-15).
  */
 #ifndef CBIS_KERNELS_H

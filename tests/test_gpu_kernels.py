@@ -421,6 +421,11 @@ def _attn_desc(cbis, n_rows, H, q, kp, vp, num_pages, bt, bt_stride, pos, out, k
     d.max_kv_len, d.split_tokens = max_kv, split
     if ws is not None:
         d.workspace, d.workspace_bytes = ptr(ws), ws.numel() * ws.element_size()
+    # The descriptor holds raw device addresses: keep every tensor it points
+    # to alive as long as the descriptor (a temporary freed here could be
+    # handed to the next allocation, e.g. the workspace, while a kernel still
+    # reads it through the descriptor).
+    d.keep_alive = (q, kp, vp, bt, pos, out, rows, row_bt, ws)
     return d
 
 
@@ -540,6 +545,99 @@ def test_decode_attention_closed_forms(cbis, oracle, dev):
     assert np.array_equal(o[0], v[5, 0])
     keys = [v[bt[1, j // 16], j % 16] for j in range(51)]
     assert np.abs(o[1] - np.mean(keys, axis=0)).max() < 1e-5
+
+
+def test_decode_attention_max_context(cbis, oracle, dev):
+    """Rows at the reference's kMaxSeqLen (kv_len 32768, include/config.hpp)
+    and one below, next to a 1-token row, bf16 K/V with 64 heads over a
+    permuted pool: the config-5 decode shape against the fp64 oracle."""
+    import torch
+    H = 64
+    kv = np.array([32768, 32767, 1, 32768], np.int32)
+    npages = (kv + 15) // 16
+    P = int(npages.sum()) + 8
+    perm = rng(9).permutation(P).astype(np.int32)
+    bt = np.zeros((len(kv), int(npages.max())), np.int32)
+    off = 0
+    for i in range(len(kv)):
+        bt[i, : npages[i]] = perm[off: off + npages[i]]
+        off += npages[i]
+    kp = torch.empty((P, 16, H, 32), dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((len(kv), H * 32), dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    for t, sd, dt in ((kp, 31, cbis.BF16), (vp, 32, cbis.BF16), (q, 33, cbis.F32)):
+        cbis.check(K.cbis_fill_normal_fast(ptr(t), dt, t.numel(), sd, 1.0, stream()))
+    pos = kv - 1
+    out = torch.empty((len(kv), H * 32), dtype=torch.float32, device=dev)
+    d = _attn_desc(cbis, len(kv), H, q, kp, vp, P, to_dev(bt, dev), bt.shape[1], to_dev(pos, dev), out,
+                   cbis.BF16, max_kv=int(kv.max()))
+    need = K.cbis_paged_attention_workspace_size(ctypes.byref(d))
+    ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+    d.workspace, d.workspace_bytes = ptr(ws), need
+    cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream()))
+    sync()
+    ref = oracle.paged_attention(q.cpu().numpy(), bits_u16(kp), bits_u16(vp), bt, pos, H, 32, 16, kv_dtype=1)
+    assert np.abs(out.cpu().numpy() - ref).max() < FP32_TOL
+
+
+def test_decode_attention_row_order_invariant(cbis, oracle, dev):
+    """The row list only orders the work (TransformerRunner passes rows
+    longest-first): any order gives bit-identical outputs."""
+    import torch
+    H, P, n = 16, 2000, 24
+    kv = oracle.uniform_int(4, 77, n, 1, 1500)
+    npages = (kv + 15) // 16
+    perm = rng(6).permutation(P).astype(np.int32)
+    bt = np.zeros((n, int(npages.max())), np.int32)
+    off = 0
+    for i in range(n):
+        bt[i, : npages[i]] = perm[off: off + npages[i]]
+        off += npages[i]
+    kp = torch.empty((P, 16, H, 32), dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    for t, sd, dt in ((kp, 41, cbis.BF16), (vp, 42, cbis.BF16), (q, 43, cbis.F32)):
+        cbis.check(K.cbis_fill_normal_fast(ptr(t), dt, t.numel(), sd, 1.0, stream()))
+    outs = []
+    for order in (np.arange(n), np.argsort(-kv, kind="stable"), rng(7).permutation(n)):
+        out = torch.empty((n, H * 32), dtype=torch.float32, device=dev)
+        d = _attn_desc(cbis, n, H, q, kp, vp, P, to_dev(bt, dev), bt.shape[1], to_dev(kv - 1, dev), out, cbis.BF16,
+                       rows=to_dev(order.astype(np.int32), dev), max_kv=int(kv.max()))
+        need = K.cbis_paged_attention_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+        d.workspace, d.workspace_bytes = ptr(ws), need
+        cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream()))
+        sync()
+        outs.append(out.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+def test_empty_calls_are_no_ops(cbis, dev):
+    """Zero rows / tiles / tokens: every entry point returns success without
+    launching (the reference's forward_step returns {} on an empty batch,
+    src/transformer.cpp:47)."""
+    K = cbis.kernels()
+    d = cbis.GemmDesc()
+    d.M, d.N, d.K = 0, 64, 64
+    d.x_dtype = d.w_dtype = cbis.BF16
+    assert K.cbis_gemm(ctypes.byref(d), None) == 0
+    a = cbis.AttnDesc()
+    a.n_rows, a.n_heads, a.head_dim, a.page_size = 0, 16, 32, 16
+    a.kv_dtype, a.num_pages, a.bt_stride = cbis.BF16, 1, 1
+    a.q = a.k_pool = a.v_pool = a.block_table = a.out = a.row_pos = 256  # never dereferenced
+    assert K.cbis_paged_attention(ctypes.byref(a), None) == 0
+    assert K.cbis_paged_prefill_attention(ctypes.byref(a), 0, None, None) == 0
+    assert K.cbis_embed(0, 256, None, None, cbis.F32, None, None, 10, 10, None, None) == 0
+    assert K.cbis_layernorm(0, 256, None, 256, None, None, 1e-5, cbis.F32, None, 256, None) == 0
+    assert K.cbis_argmax_rows(0, 10, None, 10, None, None) == 0
+    cfg = cbis.ModelConfig.make(vocab=512, n_layers=1, max_seq=64)
+    w = cbis.ModelWeights.synthetic(cfg, seed=0)
+    cache = cbis.PagedKVCache(1, 8, 16, 8, 32, "f32", pages_per_seq=4)
+    runner = cbis.TransformerRunner(w, cache, 16)
+    assert runner.forward_step([], [], []).size == 0
+    assert runner.forward_step_greedy([], [], []) == []
 
 
 def test_decode_attention_rejects_unsupported(cbis):
