@@ -582,6 +582,52 @@ def run_c2(args, cbis, oracle):
             "cpu_baseline": cpu}
 
 
+def run_gemm_shapes(args, cbis, oracle):
+    """Config 4's five bf16 GEMM shapes at M = 1216 on their own (random
+    N(0,1) X, N(0,0.02) W, fp32 Y, the split-K workspace the runner gives
+    them): a light target for rocprofv3 counter passes.  value = flop-weighted
+    TFLOP/s of one layer's four projections plus lm_head."""
+    import torch
+    dev = torch.device("cuda:0")
+    K_ = cbis.kernels()
+    M = 1216
+    ev = Events(None)
+    stream = torch.cuda.current_stream().cuda_stream
+    names = [s for s in (args.shapes or "qkv,out,fc1,fc2,lm_head").split(",")]
+    dims = {"qkv": (6144, 2048), "out": (2048, 2048), "fc1": (8192, 2048), "fc2": (2048, 8192), "lm_head": (32000, 2048)}
+    X = torch.empty((M, 8192), dtype=torch.bfloat16, device=dev)
+    cbis.check(K_.cbis_fill_normal_fast(X.data_ptr(), cbis.BF16, X.numel(), 9, 1.0, None))
+    res, fl_tot, ms_tot = {}, 0.0, 0.0
+    for name in names:
+        N, K = dims[name]
+        W = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+        cbis.check(K_.cbis_fill_normal_fast(W.data_ptr(), cbis.BF16, W.numel(), 10, 0.02, None))
+        Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        d = cbis.GemmDesc()
+        d.M, d.N, d.K = M, N, K
+        d.x_dtype, d.X, d.ldx = cbis.BF16, X.data_ptr(), 8192
+        d.w_dtype, d.W, d.ldw = cbis.BF16, W.data_ptr(), K
+        d.y_dtype, d.Y, d.ldy = cbis.F32, Y.data_ptr(), N
+        need = K_.cbis_gemm_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+        d.workspace, d.workspace_bytes = ws.data_ptr(), need
+        fn = lambda d=d: cbis.check(K_.cbis_gemm(ctypes.byref(d), stream))
+        ev.time(fn, max(1, args.warmup))
+        ms = ev.time(fn, max(5, args.steps))
+        fl = 2.0 * M * N * K
+        res[name] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 1)}
+        fl_tot += fl
+        ms_tot += ms
+        _log(f"gemm {name}: {ms * 1000:.1f} us, {fl / ms / 1e9:.1f} TFLOP/s")
+    value = fl_tot / ms_tot / 1e9
+    return {"metric": "bf16 GEMM TFLOP/s on config 4's shapes (M=1216)", "value": round(value, 1),
+            "unit": "TFLOP/s", "ms_per_step": round(ms_tot, 4), "dtype": "bf16 (fp32 accumulate)",
+            "data": "synthetic (X N(0,1), W N(0,0.02))", "config": {"workload": "c4_gemm_shapes", "shapes": res},
+            "roofline": {"bound": "mfma", "achieved": round(value, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(value / BF16_PEAK_TFLOPS, 4), "traffic": None},
+            "cpu_baseline": None}
+
+
 def run_copy_calib(args):
     """A plain device-to-device copy of known size for PMC byte calibration."""
     import torch
@@ -599,8 +645,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c2", "c3", "c5"],
-                    help="c4: the bench line (default); c1 / c3 / c5: the other BASELINE configs")
+    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c2", "c3", "c5", "gemm"],
+                    help="c4: the bench line (default); c1 / c2 / c3 / c5: the other BASELINE configs; "
+                         "gemm: config 4's GEMM shapes alone")
+    ap.add_argument("--shapes", default=None, help="--config gemm: comma list of qkv,out,fc1,fc2,lm_head")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
@@ -616,7 +664,8 @@ def main():
     cbis = _cbis()
     import oracle
     if args.config != "c4":
-        res = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c5": run_c5}[args.config](args, cbis, oracle)
+        res = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c5": run_c5,
+               "gemm": run_gemm_shapes}[args.config](args, cbis, oracle)
         line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
                 "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
                 "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"], "data": res["data"],
