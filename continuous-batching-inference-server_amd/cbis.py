@@ -121,6 +121,9 @@ RUNTIME_SYMBOLS = {
     "cbis_runner_stream": (_P, [_P]),
     "cbis_runner_set_graphs": (None, [_P, _I]),
     "cbis_run_continuous": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _IP, ctypes.POINTER(ctypes.c_double), _I]),
+    "cbis_run_continuous_chunked": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _I, _I, _IP,
+                                         ctypes.POINTER(ctypes.c_double), _I]),
+    "cbis_schedule_dry_run": (_I, [_P, _I, _IP, _IP, _IP, _I, _I, _I, _I, _IP, _IP, _I, _IP, _IP, _IP, _I]),
 }
 
 _kern = None
@@ -337,17 +340,47 @@ class TransformerRunner:
 
 
 def run_continuous(runner: TransformerRunner, cache: PagedKVCache, prompts, decode_lens, max_slots=16,
-                   max_steps=4096):
-    """Returns (tokens per request, per-step wall ms)."""
+                   max_steps=4096, prefill_chunk=0, step_token_budget=0):
+    """Continuous batching (src/bench_batching.cpp:98-179); prefill_chunk /
+    step_token_budget > 0 feed prompts in chunks.  Returns (tokens per
+    request, per-step wall ms)."""
     lens = [len(p) for p in prompts]
     flat = [t for p in prompts for t in p]
     out = (ctypes.c_int * max(1, sum(decode_lens)))()
     ms = (ctypes.c_double * max_steps)()
-    n = _rt_check(runtime().cbis_run_continuous(runner._h, cache._h, len(prompts), _iarr(lens), _iarr(flat),
-                                                _iarr(decode_lens), max_slots, out, ms, max_steps),
+    n = _rt_check(runtime().cbis_run_continuous_chunked(runner._h, cache._h, len(prompts), _iarr(lens), _iarr(flat),
+                                                        _iarr(decode_lens), max_slots, prefill_chunk,
+                                                        step_token_budget, out, ms, max_steps),
                   "run_continuous")
     toks, o = [], 0
     for d in decode_lens:
         toks.append(list(out[o: o + d]))
         o += d
     return toks, list(ms[: min(n, max_steps)])
+
+
+def schedule_dry_run(cache: PagedKVCache, prompts, decode_lens, vocab, max_slots=16, prefill_chunk=0,
+                     step_token_budget=0, max_steps=4096, max_rows=1 << 16):
+    """The scheduler alone, on the host, with the stand-in step of
+    cbis_schedule_dry_run.  Returns (tokens per request, [(tok, pos, sid)
+    rows of each step])."""
+    lens = [len(p) for p in prompts]
+    flat = [t for p in prompts for t in p]
+    out = (ctypes.c_int * max(1, sum(decode_lens)))()
+    rows = (ctypes.c_int * max_steps)()
+    rt, rp, rs = (ctypes.c_int * max_rows)(), (ctypes.c_int * max_rows)(), (ctypes.c_int * max_rows)()
+    n = _rt_check(runtime().cbis_schedule_dry_run(cache._h, len(prompts), _iarr(lens), _iarr(flat),
+                                                  _iarr(decode_lens), max_slots, prefill_chunk, step_token_budget,
+                                                  vocab, out, rows, max_steps, rt, rp, rs, max_rows),
+                  "schedule_dry_run")
+    if n > max_steps or sum(rows[:n]) > max_rows:
+        raise RuntimeError("schedule_dry_run: trace larger than the buffers")
+    toks, o = [], 0
+    for d in decode_lens:
+        toks.append(list(out[o: o + d]))
+        o += d
+    steps, r = [], 0
+    for k in range(n):
+        steps.append([(rt[r + i], rp[r + i], rs[r + i]) for i in range(rows[k])])
+        r += rows[k]
+    return toks, steps

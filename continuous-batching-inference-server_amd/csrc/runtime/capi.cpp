@@ -212,25 +212,87 @@ void* cbis_runner_stream(cbis_runner* r) { return (void*)r->impl->stream(); }
 
 void cbis_runner_set_graphs(cbis_runner* r, int enable) { r->impl->set_graphs(enable != 0); }
 
+namespace {
+std::vector<Request> make_requests(int n_requests, const int* prompt_lens, const int* prompt_tokens,
+                                   const int* decode_lens) {
+  if (n_requests < 0) throw std::invalid_argument("run_continuous: n_requests < 0");
+  std::vector<Request> reqs(n_requests);
+  size_t off = 0;
+  for (int i = 0; i < n_requests; ++i) {
+    if (prompt_lens[i] < 0) throw std::invalid_argument("run_continuous: negative prompt length");
+    reqs[i].prompt.assign(prompt_tokens + off, prompt_tokens + off + prompt_lens[i]);
+    off += prompt_lens[i];
+    reqs[i].decode_len = decode_lens[i];
+  }
+  return reqs;
+}
+
+void copy_tokens(const ContinuousResult& res, int n_requests, const int* decode_lens, int* out_tokens) {
+  size_t o = 0;
+  for (int i = 0; i < n_requests; ++i)
+    for (int j = 0; j < decode_lens[i]; ++j) out_tokens[o++] = j < (int)res.tokens[i].size() ? res.tokens[i][j] : -1;
+}
+
+ScheduleOptions options(int max_slots, int prefill_chunk, int step_token_budget) {
+  ScheduleOptions opt;
+  opt.max_slots = max_slots;
+  opt.prefill_chunk = prefill_chunk;
+  opt.step_token_budget = step_token_budget;
+  return opt;
+}
+}  // namespace
+
 int cbis_run_continuous(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
                         const int* prompt_tokens, const int* decode_lens, int max_slots, int* out_tokens,
                         double* step_ms, int max_steps) {
+  return cbis_run_continuous_chunked(r, c, n_requests, prompt_lens, prompt_tokens, decode_lens, max_slots, 0, 0,
+                                     out_tokens, step_ms, max_steps);
+}
+
+int cbis_run_continuous_chunked(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
+                                const int* prompt_tokens, const int* decode_lens, int max_slots, int prefill_chunk,
+                                int step_token_budget, int* out_tokens, double* step_ms, int max_steps) {
   return guard([&] {
-    std::vector<Request> reqs(n_requests);
-    size_t off = 0;
-    for (int i = 0; i < n_requests; ++i) {
-      reqs[i].prompt.assign(prompt_tokens + off, prompt_tokens + off + prompt_lens[i]);
-      off += prompt_lens[i];
-      reqs[i].decode_len = decode_lens[i];
-    }
-    const ContinuousResult res = run_continuous(*r->impl, *c->impl, reqs, max_slots);
-    size_t o = 0;
-    for (int i = 0; i < n_requests; ++i) {
-      for (int j = 0; j < decode_lens[i]; ++j) out_tokens[o++] = j < (int)res.tokens[i].size() ? res.tokens[i][j] : -1;
-    }
+    const std::vector<Request> reqs = make_requests(n_requests, prompt_lens, prompt_tokens, decode_lens);
+    const ContinuousResult res =
+        run_continuous(*r->impl, *c->impl, reqs, options(max_slots, prefill_chunk, step_token_budget));
+    copy_tokens(res, n_requests, decode_lens, out_tokens);
     if (step_ms)
       for (int i = 0; i < (int)res.step_ms.size() && i < max_steps; ++i) step_ms[i] = res.step_ms[i];
     return (int)res.step_ms.size();
+  });
+}
+
+int cbis_schedule_dry_run(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens,
+                          const int* decode_lens, int max_slots, int prefill_chunk, int step_token_budget, int vocab,
+                          int* out_tokens, int* step_rows, int max_steps, int* row_tok, int* row_pos, int* row_sid,
+                          int max_rows) {
+  return guard([&] {
+    if (vocab <= 0) throw std::invalid_argument("schedule_dry_run: vocab must be > 0");
+    const std::vector<Request> reqs = make_requests(n_requests, prompt_lens, prompt_tokens, decode_lens);
+    const StepFn step = [&](const std::vector<int>& t, const std::vector<int>& p, const std::vector<int>& s) {
+      std::vector<int> next(t.size());
+      for (size_t i = 0; i < t.size(); ++i)
+        next[i] = (int)(((uint32_t)t[i] * 31u + (uint32_t)p[i] * 7u + (uint32_t)s[i] * 13u + 1u) % (uint32_t)vocab);
+      return next;
+    };
+    std::vector<StepRows> trace;
+    const ContinuousResult res =
+        run_continuous(step, *c->impl, reqs, options(max_slots, prefill_chunk, step_token_budget), &trace);
+    copy_tokens(res, n_requests, decode_lens, out_tokens);
+    int row = 0;
+    for (size_t k = 0; k < trace.size(); ++k) {
+      const int n = (int)trace[k].tok.size();
+      if ((int)k < max_steps) step_rows[k] = n;
+      for (int i = 0; i < n; ++i, ++row) {
+        if (row < max_rows) {
+          row_tok[row] = trace[k].tok[i];
+          row_pos[row] = trace[k].pos[i];
+          row_sid[row] = trace[k].sid[i];
+        }
+      }
+    }
+    return (int)trace.size();
   });
 }
 

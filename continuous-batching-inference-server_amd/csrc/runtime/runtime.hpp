@@ -10,6 +10,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <stdexcept>
@@ -212,6 +213,28 @@ struct ContinuousResult {
   std::vector<double> step_ms;           // wall time of each forward step
 };
 
+// Scheduling knobs.  prefill_chunk = 0 and step_token_budget = 0 is the
+// reference's policy (a slot's whole prompt in the step after admission).
+struct ScheduleOptions {
+  int max_slots = 16;
+  int prefill_chunk = 0;      // prompt rows a slot contributes per step; 0 = the whole prompt
+  int step_token_budget = 0;  // cap on prompt rows per step (decode rows always run); 0 = none
+};
+
+// Rows of one scheduled step, in the order they were handed to the step.
+struct StepRows {
+  std::vector<int> tok, pos, sid;
+};
+
+// One forward step: rows (token, position, sequence) -> greedy next token
+// of every row.
+using StepFn = std::function<std::vector<int>(const std::vector<int>&, const std::vector<int>&,
+                                              const std::vector<int>&)>;
+
+ContinuousResult run_continuous(const StepFn& step, PagedKVCache& cache, const std::vector<Request>& reqs,
+                                const ScheduleOptions& opt, std::vector<StepRows>* trace = nullptr);
+ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, const std::vector<Request>& reqs,
+                                const ScheduleOptions& opt);
 ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, const std::vector<Request>& reqs,
                                 int max_slots);
 

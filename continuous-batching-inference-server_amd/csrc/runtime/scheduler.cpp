@@ -1,29 +1,42 @@
 // Continuous batching, the iteration-level scheduler of
 // src/bench_batching.cpp:98-179 with every request present at t = 0:
 //  * free slots admit requests in order (allocate_sequence);
-//  * an un-prefilled slot contributes its whole prompt as rows at positions
-//    0..P-1 (ensure_capacity per row); a prefilled slot one decode row at
-//    next_pos fed with its last generated token;
-//  * after the step, each slot's last row yields its next token by greedy
-//    argmax (first maximum wins, :66-73) -- taken on the device here;
+//  * slots are visited in order every step; a slot still feeding its prompt
+//    contributes its next prompt rows (ensure_capacity per row), a slot past
+//    its prompt one decode row at next_pos fed with its last generated token;
+//  * after the step, the row that ends a slot's prompt, and every decode row,
+//    yields the slot's next token by greedy argmax (first maximum wins,
+//    src/bench_batching.cpp:66-73) -- taken on the device here;
 //  * a slot completes when generated >= decode_len and frees its pages.
+// With prefill_chunk = 0 and no token budget a slot's whole prompt goes in
+// the step after its admission: the reference's schedule, row for row (and
+// so its page allocation order).  prefill_chunk > 0 feeds at most that many
+// prompt rows per slot per step (the chunked prefill of
+// src/bench_tiering.cpp:78-89, mixed with the other slots' decode rows);
+// step_token_budget > 0 caps the prompt rows of one step, decode rows are
+// never deferred.
 #include <chrono>
 
 #include "runtime.hpp"
 
 namespace cbis {
 
-ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, const std::vector<Request>& reqs,
-                                int max_slots) {
+ContinuousResult run_continuous(const StepFn& step, PagedKVCache& cache, const std::vector<Request>& reqs,
+                                const ScheduleOptions& opt, std::vector<StepRows>* trace) {
   struct Slot {
     bool active = false;
-    int req = -1, seq_id = -1, next_pos = 0, last_token = 0, generated = 0;
-    bool prefilled = false;
+    int req = -1, seq_id = -1, fed = 0, next_pos = 0, last_token = 0, generated = 0;
   };
-  if (max_slots <= 0) throw std::invalid_argument("run_continuous: max_slots must be > 0");
+  if (opt.max_slots <= 0) throw std::invalid_argument("run_continuous: max_slots must be > 0");
+  if (opt.prefill_chunk < 0 || opt.step_token_budget < 0)
+    throw std::invalid_argument("run_continuous: prefill_chunk and step_token_budget must be >= 0");
+  for (const auto& r : reqs) {
+    if (r.prompt.empty()) throw std::invalid_argument("run_continuous: empty prompt");
+    if (r.decode_len <= 0) throw std::invalid_argument("run_continuous: decode_len must be > 0");
+  }
   ContinuousResult res;
   res.tokens.assign(reqs.size(), {});
-  std::vector<Slot> slots(max_slots);
+  std::vector<Slot> slots(opt.max_slots);
   size_t next_req = 0;
   size_t completed = 0;
   using Clock = std::chrono::steady_clock;
@@ -39,20 +52,26 @@ ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, 
     std::vector<int> tok, pos, sid;
     std::vector<Slot*> owner;
     std::vector<char> last;
+    int prompt_rows = 0;
     for (auto& s : slots) {
       if (!s.active) continue;
       const Request& r = reqs[s.req];
-      if (!s.prefilled) {
-        for (int p = 0; p < (int)r.prompt.size(); ++p) {
+      const int P = (int)r.prompt.size();
+      if (s.fed < P) {
+        int n = P - s.fed;
+        if (opt.prefill_chunk > 0) n = std::min(n, opt.prefill_chunk);
+        if (opt.step_token_budget > 0) n = std::min(n, opt.step_token_budget - prompt_rows);
+        for (int p = s.fed; p < s.fed + n; ++p) {
           if (!cache.ensure_capacity(s.seq_id, p)) throw std::runtime_error("run_continuous: out of KV pages");
           tok.push_back(r.prompt[p]);
           pos.push_back(p);
           sid.push_back(s.seq_id);
           owner.push_back(&s);
-          last.push_back(p == (int)r.prompt.size() - 1);
+          last.push_back(p == P - 1);
         }
-        s.next_pos = (int)r.prompt.size();
-        s.prefilled = true;
+        s.fed += std::max(n, 0);
+        prompt_rows += std::max(n, 0);
+        s.next_pos = s.fed;
       } else {
         if (!cache.ensure_capacity(s.seq_id, s.next_pos)) throw std::runtime_error("run_continuous: out of KV pages");
         tok.push_back(s.last_token);
@@ -63,10 +82,12 @@ ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, 
         s.next_pos += 1;
       }
     }
-    if (tok.empty()) throw std::runtime_error("run_continuous: no runnable rows (empty prompt?)");
+    if (tok.empty()) throw std::runtime_error("run_continuous: no runnable rows");
+    if (trace) trace->push_back({tok, pos, sid});
     const auto t0 = Clock::now();
-    const std::vector<int> next = runner.forward_step_greedy(tok, pos, sid);
+    const std::vector<int> next = step(tok, pos, sid);
     res.step_ms.push_back(std::chrono::duration<double, std::milli>(Clock::now() - t0).count());
+    if (next.size() != tok.size()) throw std::runtime_error("run_continuous: step returned a wrong row count");
     for (size_t i = 0; i < tok.size(); ++i) {
       if (!last[i]) continue;
       Slot* s = owner[i];
@@ -81,6 +102,21 @@ ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, 
     }
   }
   return res;
+}
+
+ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, const std::vector<Request>& reqs,
+                                const ScheduleOptions& opt) {
+  const StepFn step = [&](const std::vector<int>& t, const std::vector<int>& p, const std::vector<int>& s) {
+    return runner.forward_step_greedy(t, p, s);
+  };
+  return run_continuous(step, cache, reqs, opt);
+}
+
+ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, const std::vector<Request>& reqs,
+                                int max_slots) {
+  ScheduleOptions opt;
+  opt.max_slots = max_slots;
+  return run_continuous(runner, cache, reqs, opt);
 }
 
 }  // namespace cbis

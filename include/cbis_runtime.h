@@ -102,6 +102,27 @@ int cbis_run_continuous(cbis_runner* r, cbis_cache* c, int n_requests, const int
                         const int* prompt_tokens, const int* decode_lens, int max_slots, int* out_tokens,
                         double* step_ms, int max_steps);
 
+/* The same scheduler with chunked prefill (src/bench_tiering.cpp:78-89's
+ * chunking, inside continuous batching): a slot feeds at most prefill_chunk
+ * prompt rows per step (0 = its whole prompt), and one step carries at most
+ * step_token_budget prompt rows (0 = no cap; decode rows are never
+ * deferred).  prefill_chunk = step_token_budget = 0 is cbis_run_continuous. */
+int cbis_run_continuous_chunked(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
+                                const int* prompt_tokens, const int* decode_lens, int max_slots, int prefill_chunk,
+                                int step_token_budget, int* out_tokens, double* step_ms, int max_steps);
+
+/* Runs the scheduler on the host only, with a stand-in step whose "greedy
+ * token" of row (tok, pos, seq) is (31 tok + 7 pos + 13 seq + 1) mod vocab
+ * (32-bit unsigned arithmetic), so the schedule can be checked without a
+ * GPU (c may be created with alloc_device = 0).  step_rows[k] receives the
+ * row count of step k (capacity max_steps); row_tok / row_pos / row_sid the
+ * rows of every step, concatenated (capacity max_rows).  Returns the number
+ * of steps, or negative. */
+int cbis_schedule_dry_run(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens,
+                          const int* decode_lens, int max_slots, int prefill_chunk, int step_token_budget, int vocab,
+                          int* out_tokens, int* step_rows, int max_steps, int* row_tok, int* row_pos, int* row_sid,
+                          int max_rows);
+
 #ifdef __cplusplus
 }
 #endif

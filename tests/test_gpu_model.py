@@ -60,6 +60,25 @@ def test_c1_greedy_continuous_batching(cbis, oracle):
     assert cache.num_free_pages() == 128  # every sequence freed its pages
 
 
+@pytest.mark.parametrize("chunk,budget", [(16, 0), (8, 40)])
+def test_c1_chunked_prefill_greedy(cbis, oracle, chunk, budget):
+    """Config 1's workload with the prompts fed in chunks (at most `chunk`
+    rows per slot and `budget` prompt rows per step) beside the other slots'
+    decode rows: the greedy tokens are still python/model.py's."""
+    g = np.load(os.path.join(GOLDEN, "g2_c1_greedy.npz"))
+    n = int(g["n"])
+    prompts = [[int(t) for t in g[f"prompt{i}"]] for i in range(n)]
+    cfg, w = _ref_model(cbis, vocab=512)
+    cache = cbis.PagedKVCache(4, 128, 16, 8, 32, "f32")
+    runner = cbis.TransformerRunner(w, cache, 512)
+    toks, step_ms = cbis.run_continuous(runner, cache, prompts, [32] * n, max_slots=16, prefill_chunk=chunk,
+                                        step_token_budget=budget)
+    for i in range(n):
+        assert toks[i] == [int(t) for t in g[f"gen{i}"]], i
+    assert len(step_ms) > 32
+    assert cache.num_free_pages() == 128
+
+
 def test_c1_step_logits_match_golden(cbis, oracle):
     """Same workload driven step by step through forward_step: every
     generated step's last-row logits within 1e-4 of python/model.py."""
