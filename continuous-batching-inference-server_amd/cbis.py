@@ -110,6 +110,8 @@ RUNTIME_SYMBOLS = {
     "cbis_cache_fill_normal": (_I, [_P, _U64, _F]),
     "cbis_weights_synthetic": (_P, [ctypes.POINTER(ModelConfig), _U64, _F]),
     "cbis_weights_load": (_P, [ctypes.c_char_p, ctypes.POINTER(ModelConfig)]),
+    "cbis_weights_save_packed": (_I, [_P, ctypes.c_char_p]),
+    "cbis_weights_load_packed": (_P, [ctypes.c_char_p, ctypes.POINTER(ModelConfig)]),
     "cbis_weights_destroy": (None, [_P]),
     "cbis_weights_device_bytes": (_SZ, [_P]),
     "cbis_weights_tensor": (_P, [_P, ctypes.c_char_p]),
@@ -270,6 +272,16 @@ class ModelWeights:
     @classmethod
     def load(cls, path: str, cfg: ModelConfig):
         return cls(_rt_check(runtime().cbis_weights_load(path.encode(), ctypes.byref(cfg)), "ModelWeights.load"), cfg)
+
+    @classmethod
+    def load_packed(cls, path: str):
+        """A checkpoint written by save_packed; the config comes from the file."""
+        cfg = ModelConfig()
+        h = _rt_check(runtime().cbis_weights_load_packed(path.encode(), ctypes.byref(cfg)), "ModelWeights.load_packed")
+        return cls(h, cfg)
+
+    def save_packed(self, path: str) -> None:
+        _rt_check(runtime().cbis_weights_save_packed(self._h, path.encode()), "ModelWeights.save_packed")
 
     def tensor(self, name: str) -> int:
         return _rt_check(runtime().cbis_weights_tensor(self._h, name.encode()), f"tensor {name}")

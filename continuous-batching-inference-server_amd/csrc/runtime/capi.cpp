@@ -161,6 +161,31 @@ cbis_weights* cbis_weights_load(const char* path, const cbis_model_config* cfg) 
   });
 }
 
+int cbis_weights_save_packed(const cbis_weights* w, const char* path) {
+  return guard([&] {
+    w->impl->save_packed(path ? path : "");
+    return 0;
+  });
+}
+
+cbis_weights* cbis_weights_load_packed(const char* path, cbis_model_config* cfg_out) {
+  return guard_ptr<cbis_weights>([&] {
+    auto* w = new cbis_weights();
+    try {
+      w->impl = ModelWeights::load_packed(path ? path : "");
+    } catch (...) {
+      delete w;
+      throw;
+    }
+    if (cfg_out) {
+      const ModelConfig& c = w->impl->cfg;
+      *cfg_out = {c.vocab, c.d_model, c.n_heads, c.head_dim, c.n_layers, c.mlp, c.max_seq, c.page_size,
+                  c.weight_dtype, c.kv_dtype};
+    }
+    return w;
+  });
+}
+
 void cbis_weights_destroy(cbis_weights* w) { delete w; }
 
 size_t cbis_weights_device_bytes(const cbis_weights* w) { return w->impl->device_bytes(); }

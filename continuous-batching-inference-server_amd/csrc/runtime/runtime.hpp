@@ -117,8 +117,21 @@ class ModelWeights {
   void* lm_head = nullptr;
   float* lm_scale = nullptr;
 
+  // One tensor of the device arena.
+  struct Entry {
+    std::string name;
+    int dtype;
+    size_t offset, bytes;
+  };
+
   static std::unique_ptr<ModelWeights> synthetic(const ModelConfig& cfg, uint64_t seed, float std = 0.02f);
   static std::unique_ptr<ModelWeights> load(const std::string& path, const ModelConfig& cfg);
+  // Packed checkpoint: the config, the tensor table and the arena image in
+  // its stored dtypes (bf16 / fp8 codes + fp32 scales), versioned.
+  void save_packed(const std::string& path) const;
+  static std::unique_ptr<ModelWeights> load_packed(const std::string& path);
+  // The arena's tensor table for a config (no allocation).
+  static std::vector<Entry> layout(const ModelConfig& cfg);
   ~ModelWeights();
   void free_all();
   size_t device_bytes() const { return arena_bytes_; }
@@ -130,6 +143,7 @@ class ModelWeights {
   void plan();
   uint8_t* arena_ = nullptr;
   size_t arena_bytes_ = 0;
+  std::vector<Entry> table_;
   std::map<std::string, void*> named_;
 };
 

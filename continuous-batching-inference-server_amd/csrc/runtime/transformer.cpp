@@ -37,6 +37,11 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
       cache.page_size() != cfg_.page_size || cache.kv_dtype() != cfg_.kv_dtype)
     throw std::invalid_argument("TransformerRunner: cache geometry does not match the model config");
   if (!cache.has_device()) throw std::invalid_argument("TransformerRunner: cache has no device pools");
+  // The attention kernels read a page row in 1 KiB head blocks: 8 heads of
+  // fp32 or 16 heads of bf16 (head_dim 32).
+  if (cfg_.head_dim != 32 || cfg_.n_heads % (cfg_.kv_dtype == CBIS_BF16 ? 16 : 8) != 0)
+    throw std::invalid_argument("TransformerRunner: attention needs head_dim 32 and n_heads a multiple of 8 (fp32 "
+                                "K/V) or 16 (bf16 K/V)");
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
   const size_t R = max_total_rows, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
   const size_t ae = dtype_size(cfg_.act_dtype());

@@ -68,6 +68,15 @@ int cbis_cache_fill_normal(cbis_cache* c, uint64_t seed, float std);
 cbis_weights* cbis_weights_synthetic(const cbis_model_config* cfg, uint64_t seed, float std);
 /* python/export_weights.py:42-66 layout (fp32), converted to cfg's dtypes. */
 cbis_weights* cbis_weights_load(const char* path, const cbis_model_config* cfg);
+/* Packed checkpoint (no reference counterpart; the format the reference's
+ * weights.bin reader at src/model_weights.cpp:41-75 lacks for bf16 / fp8
+ * models): a versioned header with the model config and tensor table, then
+ * the device image in its stored dtypes (fp8 codes with their fp32 channel
+ * scales).  Saving needs the weights on the device; loading validates the
+ * header, the table against the config's layout, the size and a checksum
+ * before returning.  cfg_out (optional) receives the file's config. */
+int cbis_weights_save_packed(const cbis_weights* w, const char* path);
+cbis_weights* cbis_weights_load_packed(const char* path, cbis_model_config* cfg_out);
 void cbis_weights_destroy(cbis_weights* w);
 size_t cbis_weights_device_bytes(const cbis_weights* w);
 /* Device pointer of a named tensor ("tok_emb", "pos_emb", "lm_head",

@@ -234,3 +234,49 @@ def test_graph_replay_matches_eager(cbis):
         assert np.array_equal(o, eager)
     greedy = runner.forward_step_greedy(*step)
     assert greedy == [int(np.argmax(r)) for r in eager]
+
+
+@pytest.mark.parametrize("wdt", ["bf16", "fp8", "f32"])
+def test_packed_checkpoint_round_trip(cbis, tmp_path, wdt):
+    """save_packed -> load_packed gives back the same config and the same
+    device image (re-saving reproduces the file byte for byte), the same
+    logits, and a flipped data byte fails the checksum."""
+    kvdt = "f32" if wdt == "f32" else "bf16"
+    H = 8 if wdt == "f32" else 16  # bf16 K/V pages are read in 16-head blocks
+    cfg = cbis.ModelConfig.make(vocab=512, d_model=32 * H, n_heads=H, mlp=128 * H, n_layers=2, max_seq=1024,
+                                weight_dtype=wdt, kv_dtype=kvdt)
+    w = cbis.ModelWeights.synthetic(cfg, seed=5)
+    p1, p2 = tmp_path / "a.cbisw", tmp_path / "b.cbisw"
+    w.save_packed(str(p1))
+    w2 = cbis.ModelWeights.load_packed(str(p1))
+    assert [getattr(w2.cfg, f) for f, _ in cfg._fields_] == [getattr(cfg, f) for f, _ in cfg._fields_]
+    assert w2.device_bytes() == w.device_bytes()
+    w2.save_packed(str(p2))
+    assert p1.read_bytes() == p2.read_bytes()
+    ids = [int(t) for t in np.arange(37) * 13 % 512]
+    outs = []
+    for weights in (w, w2):
+        cache = cbis.PagedKVCache(2, 16, 16, H, 32, kvdt, pages_per_seq=64)
+        runner = cbis.TransformerRunner(weights, cache, 64)
+        sid = cache.allocate_sequence()
+        for q in range(len(ids)):
+            cache.ensure_capacity(sid, q)
+        outs.append(runner.forward_step(ids, list(range(len(ids))), [sid] * len(ids)))
+        runner.close()
+    assert np.array_equal(outs[0], outs[1])
+    blob = bytearray(p1.read_bytes())
+    blob[-100] ^= 0x40
+    p2.write_bytes(bytes(blob))
+    with pytest.raises(cbis.CbisError, match="checksum"):
+        cbis.ModelWeights.load_packed(str(p2))
+
+
+
+def test_runner_rejects_unsupported_head_blocks(cbis):
+    """bf16 K/V pages are read in 16-head blocks: an 8-head bf16 model is
+    refused when the runner is built, not in the middle of a step."""
+    cfg = cbis.ModelConfig.make(vocab=512, n_layers=1, max_seq=1024, weight_dtype="bf16", kv_dtype="bf16")
+    w = cbis.ModelWeights.synthetic(cfg, seed=1)
+    cache = cbis.PagedKVCache(1, 8, 16, 8, 32, "bf16", pages_per_seq=64)
+    with pytest.raises(cbis.CbisError, match="n_heads a multiple"):
+        cbis.TransformerRunner(w, cache, 16)
