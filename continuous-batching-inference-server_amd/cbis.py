@@ -55,6 +55,14 @@ class AttnDesc(ctypes.Structure):
                 ("max_kv_len", _I), ("split_tokens", _I), ("workspace", _P), ("workspace_bytes", _SZ)]
 
 
+class EvictionParams(ctypes.Structure):
+    """include/tiered_kv_manager.hpp:40-48."""
+    _fields_ = [("alpha_staleness", ctypes.c_double), ("beta_restore_cost", ctypes.c_double),
+                ("expected_compression_ratio", ctypes.c_double), ("dram_fixed_ns", ctypes.c_double),
+                ("dram_ns_per_byte", ctypes.c_double), ("nvme_fixed_ns", ctypes.c_double),
+                ("nvme_ns_per_byte", ctypes.c_double)]
+
+
 class ModelConfig(ctypes.Structure):
     _fields_ = [("vocab", _I), ("d_model", _I), ("n_heads", _I), ("head_dim", _I), ("n_layers", _I),
                 ("mlp", _I), ("max_seq", _I), ("page_size", _I), ("weight_dtype", _I), ("kv_dtype", _I)]
@@ -78,6 +86,8 @@ KERNEL_SYMBOLS = {
     "cbis_scatter_kv_to_cache": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "cbis_fused_paged_causal_attention": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "cbis_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
+    "cbis_kv_pages_gather": (_I, [_P, _P, _I, _I, ctypes.c_int64, _P, _I, _P]),
+    "cbis_kv_pages_scatter": (_I, [_P, _P, _I, _I, ctypes.c_int64, _P, _I, _P]),
     "cbis_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "cbis_paged_attention_workspace_size": (_SZ, [ctypes.POINTER(AttnDesc)]),
     "cbis_paged_attention": (_I, [ctypes.POINTER(AttnDesc), _P]),
@@ -123,6 +133,24 @@ RUNTIME_SYMBOLS = {
     "cbis_runner_stream": (_P, [_P]),
     "cbis_runner_set_graphs": (None, [_P, _I]),
     "cbis_run_continuous": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _IP, ctypes.POINTER(ctypes.c_double), _I]),
+    "cbis_eviction_params_default": (None, [ctypes.POINTER(EvictionParams)]),
+    "cbis_tiered_create": (_P, [_I, _I, _I, _I, _I, ctypes.c_char_p, _SZ, _SZ, ctypes.POINTER(EvictionParams)]),
+    "cbis_tiered_destroy": (None, [_P]),
+    "cbis_tiered_raw_block_bytes": (_SZ, [_P]),
+    "cbis_tiered_calibrate": (_I, [_P]),
+    "cbis_tiered_params": (_I, [_P, ctypes.POINTER(EvictionParams)]),
+    "cbis_tiered_admit_gpu_resident": (_I, [_P, ctypes.c_uint64, _P, _I, ctypes.c_long]),
+    "cbis_tiered_evict_one": (_I, [_P, ctypes.c_long, ctypes.POINTER(ctypes.c_uint64)]),
+    "cbis_tiered_spill": (_I, [_P, ctypes.c_uint64, _I, ctypes.c_long]),
+    "cbis_tiered_restore": (_I, [_P, ctypes.c_uint64, _P, _I, ctypes.c_long]),
+    "cbis_tiered_spill_batch": (_I, [_P, ctypes.POINTER(ctypes.c_uint64), _I, _I, ctypes.c_long]),
+    "cbis_tiered_restore_batch": (_I, [_P, ctypes.POINTER(ctypes.c_uint64), _I, _P, _IP, ctypes.c_long]),
+    "cbis_tiered_tier_of": (_I, [_P, ctypes.c_uint64]),
+    "cbis_tiered_known": (_I, [_P, ctypes.c_uint64]),
+    "cbis_tiered_touch": (_I, [_P, ctypes.c_uint64, ctypes.c_long]),
+    "cbis_tiered_stats": (_I, [_P, ctypes.POINTER(_SZ)]),
+    "cbis_block_deflate": (ctypes.c_int64, [_P, _SZ, _P, _SZ]),
+    "cbis_block_inflate": (_I, [_P, _SZ, _P, _SZ]),
     "cbis_run_continuous_chunked": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _I, _I, _IP,
                                          ctypes.POINTER(ctypes.c_double), _I]),
     "cbis_schedule_dry_run": (_I, [_P, _I, _IP, _IP, _IP, _I, _I, _I, _I, _IP, _IP, _I, _IP, _IP, _IP, _I]),
@@ -349,6 +377,108 @@ class TransformerRunner:
 
     def set_graphs(self, enable: bool) -> None:
         runtime().cbis_runner_set_graphs(self._h, int(enable))
+
+
+TIERS = {"GPU": 0, "DRAM": 1, "NVME": 2}
+TIER_NAMES = {v: k for k, v in TIERS.items()}
+
+
+class TieredKVBlockManager:
+    """include/tiered_kv_manager.hpp:50-151 on the HIP runtime; tiers are
+    the strings "GPU", "DRAM", "NVME"."""
+
+    _h = None
+
+    def __init__(self, layer_count, page_size, n_heads, head_dim, nvme_scratch_path, gpu_capacity_blocks,
+                 dram_capacity_blocks, params: "EvictionParams" = None, kv_dtype="f32"):
+        self._h = _rt_check(runtime().cbis_tiered_create(layer_count, page_size, n_heads, head_dim, DTYPES[kv_dtype],
+                                                         str(nvme_scratch_path).encode(), gpu_capacity_blocks,
+                                                         dram_capacity_blocks,
+                                                         ctypes.byref(params) if params is not None else None),
+                            "TieredKVBlockManager")
+
+    @staticmethod
+    def default_params() -> "EvictionParams":
+        p = EvictionParams()
+        runtime().cbis_eviction_params_default(ctypes.byref(p))
+        return p
+
+    def close(self):
+        if self._h:
+            runtime().cbis_tiered_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def raw_block_bytes(self) -> int:
+        return runtime().cbis_tiered_raw_block_bytes(self._h)
+
+    def calibrate(self) -> None:
+        _rt_check(runtime().cbis_tiered_calibrate(self._h), "calibrate")
+
+    def params(self) -> "EvictionParams":
+        p = EvictionParams()
+        _rt_check(runtime().cbis_tiered_params(self._h, ctypes.byref(p)), "params")
+        return p
+
+    def admit_gpu_resident(self, block_id, cache: "PagedKVCache", physical_page, now_step):
+        _rt_check(runtime().cbis_tiered_admit_gpu_resident(self._h, block_id, cache._h, physical_page, now_step),
+                  "admit_gpu_resident")
+
+    def evict_one(self, now_step):
+        out = ctypes.c_uint64()
+        _rt_check(runtime().cbis_tiered_evict_one(self._h, now_step, ctypes.byref(out)), "evict_one")
+        return None if out.value == (1 << 64) - 1 else out.value
+
+    def spill(self, block_id, dest, now_step):
+        _rt_check(runtime().cbis_tiered_spill(self._h, block_id, TIERS[dest], now_step), "spill")
+
+    def restore(self, block_id, cache: "PagedKVCache", physical_page, now_step):
+        _rt_check(runtime().cbis_tiered_restore(self._h, block_id, cache._h, physical_page, now_step), "restore")
+
+    def spill_batch(self, block_ids, dest, now_step):
+        ids = (ctypes.c_uint64 * max(1, len(block_ids)))(*block_ids)
+        _rt_check(runtime().cbis_tiered_spill_batch(self._h, ids, len(block_ids), TIERS[dest], now_step),
+                  "spill_batch")
+
+    def restore_batch(self, block_ids, cache: "PagedKVCache", physical_pages, now_step):
+        ids = (ctypes.c_uint64 * max(1, len(block_ids)))(*block_ids)
+        _rt_check(runtime().cbis_tiered_restore_batch(self._h, ids, len(block_ids), cache._h, _iarr(physical_pages),
+                                                      now_step), "restore_batch")
+
+    def tier_of(self, block_id) -> str:
+        return TIER_NAMES[_rt_check(runtime().cbis_tiered_tier_of(self._h, block_id), "tier_of")]
+
+    def known(self, block_id) -> bool:
+        return bool(runtime().cbis_tiered_known(self._h, block_id))
+
+    def touch(self, block_id, now_step):
+        _rt_check(runtime().cbis_tiered_touch(self._h, block_id, now_step), "touch")
+
+    def stats(self) -> dict:
+        out = (_SZ * 5)()
+        _rt_check(runtime().cbis_tiered_stats(self._h, out), "stats")
+        return dict(zip(("gpu_count", "dram_count", "nvme_count", "raw_bytes_total", "compressed_bytes_total"),
+                        list(out)))
+
+
+def block_deflate(data: bytes) -> bytes:
+    cap = len(data) + len(data) // 1000 + 64
+    buf = ctypes.create_string_buffer(cap)
+    n = runtime().cbis_block_deflate(data, len(data), buf, cap)
+    if n < 0:
+        _rt_check(-1, "block_deflate")
+    return buf.raw[:n]
+
+
+def block_inflate(comp: bytes, out_len: int) -> bytes:
+    buf = ctypes.create_string_buffer(max(1, out_len))
+    _rt_check(runtime().cbis_block_inflate(comp, len(comp), buf, out_len), "block_inflate")
+    return buf.raw[:out_len]
 
 
 def run_continuous(runner: TransformerRunner, cache: PagedKVCache, prompts, decode_lens, max_slots=16,

@@ -17,6 +17,9 @@ struct cbis_weights {
 struct cbis_runner {
   std::unique_ptr<TransformerRunner> impl;
 };
+struct cbis_tiered {
+  std::unique_ptr<TieredKVBlockManager> impl;
+};
 
 namespace {
 thread_local std::string g_err;
@@ -318,6 +321,164 @@ int cbis_schedule_dry_run(cbis_cache* c, int n_requests, const int* prompt_lens,
       }
     }
     return (int)trace.size();
+  });
+}
+
+namespace {
+Tier to_tier(int t) {
+  if (t < 0 || t > 2) throw std::invalid_argument("tier must be 0 (GPU), 1 (DRAM) or 2 (NVME)");
+  return (Tier)t;
+}
+EvictionParams to_params(const cbis_eviction_params* p) {
+  EvictionParams e;
+  if (p) {
+    e.alpha_staleness = p->alpha_staleness;
+    e.beta_restore_cost = p->beta_restore_cost;
+    e.expected_compression_ratio = p->expected_compression_ratio;
+    e.dram_fixed_ns = p->dram_fixed_ns;
+    e.dram_ns_per_byte = p->dram_ns_per_byte;
+    e.nvme_fixed_ns = p->nvme_fixed_ns;
+    e.nvme_ns_per_byte = p->nvme_ns_per_byte;
+  }
+  return e;
+}
+void from_params(const EvictionParams& e, cbis_eviction_params* p) {
+  *p = {e.alpha_staleness, e.beta_restore_cost, e.expected_compression_ratio, e.dram_fixed_ns,
+        e.dram_ns_per_byte, e.nvme_fixed_ns, e.nvme_ns_per_byte};
+}
+}  // namespace
+
+void cbis_eviction_params_default(cbis_eviction_params* p) {
+  if (p) from_params(EvictionParams(), p);
+}
+
+cbis_tiered* cbis_tiered_create(int layer_count, int page_size, int n_heads, int head_dim, int kv_dtype,
+                                const char* nvme_scratch_path, size_t gpu_capacity_blocks,
+                                size_t dram_capacity_blocks, const cbis_eviction_params* params) {
+  return guard_ptr<cbis_tiered>([&] {
+    auto* t = new cbis_tiered();
+    try {
+      t->impl.reset(new TieredKVBlockManager(layer_count, page_size, n_heads, head_dim,
+                                             nvme_scratch_path ? nvme_scratch_path : "", gpu_capacity_blocks,
+                                             dram_capacity_blocks, to_params(params), kv_dtype));
+    } catch (...) {
+      delete t;
+      throw;
+    }
+    return t;
+  });
+}
+
+void cbis_tiered_destroy(cbis_tiered* t) { delete t; }
+
+size_t cbis_tiered_raw_block_bytes(const cbis_tiered* t) { return t->impl->raw_block_bytes(); }
+
+int cbis_tiered_calibrate(cbis_tiered* t) {
+  return guard([&] {
+    t->impl->calibrate();
+    return 0;
+  });
+}
+
+int cbis_tiered_params(const cbis_tiered* t, cbis_eviction_params* out) {
+  return guard([&] {
+    if (!out) throw std::invalid_argument("params: null output");
+    from_params(t->impl->params(), out);
+    return 0;
+  });
+}
+
+int cbis_tiered_admit_gpu_resident(cbis_tiered* t, uint64_t block_id, cbis_cache* c, int physical_page,
+                                   long now_step) {
+  return guard([&] {
+    t->impl->admit_gpu_resident(block_id, *c->impl, physical_page, now_step);
+    return 0;
+  });
+}
+
+int cbis_tiered_evict_one(cbis_tiered* t, long now_step, uint64_t* evicted) {
+  return guard([&] {
+    const uint64_t id = t->impl->evict_one(now_step);
+    if (evicted) *evicted = id;
+    return 0;
+  });
+}
+
+int cbis_tiered_spill(cbis_tiered* t, uint64_t block_id, int dest_tier, long now_step) {
+  return guard([&] {
+    t->impl->spill(block_id, to_tier(dest_tier), now_step);
+    return 0;
+  });
+}
+
+int cbis_tiered_restore(cbis_tiered* t, uint64_t block_id, cbis_cache* c, int physical_page, long now_step) {
+  return guard([&] {
+    t->impl->restore(block_id, *c->impl, physical_page, now_step);
+    return 0;
+  });
+}
+
+int cbis_tiered_spill_batch(cbis_tiered* t, const uint64_t* block_ids, int n, int dest_tier, long now_step) {
+  return guard([&] {
+    if (n < 0 || (n > 0 && !block_ids)) throw std::invalid_argument("spill_batch: bad block list");
+    t->impl->spill_batch(std::vector<uint64_t>(block_ids, block_ids + n), to_tier(dest_tier), now_step);
+    return 0;
+  });
+}
+
+int cbis_tiered_restore_batch(cbis_tiered* t, const uint64_t* block_ids, int n, cbis_cache* c,
+                              const int* physical_pages, long now_step) {
+  return guard([&] {
+    if (n < 0 || (n > 0 && (!block_ids || !physical_pages)))
+      throw std::invalid_argument("restore_batch: bad block list");
+    t->impl->restore_batch(std::vector<uint64_t>(block_ids, block_ids + n), *c->impl,
+                           std::vector<int>(physical_pages, physical_pages + n), now_step);
+    return 0;
+  });
+}
+
+int cbis_tiered_tier_of(const cbis_tiered* t, uint64_t block_id) {
+  return guard([&] { return (int)t->impl->tier_of(block_id); });
+}
+
+int cbis_tiered_known(const cbis_tiered* t, uint64_t block_id) { return t->impl->known(block_id) ? 1 : 0; }
+
+int cbis_tiered_touch(cbis_tiered* t, uint64_t block_id, long now_step) {
+  return guard([&] {
+    t->impl->touch(block_id, now_step);
+    return 0;
+  });
+}
+
+int cbis_tiered_stats(const cbis_tiered* t, size_t* out) {
+  return guard([&] {
+    if (!out) throw std::invalid_argument("stats: null output");
+    const BlockStats s = t->impl->stats();
+    out[0] = s.gpu_count;
+    out[1] = s.dram_count;
+    out[2] = s.nvme_count;
+    out[3] = s.raw_bytes_total;
+    out[4] = s.compressed_bytes_total;
+    return 0;
+  });
+}
+
+int64_t cbis_block_deflate(const void* src, size_t len, void* dst, size_t cap) {
+  int64_t r = -1;
+  const int rc = guard([&] {
+    const std::vector<uint8_t> c = deflate_block(src, len);
+    if (c.size() > cap) throw std::length_error("block_deflate: output capacity too small");
+    std::memcpy(dst, c.data(), c.size());
+    r = (int64_t)c.size();
+    return 0;
+  });
+  return rc < 0 ? rc : r;
+}
+
+int cbis_block_inflate(const void* src, size_t len, void* dst, size_t out_len) {
+  return guard([&] {
+    inflate_block((const uint8_t*)src, len, dst, out_len);
+    return 0;
   });
 }
 

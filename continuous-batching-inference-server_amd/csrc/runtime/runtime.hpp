@@ -214,6 +214,121 @@ class TransformerRunner {
 };
 
 // ---------------------------------------------------------------------------
+// Three-tier KV block manager (include/tiered_kv_manager.hpp,
+// include/block_storage.hpp): a block is one physical page's K and V slots in
+// every layer; GPU-resident blocks live in a PagedKVCache, colder blocks are
+// deflated (zlib, fastest level) into host DRAM or an append-only file.
+// Same API and eviction policy as the reference; batch spill / restore move
+// every block of a call with one gather / scatter launch and one host copy.
+// ---------------------------------------------------------------------------
+enum class Tier { GPU = 0, DRAM = 1, NVME = 2 };
+
+struct EvictionParams {
+  double alpha_staleness = 1.0;             // weight on steps since last access
+  double beta_restore_cost = 1.0;           // weight on the estimated restore cost (ns)
+  double expected_compression_ratio = 0.5;  // compressed / raw
+  double dram_fixed_ns = 2000.0;
+  double dram_ns_per_byte = 0.05;           // calibrate() measures H2D + D2H
+  double nvme_fixed_ns = 50000.0;
+  double nvme_ns_per_byte = 0.2;            // calibrate() measures file write + read
+};
+
+struct BlockStats {
+  size_t gpu_count = 0, dram_count = 0, nvme_count = 0;
+  size_t raw_bytes_total = 0;
+  size_t compressed_bytes_total = 0;  // DRAM + NVMe blocks
+};
+
+std::vector<uint8_t> deflate_block(const void* data, size_t len);
+void inflate_block(const uint8_t* comp, size_t comp_len, void* out, size_t out_len);
+
+// Append-only single-file blob store (pwrite / pread on one descriptor).
+class NvmeBlockStore {
+ public:
+  struct Loc {
+    uint64_t offset = 0;
+    uint32_t length = 0;
+  };
+  explicit NvmeBlockStore(const std::string& path);
+  ~NvmeBlockStore();
+  NvmeBlockStore(const NvmeBlockStore&) = delete;
+  NvmeBlockStore& operator=(const NvmeBlockStore&) = delete;
+  Loc write_block(const uint8_t* data, uint32_t length);
+  void read_block(Loc loc, uint8_t* out) const;
+  std::vector<uint8_t> read_block(Loc loc) const;
+  uint64_t bytes_written() const { return next_; }
+  const std::string& path() const { return path_; }
+
+ private:
+  std::string path_;
+  int fd_ = -1;
+  uint64_t next_ = 0;
+};
+
+class TieredKVBlockManager {
+ public:
+  TieredKVBlockManager(int layer_count, int page_size, int n_heads, int head_dim, const std::string& nvme_scratch_path,
+                       size_t gpu_capacity_blocks, size_t dram_capacity_blocks, EvictionParams params = {},
+                       int kv_dtype = CBIS_F32);
+  ~TieredKVBlockManager();
+  TieredKVBlockManager(const TieredKVBlockManager&) = delete;
+  TieredKVBlockManager& operator=(const TieredKVBlockManager&) = delete;
+
+  size_t raw_block_bytes() const { return raw_block_bytes_; }
+  const EvictionParams& params() const { return params_; }
+  void calibrate();
+
+  void admit_gpu_resident(uint64_t block_id, PagedKVCache& cache, int physical_page, long now_step);
+  uint64_t evict_one(long now_step);  // UINT64_MAX when no block is GPU-resident
+  void spill(uint64_t block_id, Tier dest, long now_step);
+  void restore(uint64_t block_id, PagedKVCache& cache, int physical_page, long now_step);
+  // Batches: the blocks' bytes move with one gather (spill) or scatter
+  // (restore) launch and one host copy; per-block bookkeeping, and the
+  // evictions a restore triggers, happen in the order of `ids`.
+  void spill_batch(const std::vector<uint64_t>& ids, Tier dest, long now_step);
+  void restore_batch(const std::vector<uint64_t>& ids, PagedKVCache& cache, const std::vector<int>& pages,
+                     long now_step);
+
+  Tier tier_of(uint64_t block_id) const;
+  void touch(uint64_t block_id, long now_step);
+  bool known(uint64_t block_id) const { return meta_.count(block_id) != 0; }
+  BlockStats stats() const;
+
+ private:
+  struct BlockMeta {
+    Tier tier = Tier::GPU;
+    long last_access_step = 0;
+    size_t compressed_bytes = 0;
+    PagedKVCache* cache = nullptr;
+    int physical_page = -1;
+    std::vector<uint8_t> dram_bytes;
+    NvmeBlockStore::Loc nvme_loc{};
+  };
+  double score(const BlockMeta& m, long now_step, Tier dest) const;
+  void check_cache(const PagedKVCache& cache) const;
+  // Device <-> pinned host: every listed page of `cache` into / out of
+  // host_stage_ (block i at i * raw_block_bytes_).
+  void gather_to_host(PagedKVCache& cache, const std::vector<int>& pages);
+  void scatter_from_host(PagedKVCache& cache, const std::vector<int>& pages);
+  void reserve(size_t blocks);
+
+  int layer_count_, page_size_, n_heads_, head_dim_, kv_dtype_;
+  size_t page_bytes_, raw_block_bytes_;
+  size_t gpu_capacity_blocks_, dram_capacity_blocks_;
+  EvictionParams params_;
+  NvmeBlockStore nvme_;
+  hipStream_t stream_ = nullptr;
+  size_t stage_blocks_ = 0;
+  uint8_t* host_stage_ = nullptr;  // pinned
+  uint8_t* dev_stage_ = nullptr;
+  int* host_pages_ = nullptr;      // pinned
+  int* dev_pages_ = nullptr;
+  std::map<uint64_t, BlockMeta> meta_;
+  size_t gpu_resident_count_ = 0;
+  size_t dram_resident_count_ = 0;
+};
+
+// ---------------------------------------------------------------------------
 // Continuous batching (src/bench_batching.cpp:98-179), all requests present
 // at t = 0.
 // ---------------------------------------------------------------------------

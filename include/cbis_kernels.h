@@ -211,6 +211,23 @@ int cbis_argmax_rows(int T, int N, const float* logits, int64_t ld, int* out, cb
 int cbis_fill_normal_exact(void* dst, int dtype, int64_t n, uint64_t seed, uint64_t stream_id,
                            uint64_t start, float std, cbis_stream_t stream);
 
+/* ---- Tiered-cache block movement -------------------------------------- */
+/* Gathers whole pages of a paged K/V allocation laid out
+ * [n_layers][2 (K, V)][max_pages][page_bytes] (PagedKVCache's single device
+ * allocation) into block-major staging [n_pages][n_layers][2][page_bytes]:
+ * block b = every layer's K and V page pages[b], in the byte order of one
+ * block of the reference's tiered cache.  Replaces read_raw_from_gpu
+ * (src/tiered_kv_manager.cpp:69-82, 2 * n_layers copies per block) with one
+ * launch per batch.  pages: device int32[n_pages]; page ids outside
+ * [0, max_pages) are skipped (callers validate them); page_bytes a multiple
+ * of 16; staging / pools 16-byte aligned. */
+int cbis_kv_pages_gather(void* staging, const void* pools, int n_layers, int max_pages, int64_t page_bytes,
+                         const int* pages, int n_pages, cbis_stream_t stream);
+/* The inverse: staging block b -> page pages[b] of every layer's K and V
+ * pool (write_raw_to_gpu, src/tiered_kv_manager.cpp:84-98). */
+int cbis_kv_pages_scatter(void* pools, const void* staging, int n_layers, int max_pages, int64_t page_bytes,
+                          const int* pages, int n_pages, cbis_stream_t stream);
+
 /* Fast N(0, std) fill for large synthetic activations / K/V pools:
  * Box-Muller over a 32-bit hash of (seed, index), fp32 or bf16. */
 int cbis_fill_normal_fast(void* dst, int dtype, int64_t n, uint64_t seed, float std, cbis_stream_t stream);

@@ -102,6 +102,52 @@ void* cbis_runner_stream(cbis_runner* r);
 /* Enable / disable HIP-graph replay of steps whose shape repeats. */
 void cbis_runner_set_graphs(cbis_runner* r, int enable);
 
+/* ---- Three-tier KV block manager (include/tiered_kv_manager.hpp:21-151,
+ *      include/block_storage.hpp:9-64) --------------------------------------
+ * A block is one physical page's K and V slots in every layer of a cache;
+ * tiers: 0 GPU (resident in a PagedKVCache page), 1 DRAM (deflated in host
+ * memory), 2 NVMe (deflated in the scratch file).  Same operations, eviction
+ * score and tier choice as the reference; the batch calls move all their
+ * blocks with one gather / scatter launch and one host copy. */
+typedef struct cbis_tiered cbis_tiered;
+typedef struct cbis_eviction_params {
+  double alpha_staleness, beta_restore_cost, expected_compression_ratio;
+  double dram_fixed_ns, dram_ns_per_byte, nvme_fixed_ns, nvme_ns_per_byte;
+} cbis_eviction_params;
+
+/* The reference's defaults (include/tiered_kv_manager.hpp:40-48). */
+void cbis_eviction_params_default(cbis_eviction_params* p);
+/* params may be NULL (defaults).  kv_dtype: CBIS_F32 (the reference's pools)
+ * or CBIS_BF16. */
+cbis_tiered* cbis_tiered_create(int layer_count, int page_size, int n_heads, int head_dim, int kv_dtype,
+                                const char* nvme_scratch_path, size_t gpu_capacity_blocks,
+                                size_t dram_capacity_blocks, const cbis_eviction_params* params);
+void cbis_tiered_destroy(cbis_tiered* t);
+size_t cbis_tiered_raw_block_bytes(const cbis_tiered* t);
+int cbis_tiered_calibrate(cbis_tiered* t);
+int cbis_tiered_params(const cbis_tiered* t, cbis_eviction_params* out);
+int cbis_tiered_admit_gpu_resident(cbis_tiered* t, uint64_t block_id, cbis_cache* c, int physical_page,
+                                   long now_step);
+/* *evicted receives the block id, or UINT64_MAX when no block is on the GPU. */
+int cbis_tiered_evict_one(cbis_tiered* t, long now_step, uint64_t* evicted);
+int cbis_tiered_spill(cbis_tiered* t, uint64_t block_id, int dest_tier, long now_step);
+int cbis_tiered_restore(cbis_tiered* t, uint64_t block_id, cbis_cache* c, int physical_page, long now_step);
+int cbis_tiered_spill_batch(cbis_tiered* t, const uint64_t* block_ids, int n, int dest_tier, long now_step);
+int cbis_tiered_restore_batch(cbis_tiered* t, const uint64_t* block_ids, int n, cbis_cache* c,
+                              const int* physical_pages, long now_step);
+/* Tier (0, 1, 2) of a tracked block; negative for an unknown one. */
+int cbis_tiered_tier_of(const cbis_tiered* t, uint64_t block_id);
+int cbis_tiered_known(const cbis_tiered* t, uint64_t block_id);
+int cbis_tiered_touch(cbis_tiered* t, uint64_t block_id, long now_step);
+/* out[5] = GPU, DRAM, NVMe block counts, raw bytes, compressed bytes. */
+int cbis_tiered_stats(const cbis_tiered* t, size_t* out);
+
+/* Host-only block codec of the colder tiers (zlib deflate, fastest level):
+ * returns the compressed length (<= cap), or negative. */
+int64_t cbis_block_deflate(const void* src, size_t len, void* dst, size_t cap);
+/* Inflates exactly out_len bytes; 0 or negative. */
+int cbis_block_inflate(const void* src, size_t len, void* dst, size_t out_len);
+
 /* ---- continuous batching (src/bench_batching.cpp:98-179) ---------------- */
 /* All requests are present at t = 0.  prompt_tokens concatenates the
  * prompts; out_tokens receives decode_lens[i] tokens per request,
