@@ -20,8 +20,9 @@ on the host on one layer of the same step plus lm_head, scaled to 16 layers.
 
 Other modes: --config c1 (tiny fp32 GPT greedy continuous batching),
 --config c2 (the isolated linear layers), --config c3 (paged decode
-attention alone), --config c5 (long-context fp8 decode); --copy-calib (a
-plain device copy for PMC byte calibration).
+attention alone), --config c5 (long-context fp8 decode), --config gemm
+(config 4's GEMM shapes alone), --config tiering (the tiered K/V prefix
+restore); --copy-calib (a plain device copy for PMC byte calibration).
 """
 import argparse
 import ctypes
@@ -628,6 +629,71 @@ def run_gemm_shapes(args, cbis, oracle):
             "cpu_baseline": None}
 
 
+def run_tiering(args, cbis, oracle):
+    """The reference's tiering scenario (src/bench_tiering.cpp): a
+    32768-token prefix of the reference model (4 layers, 8x32 heads, fp32
+    K/V: 2048 blocks of 128 KiB) spilled from the GPU to the DRAM tier and
+    restored into fresh pages.  value = restored raw bytes per second of the
+    batched restore (inflate on the host cores + one pinned H2D copy + one
+    scatter launch per 256 MiB chunk); beside it the same restore one block
+    per call (the reference's loop), the batched spill, and the scatter
+    kernel alone (roofline: HBM, bytes read + written per launch)."""
+    import tempfile
+    import torch
+    L, H, HD, PS, NB = 4, 8, 32, 16, 2048
+    cache = cbis.PagedKVCache(L, 2 * NB, PS, H, HD, "f32", pages_per_seq=NB)
+    cache.fill_normal(seed=11, std=1.0)
+    tmp = tempfile.mkdtemp(prefix="cbis_tier_")
+    mgr = cbis.TieredKVBlockManager(L, PS, H, HD, os.path.join(tmp, "scratch.nvme"), NB, NB)
+    raw = mgr.raw_block_bytes()
+    ids = list(range(NB))
+    for b in ids:
+        mgr.admit_gpu_resident(b, cache, b, 0)
+    t0 = time.perf_counter()
+    mgr.spill_batch(ids, "DRAM", 1)
+    spill_s = time.perf_counter() - t0
+    comp = mgr.stats()["compressed_bytes_total"]
+    t0 = time.perf_counter()
+    mgr.restore_batch(ids, cache, [NB + b for b in ids], 2)
+    batch_s = time.perf_counter() - t0
+    mgr.spill_batch(ids, "DRAM", 3)
+    t0 = time.perf_counter()
+    for b in ids:
+        mgr.restore(b, cache, b, 4)
+    single_s = time.perf_counter() - t0
+    mgr.close()
+    # the scatter kernel alone, device staging -> pages NB..2NB-1
+    K_ = cbis.kernels()
+    page_bytes = PS * H * HD * 4
+    stage = torch.empty(NB * raw, dtype=torch.uint8, device="cuda:0")
+    pages = torch.arange(NB, 2 * NB, dtype=torch.int32, device="cuda:0")
+    ev = Events(None)
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lambda: cbis.check(K_.cbis_kv_pages_scatter(cache.k_base(0), stage.data_ptr(), L, 2 * NB, page_bytes,
+                                                     pages.data_ptr(), NB, stream))
+    ev.time(fn, max(1, args.warmup))
+    ms = ev.time(fn, max(5, args.steps))
+    kbytes = 2.0 * NB * raw
+    kgbs = kbytes / ms / 1e6
+    total = NB * raw
+    value = total / batch_s / 1e9
+    _log(f"tiering: spill {spill_s * 1e3:.1f} ms, batched restore {batch_s * 1e3:.1f} ms, "
+         f"one-block restores {single_s * 1e3:.1f} ms, scatter kernel {ms * 1e3:.1f} us = {kgbs:.0f} GB/s")
+    return {"metric": "DRAM-tier restore GB/s (raw K/V bytes) of a 2048-block prefix", "value": round(value, 2),
+            "unit": "GB/s", "ms_per_step": round(batch_s * 1e3, 2), "dtype": "f32 K/V bytes (lossless)",
+            "data": "synthetic (K/V N(0,1))",
+            "config": {"workload": "tiering_prefix_restore", "blocks": NB, "block_bytes": raw,
+                       "layers": L, "heads": f"{H}x{HD}", "page_size": PS,
+                       "compressed_ratio": round(comp / total, 4),
+                       "spill_ms": round(spill_s * 1e3, 2), "batched_restore_ms": round(batch_s * 1e3, 2),
+                       "one_block_restores_ms": round(single_s * 1e3, 2),
+                       "host_threads": int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()},
+            "roofline": {"bound": "hbm", "kernel": "kv_pages_kernel<scatter>", "achieved": round(kgbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algorithmic_bytes": int(kbytes), "ms": round(ms, 4)},
+            "cpu_baseline": None}
+
+
 def run_copy_calib(args):
     """A plain device-to-device copy of known size for PMC byte calibration."""
     import torch
@@ -645,9 +711,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c2", "c3", "c5", "gemm"],
+    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c2", "c3", "c5", "gemm", "tiering"],
                     help="c4: the bench line (default); c1 / c2 / c3 / c5: the other BASELINE configs; "
-                         "gemm: config 4's GEMM shapes alone")
+                         "gemm: config 4's GEMM shapes alone; tiering: the tiered K/V prefix restore")
     ap.add_argument("--shapes", default=None, help="--config gemm: comma list of qkv,out,fc1,fc2,lm_head")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calib", action="store_true")
@@ -665,7 +731,7 @@ def main():
     import oracle
     if args.config != "c4":
         res = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c5": run_c5,
-               "gemm": run_gemm_shapes}[args.config](args, cbis, oracle)
+               "gemm": run_gemm_shapes, "tiering": run_tiering}[args.config](args, cbis, oracle)
         line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
                 "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
                 "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"], "data": res["data"],
