@@ -114,6 +114,15 @@ struct WLoad<uint8_t> {
 // 64 banks) per cycle; the 16 lanes of a fragment load read one chunk of 16
 // consecutive rows, i.e. 8 even rows in bytes 0-127 and 8 odd rows in bytes
 // 128-255 of the 64 banks, each set in 8 distinct slots: no bank conflicts.
+// Workgroup b is dispatched to XCD b % 8 (measured on gfx950 from the
+// XCC_ID hardware register).  Renumbering so that each XCD's workgroups take
+// one contiguous run of tiles (M fastest) keeps an XCD on few W columns, so
+// its 4 MB L2 serves the repeats instead of every XCD streaming all of W.
+__device__ inline int xcd_contiguous(int bid, int nwg) {
+  const int q = nwg >> 3, r = nwg & 7, x = bid & 7;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + (bid >> 3);
+}
+
 __device__ inline int swz_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 __device__ inline int swz(int row, int chunk) { return row * 128 + (swz_slot(row, chunk) << 4); }
 
@@ -138,7 +147,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
   const int mt = (g.M + BM - 1) / BM;
   const int nwg = gridDim.x;
   int bid = blockIdx.x;
-  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  bid = xcd_contiguous(bid, nwg);
   const int tm = bid % mt, tn = bid / mt;
   const int m0 = tm * BM, n0 = tn * BN;
   const int kz = blockIdx.z;
@@ -340,7 +349,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmAr
   const int mt = (g.M + BM - 1) / BM;
   const int nwg = gridDim.x;
   int bid = blockIdx.x;
-  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  bid = xcd_contiguous(bid, nwg);
   const int tm = bid % mt, tn = bid / mt;
   const int m0 = tm * BM, n0 = tn * BN;
   const int kz = blockIdx.z;
