@@ -78,6 +78,63 @@ __device__ inline void epilogue_store(const GemmArgs& g, int row, int col, float
   else ((float*)g.Y)[o] = v;
 }
 
+// Epilogue of one 32 x 32 MFMA block: this lane holds column `col` of rows
+// rb + 8 * (e / 4) + (e % 4), e = 0..15, handled four rows at a time.  The
+// four rows' inputs (residual, K/V slot ids) are loaded before their stores:
+// Y may alias the residual (x += ...), so loads interleaved with stores
+// would be issued one round trip at a time.  The channel scale and bias are
+// loaded once.  With ksplit > 1 the raw sums go to the partials.
+__device__ inline void epilogue_block(const GemmArgs& g, int kz, int rb, int col, const f32x16_t& acc) {
+  if (col >= g.N) return;
+  const float sc = g.w_scale ? g.w_scale[col] : 1.f;
+  const float bi = g.bias ? g.bias[col] : 0.f;
+  const bool kv = g.k_pool && col >= g.kv_col0;
+  const int c = col - g.kv_col0;
+  const bool is_v = kv && c >= g.kv_width;
+  const int ce = is_v ? c - g.kv_width : c;
+  void* pool = is_v ? g.v_pool : g.k_pool;
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    const int r0 = rb + 8 * qd;
+    bool ok[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ok[e] = r0 + e < g.M;
+    if (g.ksplit > 1) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (ok[e]) g.partial[((int64_t)kz * g.M + r0 + e) * g.N + col] = acc[4 * qd + e];
+      continue;
+    }
+    float v[4], r[4];
+    int64_t off[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[e] = (g.residual && ok[e]) ? g.residual[(int64_t)(r0 + e) * g.ldr + col] : 0.f;
+      off[e] = (kv && ok[e]) ? ((int64_t)g.wpage[r0 + e] * g.page_size + g.woff[r0 + e]) * g.kv_width + ce : 0;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = acc[4 * qd + e];
+      if (g.w_scale) v[e] *= sc;
+      if (g.bias) v[e] += bi;
+      if (g.gelu) v[e] = gelu_erf(v[e]);
+      if (g.residual) v[e] += r[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (!ok[e]) continue;
+      if (kv) {
+        if (g.kv_bf16) ((uint16_t*)pool)[off[e]] = f32_to_bf16(v[e]);
+        else ((float*)pool)[off[e]] = v[e];
+      } else {
+        const int64_t o = (int64_t)(r0 + e) * g.ldy + col;
+        if (g.y_bf16) ((uint16_t*)g.Y)[o] = f32_to_bf16(v[e]);
+        else ((float*)g.Y)[o] = v[e];
+      }
+    }
+  }
+}
+
 template <typename WT>
 struct WLoad;  // global W chunk (covering 16 bytes of LDS) -> uint4 of the compute type
 template <>
@@ -253,20 +310,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
   // Epilogue straight from the accumulators: acc[i][j][e] is row
   // 8*(e/4) + 4*half + (e%4), column l32 of block (i, j).
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int col = n0 + wn * TN + j * 32 + l32;
-      if (col >= g.N) continue;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-        if (row >= g.M) continue;
-        if (g.ksplit > 1) g.partial[((int64_t)kz * g.M + row) * g.N + col] = acc[i][j][e];
-        else epilogue_store(g, row, col, acc[i][j][e]);
-      }
-    }
-  }
+    for (int j = 0; j < FN; ++j)
+      epilogue_block(g, kz, m0 + wm * TM + i * 32 + 4 * half, n0 + wn * TN + j * 32 + l32, acc[i][j]);
 }
 
 // Sums the split-K partials (fixed order) and applies the epilogue; four
@@ -461,20 +508,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmAr
   }
 
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int col = n0 + wn * TN + j * 32 + l32;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-        if (col < g.N && row < g.M) {
-          if (g.ksplit > 1) g.partial[((int64_t)kz * g.M + row) * g.N + col] = acc[i][j][e];
-          else epilogue_store(g, row, col, acc[i][j][e]);
-        }
-      }
-    }
-  }
+    for (int j = 0; j < FN; ++j)
+      epilogue_block(g, kz, m0 + wm * TM + i * 32 + 4 * half, n0 + wn * TN + j * 32 + l32, acc[i][j]);
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES>

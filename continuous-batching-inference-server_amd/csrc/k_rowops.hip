@@ -78,14 +78,19 @@ __global__ __launch_bounds__(256) void layernorm_kernel(int T, int D, const floa
   if (row >= T) return;
   const int lane = threadIdx.x & 63;
   const float* x = X + (int64_t)row * ldx;
-  float4 v[VPL];
-  float s = 0.f;
+  float4 v[VPL], gg[VPL], bb[VPL];
+  // gamma / beta are loaded with the row, not after the two reductions, so
+  // the kernel pays one memory round trip before its stores.
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = (i * 64 + lane) * 4;
     v[i] = c < D ? *(const float4*)(x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    gg[i] = c < D ? *(const float4*)(g + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    bb[i] = c < D ? *(const float4*)(b + c) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
   const float mean = wave_sum(s) / (float)D;
   float q = 0.f;
 #pragma unroll
@@ -102,12 +107,10 @@ __global__ __launch_bounds__(256) void layernorm_kernel(int T, int D, const floa
   for (int i = 0; i < VPL; ++i) {
     const int c = (i * 64 + lane) * 4;
     if (c >= D) continue;
-    const float4 gg = *(const float4*)(g + c);
-    const float4 bb = *(const float4*)(b + c);
-    const float o0 = (v[i].x - mean) * inv * gg.x + bb.x;
-    const float o1 = (v[i].y - mean) * inv * gg.y + bb.y;
-    const float o2 = (v[i].z - mean) * inv * gg.z + bb.z;
-    const float o3 = (v[i].w - mean) * inv * gg.w + bb.w;
+    const float o0 = (v[i].x - mean) * inv * gg[i].x + bb[i].x;
+    const float o1 = (v[i].y - mean) * inv * gg[i].y + bb[i].y;
+    const float o2 = (v[i].z - mean) * inv * gg[i].z + bb[i].z;
+    const float o3 = (v[i].w - mean) * inv * gg[i].w + bb[i].w;
     if constexpr (sizeof(YT) == 4) {
       *(float4*)(y + c) = make_float4(o0, o1, o2, o3);
     } else {
