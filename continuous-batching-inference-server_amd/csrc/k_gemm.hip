@@ -55,7 +55,24 @@ struct GemmArgs {
   float* partial; // [ksplit][M][N] when ksplit > 1
 };
 
-__device__ inline float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f)); }
+// Exact-form GELU 0.5 v (1 + erf(v / sqrt 2)) (kernels/elementwise.cu:64),
+// with erf from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7):
+//   erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
+//   t = 1 / (1 + p z), z >= 0, odd extension for z < 0.
+// A dozen VALU ops against the libm erff's range-split polynomial; the GELU
+// error it adds (<= 0.75e-7 |v|) is far below the fp32 rounding of the
+// GEMM that feeds it.
+__device__ inline float gelu_erf(float v) {
+  const float z = fabsf(v) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  float poly = fmaf(t, 1.061405429f, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  poly *= t;
+  const float erf_abs = 1.0f - poly * fast_exp2(-(z * z) * kLog2e);
+  return 0.5f * v * (1.0f + copysignf(erf_abs, v));
+}
 
 // Applies the epilogue to one accumulator and stores it.
 __device__ inline void epilogue_store(const GemmArgs& g, int row, int col, float v) {
@@ -93,6 +110,10 @@ __device__ inline void epilogue_block(const GemmArgs& g, int kz, int rb, int col
   const bool is_v = kv && c >= g.kv_width;
   const int ce = is_v ? c - g.kv_width : c;
   void* pool = is_v ? g.v_pool : g.k_pool;
+  // Column pairs (2i, 2i+1) stay together (both < N, same K/V half, 4-byte
+  // aligned destinations) when these are all even.
+  const bool pair_ok = ((g.N | g.ldy) & 1) == 0 && (!g.k_pool || ((g.kv_col0 | g.kv_width) & 1) == 0) &&
+                       (((uintptr_t)g.Y | (uintptr_t)g.k_pool | (uintptr_t)g.v_pool) & 3) == 0;
 #pragma unroll
   for (int qd = 0; qd < 4; ++qd) {
     const int r0 = rb + 8 * qd;
@@ -119,6 +140,25 @@ __device__ inline void epilogue_block(const GemmArgs& g, int kz, int rb, int col
       if (g.bias) v[e] += bi;
       if (g.gelu) v[e] = gelu_erf(v[e]);
       if (g.residual) v[e] += r[e];
+    }
+    const bool bf16_out = kv ? g.kv_bf16 : g.y_bf16;
+    if (bf16_out && pair_ok) {
+      // Lanes 2i and 2i+1 hold adjacent columns: trade values so the even
+      // lane stores rows r0, r0+1 and the odd lane rows r0+2, r0+3 of both
+      // columns as 4-byte bf16 pairs (half the store instructions).
+      const int odd = col & 1;
+      float nb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) nb[e] = __shfl_xor(v[e], 1, 64);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int e = 2 * odd + k;
+        if (!ok[e]) continue;
+        const uint32_t w = odd ? pack_bf16x2(nb[e], v[e]) : pack_bf16x2(v[e], nb[e]);
+        if (kv) *(uint32_t*)((uint16_t*)pool + off[e] - odd) = w;
+        else *(uint32_t*)((uint16_t*)g.Y + (int64_t)(r0 + e) * g.ldy + col - odd) = w;
+      }
+      continue;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {

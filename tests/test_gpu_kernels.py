@@ -159,6 +159,31 @@ def test_gemm_bf16_c4_shapes(cbis, oracle, dev, N, K):
     assert np.abs(Y.cpu().numpy()[rows] - ref).max() < FP32_TOL * 4
 
 
+@pytest.mark.parametrize("M,xdt", [(16, "f32"), (256, "f32"), (16, "bf16"), (256, "bf16")])
+def test_gemm_gelu_epilogue_accuracy(cbis, dev, M, xdt):
+    """The fused GELU against fp64 erf on GEMM outputs that are exact
+    (one non-zero product per output, values from -8 to 8 and around 0):
+    |error| <= 1e-6 (1 + |v|), on the skinny (M=16) and tiled (M=256) paths."""
+    import math
+    import torch
+    from helpers import sync
+    N, K = 64, 64
+    v = np.concatenate([np.linspace(-8, 8, M - 6), [0.0, 1e-4, -1e-4, 0.5, -0.5, 3.0]]).astype(np.float32)
+    if xdt == "bf16":
+        v = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    x = np.zeros((M, K), np.float32); x[:, 0] = v
+    w = np.zeros((N, K), np.float32); w[:, 0] = 1.0
+    dt = torch.float32 if xdt == "f32" else torch.bfloat16
+    X, W = torch.from_numpy(x).to(dev).to(dt), torch.from_numpy(w).to(dev).to(dt)
+    Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    code = cbis.F32 if xdt == "f32" else cbis.BF16
+    _gemm(cbis, M, N, K, X, code, W, code, Y, cbis.F32, gelu=True)
+    sync()
+    ref = np.array([0.5 * a * (1 + math.erf(a / math.sqrt(2))) for a in v.astype(np.float64)])
+    got = Y.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got - ref[:, None]) <= 1e-6 * (1 + np.abs(ref[:, None])))
+
+
 @pytest.mark.parametrize("M", [192, 1216])
 @pytest.mark.parametrize("N,K,gelu", [(2048, 4096, False), (2048, 8192, False), (1024, 4096, True), (1030, 4096, False)])
 def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
