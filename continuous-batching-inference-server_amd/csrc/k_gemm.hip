@@ -889,9 +889,10 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
         g.k_per = p.k_per;
         g.partial = (float*)d->workspace;
       }
-      // Grids that would leave most CUs idle run 64 x 64 tiles (4 waves of
-      // 32 x 32): four times the workgroups.
-      if (g.ksplit == 1 && cdiv(d->M, kDmaBM) * cdiv(d->N, kDmaBN) < kCUs / 2)
+      // Grids with fewer 128 x 128 tiles than CUs run 64 x 64 tiles (4 waves
+      // of 32 x 32): four times the workgroups (config 4's out-projection,
+      // 160 tiles: 28.3 -> 23.4 us).
+      if (g.ksplit == 1 && cdiv(d->M, kDmaBM) * cdiv(d->N, kDmaBN) < kCUs)
         return launch_dma<64, 64, 2, 2, 2>(g, s);
       return launch_dma<kDmaBM, kDmaBN, 2, 4, 2>(g, s);
     }
