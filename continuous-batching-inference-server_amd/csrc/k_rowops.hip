@@ -159,19 +159,53 @@ __device__ inline void argmax_combine(float& v, int& i, float v2, int i2) {
   }
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(int N, const float* __restrict__ L, int64_t ld,
-                                                     int* __restrict__ out) {
+// One 1024-thread workgroup per row.  When the row is 16-byte aligned
+// (N % 4 == 0 and ld % 4 == 0) each thread issues all its float4 loads
+// before comparing, so a 32000-wide row is one round trip of 8 loads per
+// thread; the column order inside a thread does not matter because ties go
+// to the lower index.
+constexpr int kArgmaxThreads = 1024;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int N, const float* __restrict__ L, int64_t ld,
+                                                                int* __restrict__ out) {
   const float* row = L + (int64_t)blockIdx.x * ld;
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
-  for (int c = threadIdx.x; c < N; c += 256) argmax_combine(bv, bi, row[c], c);
+  if (((N | ld) & 3) == 0 && ((uintptr_t)L & 15) == 0) {
+    const int n4 = N >> 2;
+    constexpr int U = 8;
+    int c4 = threadIdx.x;
+    for (; c4 + (U - 1) * kArgmaxThreads < n4; c4 += U * kArgmaxThreads) {
+      f32x4_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load((const f32x4_t*)row + c4 + u * kArgmaxThreads);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = 4 * (c4 + u * kArgmaxThreads);
+        argmax_combine(bv, bi, v[u][0], c);
+        argmax_combine(bv, bi, v[u][1], c + 1);
+        argmax_combine(bv, bi, v[u][2], c + 2);
+        argmax_combine(bv, bi, v[u][3], c + 3);
+      }
+    }
+    for (; c4 < n4; c4 += kArgmaxThreads) {
+      const float4 v = *((const float4*)row + c4);
+      argmax_combine(bv, bi, v.x, 4 * c4);
+      argmax_combine(bv, bi, v.y, 4 * c4 + 1);
+      argmax_combine(bv, bi, v.z, 4 * c4 + 2);
+      argmax_combine(bv, bi, v.w, 4 * c4 + 3);
+    }
+  } else {
+    for (int c = threadIdx.x; c < N; c += kArgmaxThreads) argmax_combine(bv, bi, row[c], c);
+  }
   for (int off = 32; off > 0; off >>= 1) {
     const float v2 = __shfl_xor(bv, off, 64);
     const int i2 = __shfl_xor(bi, off, 64);
     argmax_combine(bv, bi, v2, i2);
   }
-  __shared__ float sv[4];
-  __shared__ int si[4];
+  constexpr int W = kArgmaxThreads / 64;
+  __shared__ float sv[W];
+  __shared__ int si[W];
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     sv[w] = bv;
@@ -179,7 +213,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(int N, const float* __restr
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int k = 1; k < 4; ++k) argmax_combine(bv, bi, sv[k], si[k]);
+    for (int k = 1; k < W; ++k) argmax_combine(bv, bi, sv[k], si[k]);
     // A row that is all -inf (or NaN) keeps index 0, like the sequential scan.
     out[blockIdx.x] = (bi == 0x7FFFFFFF) ? 0 : bi;
   }
@@ -314,7 +348,7 @@ int cbis_argmax_rows(int T, int N, const float* L, int64_t ld, int* out, cbis_st
   CBIS_REQUIRE(T >= 0 && N > 0 && ld >= N, CBIS_ERR_INVALID, "cbis_argmax_rows: bad sizes");
   if (T == 0) return CBIS_OK;
   CBIS_REQUIRE(L && out, CBIS_ERR_INVALID, "cbis_argmax_rows: null pointer");
-  argmax_kernel<<<T, 256, 0, (hipStream_t)stream>>>(N, L, ld, out);
+  argmax_kernel<<<T, kArgmaxThreads, 0, (hipStream_t)stream>>>(N, L, ld, out);
   return check_launch("cbis_argmax_rows");
 }
 

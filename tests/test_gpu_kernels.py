@@ -382,14 +382,17 @@ def test_embed(cbis, oracle, dev, edt):
     assert np.array_equal(out.cpu().numpy(), ref.astype(np.float32))
 
 
-def test_argmax_first_max_wins(cbis, oracle, dev):
+@pytest.mark.parametrize("N", [32000, 1001, 4 * 1024 * 9 + 12])
+def test_argmax_first_max_wins(cbis, oracle, dev, N):
+    """Both load paths (16-byte rows in unrolled float4 rounds plus a tail,
+    and the scalar path for an odd width) against the sequential scan."""
     import torch
-    M, N = 64, 32000
+    M = 64
     L = oracle.normal(18, 1, M * N).reshape(M, N)
     L[0, :] = 1.0                   # all equal -> 0
-    L[1, 5] = L[1, 31999] = 99.0    # tie -> 5
+    L[1, 5] = L[1, N - 1] = 99.0    # tie -> 5
     L[2, :] = -np.inf               # -inf row -> 0
-    L[3, 31999] = 50.0              # last column
+    L[3, N - 1] = 50.0              # last column
     T = to_dev(L, dev)
     out = torch.empty(M, dtype=torch.int32, device=dev)
     cbis.check(cbis.kernels().cbis_argmax_rows(M, N, ptr(T), N, ptr(out), stream()))
