@@ -206,11 +206,6 @@ struct WLoad<uint8_t> {
   }
 };
 
-// LDS image of a 128-byte tile row: 16-byte chunk c of row r sits in slot
-// c ^ ((r >> 1) & 7).  gfx950 serves a ds_read_b128 16 lanes (256 bytes, all
-// 64 banks) per cycle; the 16 lanes of a fragment load read one chunk of 16
-// consecutive rows, i.e. 8 even rows in bytes 0-127 and 8 odd rows in bytes
-// 128-255 of the 64 banks, each set in 8 distinct slots: no bank conflicts.
 // Workgroup b is dispatched to XCD b % 8 (measured on gfx950 from the
 // XCC_ID hardware register).  Renumbering so that each XCD's workgroups take
 // one contiguous run of tiles (M fastest) keeps an XCD on few W columns, so
@@ -220,6 +215,11 @@ __device__ inline int xcd_contiguous(int bid, int nwg) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + (bid >> 3);
 }
 
+// LDS image of a 128-byte tile row: 16-byte chunk c of row r sits in slot
+// c ^ ((r >> 1) & 7).  gfx950 serves a ds_read_b128 16 lanes (256 bytes, all
+// 64 banks) per cycle; the 16 lanes of a fragment load read one chunk of 16
+// consecutive rows, i.e. 8 even rows in bytes 0-127 and 8 odd rows in bytes
+// 128-255 of the 64 banks, each set in 8 distinct slots: no bank conflicts.
 __device__ inline int swz_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 __device__ inline int swz(int row, int chunk) { return row * 128 + (swz_slot(row, chunk) << 4); }
 
