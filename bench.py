@@ -281,6 +281,51 @@ def recorded_traffic(name):
     return None
 
 
+def machine_peaks():
+    """The box's own figures beside the published peaks: CU count and
+    maximum engine clock from rocminfo (bf16 dense MFMA = CUs x 4096 flop/clk
+    x clock), and a measured device-to-device copy (1 GiB read + 1 GiB
+    written) as the practical HBM figure."""
+    import subprocess
+    import torch
+    out = {"published": {"hbm_gbs": HBM_PEAK_GBS, "bf16_tflops": BF16_PEAK_TFLOPS}}
+    try:
+        txt = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60).stdout
+        cus, mhz = None, None
+        for blk in txt.split("*******"):
+            if "gfx950" not in blk:
+                continue
+            for line in blk.splitlines():
+                line = line.strip()
+                if line.startswith("Compute Unit:"):
+                    cus = int(line.split(":")[1])
+                elif line.startswith("Max Clock Freq. (MHz):"):
+                    mhz = int(line.split(":")[1])
+            if cus and mhz:
+                break
+        if cus and mhz:
+            out["rocminfo"] = {"compute_units": cus, "max_clock_mhz": mhz,
+                               "bf16_dense_tflops": round(cus * 4096 * mhz * 1e6 / 1e12, 1)}
+    except Exception as e:  # rocminfo missing or refused: report what is known
+        out["rocminfo"] = f"unavailable ({type(e).__name__})"
+    n = 1 << 28
+    a = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_.record()
+    for _ in range(10):
+        b.copy_(a)
+    e_.record()
+    e_.synchronize()
+    ms = s_.elapsed_time(e_) / 10
+    out["measured_copy_gbs"] = round(2 * n * 4 / ms / 1e6, 1)
+    del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_c4(args, cbis, oracle):
     st = c4_setup(cbis, oracle)
     runner = st["runner"]
@@ -307,7 +352,10 @@ def run_c4(args, cbis, oracle):
     if not args.no_cpu:
         cpu = cpu_baseline_c4(oracle, st, cbis)
         _log(f"cpu baseline: {cpu}")
+    peaks = machine_peaks()
+    _log(f"machine: {json.dumps(peaks)}")
     return {
+        "machine": peaks,
         "metric": "decode tokens/s (config 4 mixed continuous-batch step, mid-size GPT)",
         "value": round(value, 2),
         "unit": "decode tokens/s",
@@ -742,7 +790,8 @@ def main():
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": res["dtype"], "data": res["data"], "config": res["config"],
-            "roofline": res["roofline"], "gemm_roofline": res["gemm_roofline"], "cpu_baseline": res["cpu_baseline"]}
+            "roofline": res["roofline"], "gemm_roofline": res["gemm_roofline"], "cpu_baseline": res["cpu_baseline"],
+            "machine": res["machine"]}
     print(json.dumps(line), flush=True)
 
 
