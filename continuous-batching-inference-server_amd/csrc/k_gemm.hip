@@ -565,6 +565,298 @@ int launch_dma(const GemmArgs& g, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// bf16 x bf16, wave-specialised, for grids of at least half a CU count of
+// 128 x 128 tiles.
+//
+// 8 waves, one workgroup per CU.  Waves 0-3 (one per SIMD) are consumers:
+// they only read fragments from LDS and issue MFMAs, each on a
+// (BM/2) x (BN/2) sub-tile.  Waves 4-7 are producers: they only issue the
+// direct-to-LDS loads of a STAGES-slot ring (same row layout and swizzle as
+// gemm_bf16_dma_kernel) and wait for them, so a load that stalls at issue
+// (the texture path takes a 1 KiB DMA instruction per ~16 cycles per CU)
+// never holds back an MFMA.  One barrier per K tile: before barrier t the
+// producers have waited (vmcnt) for tile t and the consumers have finished
+// their ds_reads of tile t - 1, whose slot the producers refill with tile
+// t - 1 + STAGES right after it.
+//
+// After the K loop the consumers park their accumulators in LDS as a
+// row-major fp32 tile (the ring is free by then) and all 8 waves apply the
+// epilogue row by row, 4 consecutive columns per thread: the channel scale
+// and bias are loaded once per thread, residual / partial accesses are 16
+// bytes and bf16 / K/V stores 8 bytes, and every thread loads the inputs of
+// 4 rows before storing them (Y may alias the residual).
+// ---------------------------------------------------------------------------
+constexpr int kWsProducers = 4;
+
+template <int BM, int BN, int STAGES>
+struct WsTile {
+  static constexpr int TM = BM / 2, TN = BN / 2;
+  static constexpr int FM = TM / 32, FN = TN / 32;
+  static constexpr int ROWS = BM + BN;
+  static constexpr int LPW = ROWS / 8 / kWsProducers;  // 1 KiB DMA instructions per producer per tile
+  static constexpr int STAGE_BYTES = ROWS * 128;
+  static constexpr int RING = STAGES * STAGE_BYTES;
+  static constexpr int PITCH = BN + 8;                 // floats per parked output row
+  static constexpr int PARK = BM * PITCH * 4;
+  static constexpr int LDS = RING > PARK ? RING : PARK;
+  static_assert(LPW * 8 * kWsProducers == ROWS, "tile rows / producers");
+  static_assert(LPW * (STAGES - 1) < 64, "vmcnt range");
+  static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+// Epilogue over a parked BM x BN fp32 tile by the workgroup's 512 threads.
+template <int BM, int BN>
+__device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* tile, int pitch, int m0, int n0,
+                                     int tid) {
+  constexpr int CG = BN / 4;      // 4-column groups per row
+  constexpr int RPP = 512 / CG;   // rows per pass
+  constexpr int PASSES = BM / RPP;
+  static_assert(RPP * CG == 512 && PASSES % 4 == 0, "epilogue thread map");
+  const int cg = tid % CG, rs = tid / CG;
+  const int col = n0 + 4 * cg;
+  if (col >= g.N) return;
+  const int nc = min(4, g.N - col);
+  float sc[4], bi[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sc[e] = (g.w_scale && e < nc) ? g.w_scale[col + e] : 1.f;
+    bi[e] = (g.bias && e < nc) ? g.bias[col + e] : 0.f;
+  }
+  // Destination of the 4 columns and whether one vector access serves them.
+  const bool split = g.ksplit > 1;
+  const bool to_kv = !split && g.k_pool && col >= g.kv_col0;
+  const int c = col - g.kv_col0;
+  const bool is_v = to_kv && c >= g.kv_width;
+  const int ce = is_v ? c - g.kv_width : c;
+  void* pool = is_v ? g.v_pool : g.k_pool;
+  bool vec = nc == 4;
+  if (split) {
+    vec = vec && (g.N & 3) == 0 && ((uintptr_t)g.partial & 15u) == 0;
+  } else if (to_kv) {
+    vec = vec && (ce & 3) == 0 && ce + 3 < g.kv_width &&
+          ((uintptr_t)pool & (g.kv_bf16 ? 7u : 15u)) == 0 && (g.kv_width & 3) == 0;
+  } else {
+    vec = vec && (!g.k_pool || col + 3 < g.kv_col0) && (g.ldy & 3) == 0 &&
+          ((uintptr_t)g.Y & (g.y_bf16 ? 7u : 15u)) == 0;
+  }
+  const bool res_vec = g.residual && (g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15u) == 0;
+  const bool kv_bf16 = g.kv_bf16, y_bf16 = g.y_bf16;
+
+#pragma unroll 1
+  for (int p0 = 0; p0 < PASSES; p0 += 4) {
+    float v[4][4], r[4][4];
+    int64_t slot[4];
+    bool ok[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int lr = (p0 + q) * RPP + rs;
+      const int row = m0 + lr;
+      ok[q] = row < g.M;
+      const float4 t = *(const float4*)(tile + lr * pitch + 4 * cg);
+      v[q][0] = t.x; v[q][1] = t.y; v[q][2] = t.z; v[q][3] = t.w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[q][e] = 0.f;
+      slot[q] = 0;
+      if (!ok[q] || split) continue;
+      if (g.residual) {
+        const float* rp = g.residual + (int64_t)row * g.ldr + col;
+        if (res_vec && nc == 4) {
+          const float4 rv = *(const float4*)rp;
+          r[q][0] = rv.x; r[q][1] = rv.y; r[q][2] = rv.z; r[q][3] = rv.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < nc) r[q][e] = rp[e];
+        }
+      }
+      if (to_kv) slot[q] = (int64_t)g.wpage[row] * g.page_size + g.woff[row];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (!ok[q]) continue;
+      const int row = m0 + (p0 + q) * RPP + rs;
+      if (split) {
+        float* pp = g.partial + ((int64_t)kz * g.M + row) * g.N + col;
+        if (vec) {
+          *(float4*)pp = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < nc) pp[e] = v[q][e];
+        }
+        continue;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x = v[q][e];
+        if (g.w_scale) x *= sc[e];
+        if (g.bias) x += bi[e];
+        if (g.gelu) x = gelu_erf(x);
+        if (g.residual) x += r[q][e];
+        v[q][e] = x;
+      }
+      if (!vec) {
+        // Mixed or unaligned group: element by element, like epilogue_store
+        // after the scale / bias / GELU / residual above.
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (e >= nc) continue;
+          const int cc = col + e;
+          if (g.k_pool && cc >= g.kv_col0) {
+            const int c2 = cc - g.kv_col0;
+            const bool v2 = c2 >= g.kv_width;
+            const int64_t off = ((int64_t)g.wpage[row] * g.page_size + g.woff[row]) * g.kv_width +
+                                (v2 ? c2 - g.kv_width : c2);
+            void* pl = v2 ? g.v_pool : g.k_pool;
+            if (kv_bf16) ((uint16_t*)pl)[off] = f32_to_bf16(v[q][e]);
+            else ((float*)pl)[off] = v[q][e];
+          } else {
+            const int64_t o = (int64_t)row * g.ldy + cc;
+            if (y_bf16) ((uint16_t*)g.Y)[o] = f32_to_bf16(v[q][e]);
+            else ((float*)g.Y)[o] = v[q][e];
+          }
+        }
+        continue;
+      }
+      const bool bf = to_kv ? kv_bf16 : y_bf16;
+      void* dst = to_kv ? (void*)((char*)pool + (slot[q] * g.kv_width + ce) * (bf ? 2 : 4))
+                        : (void*)((char*)g.Y + ((int64_t)row * g.ldy + col) * (bf ? 2 : 4));
+      if (bf) *(uint2*)dst = make_uint2(pack_bf16x2(v[q][0], v[q][1]), pack_bf16x2(v[q][2], v[q][3]));
+      else *(float4*)dst = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+    }
+  }
+}
+
+template <int BM, int BN, int STAGES>
+__global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
+  typedef WsTile<BM, BN, STAGES> T;
+  constexpr int LPW = T::LPW, STAGE_BYTES = T::STAGE_BYTES, FM = T::FM, FN = T::FN;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::LDS];
+
+  const int mt = (g.M + BM - 1) / BM;
+  const int bid = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int m0 = (bid % mt) * BM, n0 = (bid / mt) * BN;
+  const int kz = blockIdx.z;
+  const int kbeg = kz * g.k_per;
+  const int KT = min(g.k_per, g.K - kbeg) / 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  if (wave >= 4) {
+    // Producer: tile rows p*8*LPW .. of every stage (A rows first, then B).
+    const int p = wave - 4;
+    const uint16_t* src[LPW];
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int rr = (p * LPW + j) * 8 + (lane >> 3);
+      const int chunk = swz_slot(rr, lane & 7);  // the chunk that belongs in slot lane & 7 of row rr
+      if (rr < BM) src[j] = (const uint16_t*)g.X + (int64_t)min(m0 + rr, g.M - 1) * g.ldx + kbeg + chunk * 8;
+      else src[j] = (const uint16_t*)g.W + (int64_t)min(n0 + rr - BM, g.N - 1) * g.ldw + kbeg + chunk * 8;
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+    const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds0 + p * LPW * 1024);
+    auto issue = [&](int kt) {
+      const uint32_t base = wave_lds + (uint32_t)((kt % STAGES) * STAGE_BYTES);
+#pragma unroll
+      for (int j = 0; j < LPW; ++j) lds_dma16(src[j] + kt * 64, base + j * 1024);
+    };
+    // Waits for a tile with `younger` tiles issued after it.
+    auto wait_tile = [&](int younger) {
+      if constexpr (STAGES >= 4) {
+        if (younger >= 3) { wait_vmcnt<3 * LPW>(); return; }
+      }
+      if constexpr (STAGES >= 3) {
+        if (younger >= 2) { wait_vmcnt<2 * LPW>(); return; }
+      }
+      if (younger >= 1) wait_vmcnt<LPW>();
+      else wait_vmcnt<0>();
+    };
+#pragma unroll
+    for (int t = 0; t < STAGES; ++t)
+      if (t < KT) issue(t);
+    wait_tile(min(KT - 1, STAGES - 1));
+    asm volatile("s_barrier" ::: "memory");
+    for (int kt = 0; kt + 1 < KT; ++kt) {
+      wait_tile(min(KT - 1, kt + STAGES - 1) - (kt + 1));
+      asm volatile("s_barrier" ::: "memory");
+      if (kt + STAGES < KT) issue(kt + STAGES);
+    }
+    wait_vmcnt<0>();
+    asm volatile("s_barrier" ::: "memory");  // consumers done with the ring
+    asm volatile("s_barrier" ::: "memory");  // accumulators parked
+  } else {
+    // Consumer: sub-tile (wm, wn) of 2 x 2.
+    __builtin_amdgcn_s_setprio(2);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int half = lane >> 5, l32 = lane & 31;
+    f32x16_t acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    const int a_row0 = (wm * T::TM + l32) * 128;
+    const int b_row0 = (BM + wn * T::TN + l32) * 128;
+    const int sw = (l32 >> 1) & 7;  // swizzle key of every fragment row this lane reads
+    bf16x8_t af[2][FM], bf[2][FN];
+    auto load_frags = [&](int slot, int ks, int fb) {
+      const uint8_t* st = smem + slot * STAGE_BYTES;
+      const int kc = ((2 * ks + half) ^ sw) << 4;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[fb][i] = *(const bf16x8_t*)(st + a_row0 + i * 32 * 128 + kc);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[fb][j] = *(const bf16x8_t*)(st + b_row0 + j * 32 * 128 + kc);
+    };
+    asm volatile("s_barrier" ::: "memory");
+    load_frags(0, 0, 0);
+    for (int kt = 0; kt < KT; ++kt) {
+      const int slot = kt % STAGES;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int fb = ks & 1;
+        if (ks < 3) {
+          load_frags(slot, ks + 1, fb ^ 1);
+        } else if (kt + 1 < KT) {
+          asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+          load_frags((kt + 1) % STAGES, 0, fb ^ 1);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fb][i], bf[fb][j], acc[i][j], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    float* park = (float*)smem;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = wm * T::TM + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+          park[r * T::PITCH + wn * T::TN + j * 32 + l32] = acc[i][j][e];
+        }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+  epilogue_rows<BM, BN>(g, kz, (const float*)smem, T::PITCH, m0, n0, tid);
+}
+
+template <int BM, int BN, int STAGES>
+int launch_ws(const GemmArgs& g, hipStream_t s) {
+  const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
+  gemm_bf16_ws_kernel<BM, BN, STAGES><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
+  int rc = check_launch("cbis_gemm(bf16 ws)");
+  if (rc || g.ksplit <= 1) return rc;
+  splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
+  return check_launch("cbis_gemm(split-k reduce)");
+}
+
+// ---------------------------------------------------------------------------
 // Skinny GEMM for M <= 64 rows (decode steps): weight-streaming on MFMA.
 //
 // A workgroup of 8 waves owns 16 output columns; the waves split K into 8
@@ -762,12 +1054,32 @@ struct SplitPlan {
   int k_per = 0;
 };
 
+// Kernel for a bf16 x bf16 problem on the direct-to-LDS paths, from the
+// tile counts (measured on config 4's shapes at M = 1216):
+//   < kCUs / 2 tiles of 128 x 128: gemm_bf16_dma_kernel, 64 x 64 tiles or
+//     128 x 128 with split-K (plan_dma_split);
+//   < kCUs tiles: wave-specialised 128 x 128, 3 stages (out-projection and
+//     fc2 shapes: 469 and 708 TFLOP/s against 452 and 646);
+//   otherwise wave-specialised 128 x 256 when its tiles fill their last
+//     round of kCUs workgroups to >= 3/4 (qkv 742 against 645, lm_head 796
+//     against 743), else gemm_bf16_dma_kernel 128 x 128 with two workgroups
+//     per CU (fc1: 640 against 623 for 320 tiles of 128 x 256).
+enum class Bf16Path { kSmall, kWs128, kWs256, kDma128 };
+
+Bf16Path choose_bf16(int M, int N) {
+  const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
+  if (t128 < kCUs / 2) return Bf16Path::kSmall;
+  if (t128 < kCUs) return Bf16Path::kWs128;
+  const int64_t last = (cdiv(M, 128) * cdiv(N, 256)) % kCUs;
+  return (last == 0 || 4 * last >= 3 * kCUs) ? Bf16Path::kWs256 : Bf16Path::kDma128;
+}
+
 SplitPlan plan_dma_split(int M, int N, int K) {
   SplitPlan p;
   p.k_per = K;
   const int64_t tiles = cdiv(M, kDmaBM) * cdiv(N, kDmaBN);
   const int kt = K / 64;
-  if (tiles >= kCUs || kt < 64) return p;
+  if (choose_bf16(M, N) != Bf16Path::kSmall || tiles >= kCUs || kt < 64) return p;
   int ks = (int)std::max<int64_t>(2, std::min<int64_t>(4, (2 * kCUs) / tiles));
   ks = std::min(ks, kt / 16);
   if (ks <= 1) return p;
@@ -882,6 +1194,12 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
   if (d->w_dtype == CBIS_BF16) {
     // The direct-to-LDS path needs 16-byte aligned rows of both operands.
     if (dma_eligible(d)) {
+      switch (choose_bf16(d->M, d->N)) {
+        case Bf16Path::kWs256: return launch_ws<128, 256, 3>(g, s);
+        case Bf16Path::kWs128: return launch_ws<128, 128, 3>(g, s);
+        case Bf16Path::kDma128: return launch_dma<kDmaBM, kDmaBN, 2, 4, 2>(g, s);
+        case Bf16Path::kSmall: break;
+      }
       const SplitPlan p = plan_dma_split(d->M, d->N, d->K);
       const size_t need = (size_t)p.ksplit * d->M * d->N * sizeof(float);
       if (p.ksplit > 1 && d->workspace && d->workspace_bytes >= need) {

@@ -185,11 +185,15 @@ def test_gemm_gelu_epilogue_accuracy(cbis, dev, M, xdt):
 
 
 @pytest.mark.parametrize("M", [192, 1216])
-@pytest.mark.parametrize("N,K,gelu", [(2048, 4096, False), (2048, 8192, False), (1024, 4096, True), (1030, 4096, False)])
+@pytest.mark.parametrize("N,K,gelu", [(2048, 4096, False), (2048, 8192, False), (1024, 4096, True), (1030, 4096, False),
+                                      (2050, 4096, False)])
 def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
-    """Split-K (fp32 partials in a caller workspace, reduce + epilogue) on the
-    shapes whose output tiles cannot fill the GPU: bias, GELU, and a residual
-    that aliases Y, against the fp64 oracle; the split must engage."""
+    """Bias, GELU, and a residual that aliases Y, against the fp64 oracle, on
+    the two bf16 tiled paths: grids of fewer than 128 tiles of 128 x 128
+    cannot fill the GPU and split-K (fp32 partials in a caller workspace,
+    reduce + epilogue) must engage; larger ones (M=1216 with N=2048 or 2050)
+    run the wave-specialised kernel whole-K (no workspace) with its row-wise
+    epilogue, N=2050 ending in a ragged column group."""
     import torch
     X, x = bf16_dev(oracle.normal(15, 1, M * K).reshape(M, K), dev)
     W, w = bf16_dev(oracle.normal(15, 2, N * K, 0.02).reshape(N, K), dev)
@@ -199,7 +203,7 @@ def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
     Y = to_dev(r, dev) if r is not None else torch.empty((M, N), dtype=torch.float32, device=dev)
     used = _gemm(cbis, M, N, K, X, cbis.BF16, W, cbis.BF16, Y, cbis.F32, bias=B, gelu=gelu,
                  residual=Y if r is not None else None, workspace=True)
-    assert used > 0
+    assert (used > 0) == (-(-M // 128) * -(-N // 128) < 128)
     rows = _sample_rows(M, 48, N + K)
     rows[-1] = M - 1
     ref = oracle.gemm(x[rows], w, bias=b, gelu=gelu, residual=None if r is None else r[rows])
@@ -321,6 +325,44 @@ def test_gemm_qkv_scatter_epilogue(cbis, oracle, dev, kv_dtype):
         assert row_rel_err(gk, ref[:, D:2 * D]) < LOWP_TOL
         assert row_rel_err(gv, ref[:, 2 * D:]) < LOWP_TOL
     # untouched slots stay zero
+    mask = np.ones((P, 16), bool)
+    mask[wpage, woff] = False
+    assert not kh[mask].any() and not vh[mask].any()
+
+
+@pytest.mark.parametrize("M,D", [(700, 1024), (1216, 2048)])
+@pytest.mark.parametrize("ydt", ["f32", "bf16"])
+def test_gemm_qkv_scatter_epilogue_wave_specialised(cbis, oracle, dev, M, D, ydt):
+    """The fused QKV projection at sizes that run the wave-specialised kernel
+    (M=700, d=1024: 144 tiles of 128 x 128; M=1216, d=2048: config 4, tiles of
+    128 x 256): bf16 K/V straight into page slots, Q in fp32 or bf16, through
+    the row-wise epilogue."""
+    import torch
+    P = M // 16 + 8
+    x = oracle.normal(16, 1, M * D).reshape(M, D)
+    w = oracle.normal(16, 2, 3 * D * D, 0.02).reshape(3 * D, D)
+    b = oracle.normal(16, 3, 3 * D, 0.02)
+    X, xv = bf16_dev(x, dev)
+    W, wv = bf16_dev(w, dev)
+    slots = rng(6).permutation(P * 16)[:M]
+    wpage, woff = (slots // 16).astype(np.int32), (slots % 16).astype(np.int32)
+    kp = torch.zeros((P, 16, D), dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros((P, 16, D), dtype=torch.bfloat16, device=dev)
+    qdt = torch.float32 if ydt == "f32" else torch.bfloat16
+    Q = torch.zeros((M, D), dtype=qdt, device=dev)
+    kv = {"col0": D, "width": D, "dtype": cbis.BF16, "k": kp, "v": vp, "wpage": to_dev(wpage, dev),
+          "woff": to_dev(woff, dev), "ldy": D}
+    _gemm(cbis, M, 3 * D, D, X, cbis.BF16, W, cbis.BF16, Q, cbis.F32 if ydt == "f32" else cbis.BF16,
+          bias=to_dev(b, dev), kv=kv)
+    ref = oracle.gemm(xv, wv, bias=b)
+    q = Q.float().cpu().numpy()
+    if ydt == "f32":
+        assert np.abs(q - ref[:, :D]).max() < FP32_TOL * 4
+    else:
+        assert row_rel_err(q, ref[:, :D]) < LOWP_TOL
+    kh, vh = kp.float().cpu().numpy(), vp.float().cpu().numpy()
+    assert row_rel_err(kh[wpage, woff], ref[:, D:2 * D]) < LOWP_TOL
+    assert row_rel_err(vh[wpage, woff], ref[:, 2 * D:]) < LOWP_TOL
     mask = np.ones((P, 16), bool)
     mask[wpage, woff] = False
     assert not kh[mask].any() and not vh[mask].any()
