@@ -577,7 +577,10 @@ int launch_dma(const GemmArgs& g, hipStream_t s) {
 // never holds back an MFMA.  One barrier per K tile: before barrier t the
 // producers have waited (vmcnt) for tile t and the consumers have finished
 // their ds_reads of tile t - 1, whose slot the producers refill with tile
-// t - 1 + STAGES right after it.
+// t - 1 + STAGES right after it.  With REGS > 0 the producers instead load
+// into a REGS-deep ring of VGPRs (they have the registers the consumers need,
+// unused) and ds_write each tile into its slot, so a 2-slot ring (64 KiB at
+// 128 x 128) is enough and two workgroups share a CU.
 //
 // After the K loop the consumers park their accumulators in LDS as a
 // row-major fp32 tile (the ring is free by then) and all 8 waves apply the
@@ -727,7 +730,7 @@ __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* til
   }
 }
 
-template <int BM, int BN, int STAGES>
+template <int BM, int BN, int STAGES, int REGS>
 __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
   typedef WsTile<BM, BN, STAGES> T;
   constexpr int LPW = T::LPW, STAGE_BYTES = T::STAGE_BYTES, FM = T::FM, FN = T::FN;
@@ -754,35 +757,79 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
       if (rr < BM) src[j] = (const uint16_t*)g.X + (int64_t)min(m0 + rr, g.M - 1) * g.ldx + kbeg + chunk * 8;
       else src[j] = (const uint16_t*)g.W + (int64_t)min(n0 + rr - BM, g.N - 1) * g.ldw + kbeg + chunk * 8;
     }
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
-    const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds0 + p * LPW * 1024);
-    auto issue = [&](int kt) {
-      const uint32_t base = wave_lds + (uint32_t)((kt % STAGES) * STAGE_BYTES);
+    if constexpr (REGS == 0) {
+      const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+      const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds0 + p * LPW * 1024);
+      auto issue = [&](int kt) {
+        const uint32_t base = wave_lds + (uint32_t)((kt % STAGES) * STAGE_BYTES);
 #pragma unroll
-      for (int j = 0; j < LPW; ++j) lds_dma16(src[j] + kt * 64, base + j * 1024);
-    };
-    // Waits for a tile with `younger` tiles issued after it.
-    auto wait_tile = [&](int younger) {
-      if constexpr (STAGES >= 4) {
-        if (younger >= 3) { wait_vmcnt<3 * LPW>(); return; }
-      }
-      if constexpr (STAGES >= 3) {
-        if (younger >= 2) { wait_vmcnt<2 * LPW>(); return; }
-      }
-      if (younger >= 1) wait_vmcnt<LPW>();
-      else wait_vmcnt<0>();
-    };
+        for (int j = 0; j < LPW; ++j) lds_dma16(src[j] + kt * 64, base + j * 1024);
+      };
+      // Waits for a tile with `younger` tiles issued after it.
+      auto wait_tile = [&](int younger) {
+        if constexpr (STAGES >= 4) {
+          if (younger >= 3) { wait_vmcnt<3 * LPW>(); return; }
+        }
+        if constexpr (STAGES >= 3) {
+          if (younger >= 2) { wait_vmcnt<2 * LPW>(); return; }
+        }
+        if (younger >= 1) wait_vmcnt<LPW>();
+        else wait_vmcnt<0>();
+      };
 #pragma unroll
-    for (int t = 0; t < STAGES; ++t)
-      if (t < KT) issue(t);
-    wait_tile(min(KT - 1, STAGES - 1));
-    asm volatile("s_barrier" ::: "memory");
-    for (int kt = 0; kt + 1 < KT; ++kt) {
-      wait_tile(min(KT - 1, kt + STAGES - 1) - (kt + 1));
+      for (int t = 0; t < STAGES; ++t)
+        if (t < KT) issue(t);
+      wait_tile(min(KT - 1, STAGES - 1));
       asm volatile("s_barrier" ::: "memory");
-      if (kt + STAGES < KT) issue(kt + STAGES);
+      for (int kt = 0; kt + 1 < KT; ++kt) {
+        wait_tile(min(KT - 1, kt + STAGES - 1) - (kt + 1));
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + STAGES < KT) issue(kt + STAGES);
+      }
+      wait_vmcnt<0>();
+    } else {
+      // Register-staged: tiles go global -> VGPRs (a REGS-deep ring, the
+      // compiler waits for each load where its ds_write uses it) -> LDS.
+      // After barrier j the slot of tile j - 1 is free and receives tile
+      // j + STAGES - 1, whose registers are refilled with tile
+      // j + STAGES - 1 + REGS; its ds_writes finish before barrier j + 1.
+      static_assert(STAGES >= 2 && STAGES - 1 <= REGS, "register ring shorter than the LDS lead");
+      u32x4_t regs[REGS][LPW];
+      uint8_t* my_lds = smem + p * LPW * 1024 + lane * 16;
+      auto load = [&](int r, int t) {
+#pragma unroll
+        for (int j = 0; j < LPW; ++j) regs[r][j] = *(const u32x4_t*)(src[j] + t * 64);
+      };
+      auto store = [&](int r, int t) {
+#pragma unroll
+        for (int j = 0; j < LPW; ++j) *(u32x4_t*)(my_lds + (t % STAGES) * STAGE_BYTES + j * 1024) = regs[r][j];
+      };
+#pragma unroll
+      for (int r = 0; r < REGS; ++r)
+        if (r < KT) load(r, r);
+#pragma unroll
+      for (int t = 0; t < STAGES - 1; ++t)
+        if (t < KT) {
+          store(t % REGS, t);
+          if (t + REGS < KT) load(t % REGS, t + REGS);
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      for (int j0 = 0; j0 < KT; j0 += REGS) {
+#pragma unroll
+        for (int r = 0; r < REGS; ++r) {
+          const int j = j0 + r;
+          if (j >= KT) break;
+          const int t = j + STAGES - 1;
+          constexpr int kLead = STAGES - 1;
+          const int rs = (r + kLead) % REGS;  // t % REGS: j0 is a multiple of REGS
+          if (t < KT) {
+            store(rs, t);
+            if (t + REGS < KT) load(rs, t + REGS);
+          }
+          if (j + 1 < KT) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+      }
     }
-    wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");  // consumers done with the ring
     asm volatile("s_barrier" ::: "memory");  // accumulators parked
   } else {
@@ -846,10 +893,10 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
   epilogue_rows<BM, BN>(g, kz, (const float*)smem, T::PITCH, m0, n0, tid);
 }
 
-template <int BM, int BN, int STAGES>
+template <int BM, int BN, int STAGES, int REGS = 0>
 int launch_ws(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
-  gemm_bf16_ws_kernel<BM, BN, STAGES><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
+  gemm_bf16_ws_kernel<BM, BN, STAGES, REGS><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
   int rc = check_launch("cbis_gemm(bf16 ws)");
   if (rc || g.ksplit <= 1) return rc;
   splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
@@ -1062,16 +1109,17 @@ struct SplitPlan {
 //     fc2 shapes: 469 and 708 TFLOP/s against 452 and 646);
 //   otherwise wave-specialised 128 x 256 when its tiles fill their last
 //     round of kCUs workgroups to >= 3/4 (qkv 742 against 645, lm_head 796
-//     against 743), else gemm_bf16_dma_kernel 128 x 128 with two workgroups
-//     per CU (fc1: 640 against 623 for 320 tiles of 128 x 256).
-enum class Bf16Path { kSmall, kWs128, kWs256, kDma128 };
+//     against 743), else wave-specialised 128 x 128 with register-staged
+//     producers and a 2-slot ring, two workgroups per CU (fc1: 699 against
+//     654 for gemm_bf16_dma_kernel and 576 for 320 tiles of 128 x 256).
+enum class Bf16Path { kSmall, kWs128, kWs256, kWs128R };
 
 Bf16Path choose_bf16(int M, int N) {
   const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
   if (t128 < kCUs / 2) return Bf16Path::kSmall;
   if (t128 < kCUs) return Bf16Path::kWs128;
   const int64_t last = (cdiv(M, 128) * cdiv(N, 256)) % kCUs;
-  return (last == 0 || 4 * last >= 3 * kCUs) ? Bf16Path::kWs256 : Bf16Path::kDma128;
+  return (last == 0 || 4 * last >= 3 * kCUs) ? Bf16Path::kWs256 : Bf16Path::kWs128R;
 }
 
 SplitPlan plan_dma_split(int M, int N, int K) {
@@ -1197,7 +1245,7 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
       switch (choose_bf16(d->M, d->N)) {
         case Bf16Path::kWs256: return launch_ws<128, 256, 3>(g, s);
         case Bf16Path::kWs128: return launch_ws<128, 128, 3>(g, s);
-        case Bf16Path::kDma128: return launch_dma<kDmaBM, kDmaBN, 2, 4, 2>(g, s);
+        case Bf16Path::kWs128R: return launch_ws<128, 128, 2, 3>(g, s);
         case Bf16Path::kSmall: break;
       }
       const SplitPlan p = plan_dma_split(d->M, d->N, d->K);

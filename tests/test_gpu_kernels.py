@@ -186,14 +186,15 @@ def test_gemm_gelu_epilogue_accuracy(cbis, dev, M, xdt):
 
 @pytest.mark.parametrize("M", [192, 1216])
 @pytest.mark.parametrize("N,K,gelu", [(2048, 4096, False), (2048, 8192, False), (1024, 4096, True), (1030, 4096, False),
-                                      (2050, 4096, False)])
+                                      (2050, 4096, False), (8192, 2048, True)])
 def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
     """Bias, GELU, and a residual that aliases Y, against the fp64 oracle, on
     the two bf16 tiled paths: grids of fewer than 128 tiles of 128 x 128
     cannot fill the GPU and split-K (fp32 partials in a caller workspace,
     reduce + epilogue) must engage; larger ones (M=1216 with N=2048 or 2050)
     run the wave-specialised kernel whole-K (no workspace) with its row-wise
-    epilogue, N=2050 ending in a ragged column group."""
+    epilogue, N=2050 ending in a ragged column group, N=8192 with
+    register-staged producers (config 4's fc1 with its GELU)."""
     import torch
     X, x = bf16_dev(oracle.normal(15, 1, M * K).reshape(M, K), dev)
     W, w = bf16_dev(oracle.normal(15, 2, N * K, 0.02).reshape(N, K), dev)
