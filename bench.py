@@ -330,7 +330,11 @@ def run_c4(args, cbis, oracle):
     st = c4_setup(cbis, oracle)
     runner = st["runner"]
     import torch
-    step = lambda: runner.forward_step_greedy(st["tok"], st["pos"], st["sid"])
+    # The step's rows as int32 arrays (the binding passes them to the C++
+    # runner without a per-element conversion); the runner redoes all of its
+    # per-step host work (checks, slot resolution, block tables, one H2D copy).
+    tok, pos, sid = (np.asarray(st[k], dtype=np.int32) for k in ("tok", "pos", "sid"))
+    step = lambda: runner.forward_step_greedy(tok, pos, sid)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()

@@ -16,6 +16,8 @@ from __future__ import annotations
 import ctypes
 import os
 
+import numpy as np
+
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(HERE, "lib")
 KERNELS_SO = os.path.join(LIB_DIR, "libcbis_kernels.so")
@@ -207,8 +209,16 @@ def _rt_check(rc, what):
 
 
 def _iarr(vals):
-    vals = list(int(v) for v in vals)
-    return (ctypes.c_int * max(1, len(vals)))(*vals)
+    """int32 C view of `vals` for an `int*` argument.  A C-contiguous numpy
+    int32 array is passed without a copy; anything else is converted once
+    through numpy (integers outside int32 raise OverflowError).  The returned
+    pointer keeps its array alive for the call."""
+    a = np.ascontiguousarray(vals, dtype=np.int32)
+    if a.ndim != 1:
+        a = a.reshape(-1)
+    if a.size == 0:
+        a = np.zeros(1, dtype=np.int32)
+    return a.ctypes.data_as(_IP)
 
 
 # --------------------------------------------------------------------------
