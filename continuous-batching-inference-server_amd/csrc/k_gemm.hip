@@ -356,35 +356,147 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
       epilogue_block(g, kz, m0 + wm * TM + i * 32 + 4 * half, n0 + wn * TN + j * 32 + l32, acc[i][j]);
 }
 
-// Sums the split-K partials (fixed order) and applies the epilogue; four
-// consecutive columns per thread (16-byte partial loads) when N % 4 == 0.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs g) {
-  const int64_t MN = (int64_t)g.M * g.N;
-  if ((g.N & 3) == 0) {
-    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    if (idx >= MN) return;
-    float4 v = *(const float4*)(g.partial + idx);
-    for (int z = 1; z < g.ksplit; ++z) {
-      const float4 p = *(const float4*)(g.partial + z * MN + idx);
-      v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+// Epilogue of the 4 consecutive output columns col..col+3 (fewer at the
+// right edge) handled by one thread: the per-column constants once, then per
+// row the inputs (residual, K/V slot) and the finished store.  One 16-byte
+// (fp32) or 8-byte (bf16) store when the 4 columns share a destination and
+// its alignment allows, else element by element like epilogue_store.
+struct Cols4 {
+  int col, nc;
+  float sc[4], bi[4];
+  bool to_kv, vec, res_vec;
+  int ce;
+  void* pool;
+
+  // raw: the destination is the split-K partials (no epilogue).
+  __device__ Cols4(const GemmArgs& g, int col_, bool raw) : col(col_), nc(min(4, g.N - col_)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sc[e] = (!raw && g.w_scale && e < nc) ? g.w_scale[col + e] : 1.f;
+      bi[e] = (!raw && g.bias && e < nc) ? g.bias[col + e] : 0.f;
     }
-    const int row = (int)(idx / g.N), col = (int)(idx % g.N);
-    epilogue_store(g, row, col, v.x);
-    epilogue_store(g, row, col + 1, v.y);
-    epilogue_store(g, row, col + 2, v.z);
-    epilogue_store(g, row, col + 3, v.w);
-    return;
+    to_kv = !raw && g.k_pool && col >= g.kv_col0;
+    const int c = col - g.kv_col0;
+    const bool is_v = to_kv && c >= g.kv_width;
+    ce = is_v ? c - g.kv_width : c;
+    pool = is_v ? g.v_pool : g.k_pool;
+    vec = nc == 4;
+    if (raw) {
+      vec = vec && (g.N & 3) == 0 && ((uintptr_t)g.partial & 15u) == 0;
+    } else if (to_kv) {
+      vec = vec && (ce & 3) == 0 && ce + 3 < g.kv_width && ((uintptr_t)pool & (g.kv_bf16 ? 7u : 15u)) == 0 &&
+            (g.kv_width & 3) == 0;
+    } else {
+      vec = vec && (!g.k_pool || col + 3 < g.kv_col0) && (g.ldy & 3) == 0 &&
+            ((uintptr_t)g.Y & (g.y_bf16 ? 7u : 15u)) == 0;
+    }
+    res_vec = g.residual && nc == 4 && (g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15u) == 0;
   }
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= MN) return;
-  float v = 0.f;
-  for (int z = 0; z < g.ksplit; ++z) v += g.partial[z * MN + idx];
-  epilogue_store(g, (int)(idx / g.N), (int)(idx % g.N), v);
+
+  // Inputs of one row: residual values and the K/V slot.
+  __device__ void load(const GemmArgs& g, int row, float* r, int64_t& slot) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = 0.f;
+    slot = 0;
+    if (g.residual) {
+      const float* rp = g.residual + (int64_t)row * g.ldr + col;
+      if (res_vec) {
+        const float4 rv = *(const float4*)rp;
+        r[0] = rv.x; r[1] = rv.y; r[2] = rv.z; r[3] = rv.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (e < nc) r[e] = rp[e];
+      }
+    }
+    if (to_kv) slot = (int64_t)g.wpage[row] * g.page_size + g.woff[row];
+  }
+
+  // Scale, bias, GELU, residual, then the store.
+  __device__ void finish(const GemmArgs& g, int row, float* v, const float* r, int64_t slot) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = v[e];
+      if (g.w_scale) x *= sc[e];
+      if (g.bias) x += bi[e];
+      if (g.gelu) x = gelu_erf(x);
+      if (g.residual) x += r[e];
+      v[e] = x;
+    }
+    if (!vec) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (e >= nc) continue;
+        const int cc = col + e;
+        if (g.k_pool && cc >= g.kv_col0) {
+          const int c2 = cc - g.kv_col0;
+          const bool v2 = c2 >= g.kv_width;
+          const int64_t off =
+              ((int64_t)g.wpage[row] * g.page_size + g.woff[row]) * g.kv_width + (v2 ? c2 - g.kv_width : c2);
+          void* pl = v2 ? g.v_pool : g.k_pool;
+          if (g.kv_bf16) ((uint16_t*)pl)[off] = f32_to_bf16(v[e]);
+          else ((float*)pl)[off] = v[e];
+        } else {
+          const int64_t o = (int64_t)row * g.ldy + cc;
+          if (g.y_bf16) ((uint16_t*)g.Y)[o] = f32_to_bf16(v[e]);
+          else ((float*)g.Y)[o] = v[e];
+        }
+      }
+      return;
+    }
+    const bool bf = to_kv ? g.kv_bf16 : g.y_bf16;
+    void* dst = to_kv ? (void*)((char*)pool + (slot * g.kv_width + ce) * (bf ? 2 : 4))
+                      : (void*)((char*)g.Y + ((int64_t)row * g.ldy + col) * (bf ? 2 : 4));
+    if (bf) *(uint2*)dst = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    else *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+  }
+
+  // Raw sums to split kz's partials.
+  __device__ void store_partial(const GemmArgs& g, int kz, int row, const float* v) const {
+    float* pp = g.partial + ((int64_t)kz * g.M + row) * g.N + col;
+    if (vec) {
+      *(float4*)pp = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < nc) pp[e] = v[e];
+    }
+  }
+};
+
+// Sums the split-K partials (fixed order z = 0, 1, ...) and applies the
+// epilogue: one thread per 4 consecutive columns of a row.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs g) {
+  const int cgn = (g.N + 3) / 4;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)g.M * cgn) return;
+  const int row = (int)(t / cgn), col = (int)(t % cgn) * 4;
+  const Cols4 c(g, col, false);
+  float r[4];
+  int64_t slot;
+  c.load(g, row, r, slot);
+  const int64_t MN = (int64_t)g.M * g.N;
+  const float* pp = g.partial + (int64_t)row * g.N + col;
+  const bool pvec = c.nc == 4 && (g.N & 3) == 0 && ((uintptr_t)g.partial & 15u) == 0;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < g.ksplit; ++z) {
+    float p[4] = {0.f, 0.f, 0.f, 0.f};
+    if (pvec) {
+      const float4 q = *(const float4*)(pp + z * MN);
+      p[0] = q.x; p[1] = q.y; p[2] = q.z; p[3] = q.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < c.nc) p[e] = pp[z * MN + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = z == 0 ? p[e] : v[e] + p[e];
+  }
+  c.finish(g, row, v, r, slot);
 }
 
 inline unsigned splitk_reduce_blocks(const GemmArgs& g) {
-  const int64_t MN = (int64_t)g.M * g.N;
-  return (unsigned)cdiv((g.N & 3) == 0 ? cdiv(MN, 4) : MN, 256);
+  return (unsigned)cdiv((int64_t)g.M * cdiv(g.N, 4), 256);
 }
 
 // ---------------------------------------------------------------------------
@@ -607,7 +719,9 @@ struct WsTile {
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
-// Epilogue over a parked BM x BN fp32 tile by the workgroup's 512 threads.
+// Epilogue over a parked BM x BN fp32 tile by the workgroup's 512 threads:
+// thread (rs, cg) takes columns 4cg..4cg+3 of rows rs, rs + RPP, ...; the
+// inputs of 4 rows are loaded before their stores (Y may alias the residual).
 template <int BM, int BN>
 __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* tile, int pitch, int m0, int n0,
                                      int tid) {
@@ -616,116 +730,26 @@ __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* til
   constexpr int PASSES = BM / RPP;
   static_assert(RPP * CG == 512 && PASSES % 4 == 0, "epilogue thread map");
   const int cg = tid % CG, rs = tid / CG;
-  const int col = n0 + 4 * cg;
-  if (col >= g.N) return;
-  const int nc = min(4, g.N - col);
-  float sc[4], bi[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    sc[e] = (g.w_scale && e < nc) ? g.w_scale[col + e] : 1.f;
-    bi[e] = (g.bias && e < nc) ? g.bias[col + e] : 0.f;
-  }
-  // Destination of the 4 columns and whether one vector access serves them.
-  const bool split = g.ksplit > 1;
-  const bool to_kv = !split && g.k_pool && col >= g.kv_col0;
-  const int c = col - g.kv_col0;
-  const bool is_v = to_kv && c >= g.kv_width;
-  const int ce = is_v ? c - g.kv_width : c;
-  void* pool = is_v ? g.v_pool : g.k_pool;
-  bool vec = nc == 4;
-  if (split) {
-    vec = vec && (g.N & 3) == 0 && ((uintptr_t)g.partial & 15u) == 0;
-  } else if (to_kv) {
-    vec = vec && (ce & 3) == 0 && ce + 3 < g.kv_width &&
-          ((uintptr_t)pool & (g.kv_bf16 ? 7u : 15u)) == 0 && (g.kv_width & 3) == 0;
-  } else {
-    vec = vec && (!g.k_pool || col + 3 < g.kv_col0) && (g.ldy & 3) == 0 &&
-          ((uintptr_t)g.Y & (g.y_bf16 ? 7u : 15u)) == 0;
-  }
-  const bool res_vec = g.residual && (g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15u) == 0;
-  const bool kv_bf16 = g.kv_bf16, y_bf16 = g.y_bf16;
-
+  if (n0 + 4 * cg >= g.N) return;
+  const bool raw = g.ksplit > 1;
+  const Cols4 c(g, n0 + 4 * cg, raw);
 #pragma unroll 1
   for (int p0 = 0; p0 < PASSES; p0 += 4) {
     float v[4][4], r[4][4];
     int64_t slot[4];
-    bool ok[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int lr = (p0 + q) * RPP + rs;
-      const int row = m0 + lr;
-      ok[q] = row < g.M;
       const float4 t = *(const float4*)(tile + lr * pitch + 4 * cg);
       v[q][0] = t.x; v[q][1] = t.y; v[q][2] = t.z; v[q][3] = t.w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) r[q][e] = 0.f;
-      slot[q] = 0;
-      if (!ok[q] || split) continue;
-      if (g.residual) {
-        const float* rp = g.residual + (int64_t)row * g.ldr + col;
-        if (res_vec && nc == 4) {
-          const float4 rv = *(const float4*)rp;
-          r[q][0] = rv.x; r[q][1] = rv.y; r[q][2] = rv.z; r[q][3] = rv.w;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (e < nc) r[q][e] = rp[e];
-        }
-      }
-      if (to_kv) slot[q] = (int64_t)g.wpage[row] * g.page_size + g.woff[row];
+      if (!raw && m0 + lr < g.M) c.load(g, m0 + lr, r[q], slot[q]);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      if (!ok[q]) continue;
       const int row = m0 + (p0 + q) * RPP + rs;
-      if (split) {
-        float* pp = g.partial + ((int64_t)kz * g.M + row) * g.N + col;
-        if (vec) {
-          *(float4*)pp = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (e < nc) pp[e] = v[q][e];
-        }
-        continue;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float x = v[q][e];
-        if (g.w_scale) x *= sc[e];
-        if (g.bias) x += bi[e];
-        if (g.gelu) x = gelu_erf(x);
-        if (g.residual) x += r[q][e];
-        v[q][e] = x;
-      }
-      if (!vec) {
-        // Mixed or unaligned group: element by element, like epilogue_store
-        // after the scale / bias / GELU / residual above.
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (e >= nc) continue;
-          const int cc = col + e;
-          if (g.k_pool && cc >= g.kv_col0) {
-            const int c2 = cc - g.kv_col0;
-            const bool v2 = c2 >= g.kv_width;
-            const int64_t off = ((int64_t)g.wpage[row] * g.page_size + g.woff[row]) * g.kv_width +
-                                (v2 ? c2 - g.kv_width : c2);
-            void* pl = v2 ? g.v_pool : g.k_pool;
-            if (kv_bf16) ((uint16_t*)pl)[off] = f32_to_bf16(v[q][e]);
-            else ((float*)pl)[off] = v[q][e];
-          } else {
-            const int64_t o = (int64_t)row * g.ldy + cc;
-            if (y_bf16) ((uint16_t*)g.Y)[o] = f32_to_bf16(v[q][e]);
-            else ((float*)g.Y)[o] = v[q][e];
-          }
-        }
-        continue;
-      }
-      const bool bf = to_kv ? kv_bf16 : y_bf16;
-      void* dst = to_kv ? (void*)((char*)pool + (slot[q] * g.kv_width + ce) * (bf ? 2 : 4))
-                        : (void*)((char*)g.Y + ((int64_t)row * g.ldy + col) * (bf ? 2 : 4));
-      if (bf) *(uint2*)dst = make_uint2(pack_bf16x2(v[q][0], v[q][1]), pack_bf16x2(v[q][2], v[q][3]));
-      else *(float4*)dst = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+      if (row >= g.M) continue;
+      if (raw) c.store_partial(g, kz, row, v[q]);
+      else c.finish(g, row, v[q], r[q], slot[q]);
     }
   }
 }
@@ -1106,18 +1130,20 @@ struct SplitPlan {
 //   < kCUs / 2 tiles of 128 x 128: gemm_bf16_dma_kernel, 64 x 64 tiles or
 //     128 x 128 with split-K (plan_dma_split);
 //   < kCUs tiles: wave-specialised 128 x 128, 3 stages (out-projection and
-//     fc2 shapes: 469 and 708 TFLOP/s against 452 and 646);
+//     fc2 shapes: 469 and 708 TFLOP/s against 452 and 646); with K of 96
+//     tiles or more, split-K 3 on the register-staged form instead (two
+//     workgroups per CU: the 3 x tiles run in one round, each on a third of K);
 //   otherwise wave-specialised 128 x 256 when its tiles fill their last
 //     round of kCUs workgroups to >= 3/4 (qkv 742 against 645, lm_head 796
 //     against 743), else wave-specialised 128 x 128 with register-staged
 //     producers and a 2-slot ring, two workgroups per CU (fc1: 699 against
 //     654 for gemm_bf16_dma_kernel and 576 for 320 tiles of 128 x 256).
-enum class Bf16Path { kSmall, kWs128, kWs256, kWs128R };
+enum class Bf16Path { kSmall, kWs128, kWs128Split, kWs256, kWs128R };
 
-Bf16Path choose_bf16(int M, int N) {
+Bf16Path choose_bf16(int M, int N, int K) {
   const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
   if (t128 < kCUs / 2) return Bf16Path::kSmall;
-  if (t128 < kCUs) return Bf16Path::kWs128;
+  if (t128 < kCUs) return K / 64 >= 96 ? Bf16Path::kWs128Split : Bf16Path::kWs128;
   const int64_t last = (cdiv(M, 128) * cdiv(N, 256)) % kCUs;
   return (last == 0 || 4 * last >= 3 * kCUs) ? Bf16Path::kWs256 : Bf16Path::kWs128R;
 }
@@ -1127,7 +1153,14 @@ SplitPlan plan_dma_split(int M, int N, int K) {
   p.k_per = K;
   const int64_t tiles = cdiv(M, kDmaBM) * cdiv(N, kDmaBN);
   const int kt = K / 64;
-  if (choose_bf16(M, N) != Bf16Path::kSmall || tiles >= kCUs || kt < 64) return p;
+  const Bf16Path path = choose_bf16(M, N, K);
+  if (path == Bf16Path::kWs128Split) {
+    const int per = (kt + 2) / 3;
+    p.ksplit = (kt + per - 1) / per;
+    p.k_per = per * 64;
+    return p;
+  }
+  if (path != Bf16Path::kSmall || tiles >= kCUs || kt < 64) return p;
   int ks = (int)std::max<int64_t>(2, std::min<int64_t>(4, (2 * kCUs) / tiles));
   ks = std::min(ks, kt / 16);
   if (ks <= 1) return p;
@@ -1242,18 +1275,22 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
   if (d->w_dtype == CBIS_BF16) {
     // The direct-to-LDS path needs 16-byte aligned rows of both operands.
     if (dma_eligible(d)) {
-      switch (choose_bf16(d->M, d->N)) {
-        case Bf16Path::kWs256: return launch_ws<128, 256, 3>(g, s);
-        case Bf16Path::kWs128: return launch_ws<128, 128, 3>(g, s);
-        case Bf16Path::kWs128R: return launch_ws<128, 128, 2, 3>(g, s);
-        case Bf16Path::kSmall: break;
-      }
+      const Bf16Path path = choose_bf16(d->M, d->N, d->K);
       const SplitPlan p = plan_dma_split(d->M, d->N, d->K);
       const size_t need = (size_t)p.ksplit * d->M * d->N * sizeof(float);
-      if (p.ksplit > 1 && d->workspace && d->workspace_bytes >= need) {
+      const bool split = p.ksplit > 1 && d->workspace && d->workspace_bytes >= need;
+      if (split) {
         g.ksplit = p.ksplit;
         g.k_per = p.k_per;
         g.partial = (float*)d->workspace;
+      }
+      switch (path) {
+        case Bf16Path::kWs256: return launch_ws<128, 256, 3>(g, s);
+        case Bf16Path::kWs128: return launch_ws<128, 128, 3>(g, s);
+        case Bf16Path::kWs128Split:
+          return split ? launch_ws<128, 128, 2, 3>(g, s) : launch_ws<128, 128, 3>(g, s);
+        case Bf16Path::kWs128R: return launch_ws<128, 128, 2, 3>(g, s);
+        case Bf16Path::kSmall: break;
       }
       // Grids with fewer 128 x 128 tiles than CUs run 64 x 64 tiles (4 waves
       // of 32 x 32): four times the workgroups (config 4's out-projection,
