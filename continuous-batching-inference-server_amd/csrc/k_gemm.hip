@@ -682,7 +682,8 @@ int launch_dma(const GemmArgs& g, hipStream_t s) {
 //
 // 8 waves, one workgroup per CU.  Waves 0-3 (one per SIMD) are consumers:
 // they only read fragments from LDS and issue MFMAs, each on a
-// (BM/2) x (BN/2) sub-tile.  Waves 4-7 are producers: they only issue the
+// (BM/WM) x (BN/(4/WM)) sub-tile (2 x 2, or 1 x 4 for 160-row tiles).
+// Waves 4-7 are producers: they only issue the
 // direct-to-LDS loads of a STAGES-slot ring (same row layout and swizzle as
 // gemm_bf16_dma_kernel) and wait for them, so a load that stalls at issue
 // (the texture path takes a 1 KiB DMA instruction per ~16 cycles per CU)
@@ -695,7 +696,8 @@ int launch_dma(const GemmArgs& g, hipStream_t s) {
 // 128 x 128) is enough and two workgroups share a CU.
 //
 // After the K loop the consumers park their accumulators in LDS as a
-// row-major fp32 tile (the ring is free by then) and all 8 waves apply the
+// row-major fp32 tile (the ring is free by then; a tile too large for LDS is
+// parked in two row blocks, one after the other) and all 8 waves apply the
 // epilogue row by row, 4 consecutive columns per thread: the channel scale
 // and bias are loaded once per thread, residual / partial accesses are 16
 // bytes and bf16 / K/V stores 8 bytes, and every thread loads the inputs of
@@ -703,49 +705,57 @@ int launch_dma(const GemmArgs& g, hipStream_t s) {
 // ---------------------------------------------------------------------------
 constexpr int kWsProducers = 4;
 
-template <int BM, int BN, int STAGES>
+template <int BM, int BN, int STAGES, int WM>
 struct WsTile {
-  static constexpr int TM = BM / 2, TN = BN / 2;
+  static constexpr int WN = 4 / WM;                    // consumers as WM x WN
+  static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 32, FN = TN / 32;
   static constexpr int ROWS = BM + BN;
   static constexpr int LPW = ROWS / 8 / kWsProducers;  // 1 KiB DMA instructions per producer per tile
   static constexpr int STAGE_BYTES = ROWS * 128;
   static constexpr int RING = STAGES * STAGE_BYTES;
   static constexpr int PITCH = BN + 8;                 // floats per parked output row
-  static constexpr int PARK = BM * PITCH * 4;
+  static constexpr int kLdsMax = 160 * 1024;
+  // The accumulators are parked PH row blocks at a time when the whole tile
+  // does not fit.
+  static constexpr int PH = BM * PITCH * 4 <= kLdsMax ? 1 : (BM / 2) * PITCH * 4 <= kLdsMax ? 2 : 4;
+  static constexpr int PR = BM / PH;                   // rows per parked block
+  static constexpr int PARK = PR * PITCH * 4;
   static constexpr int LDS = RING > PARK ? RING : PARK;
+  static_assert(WM * WN == 4 && TM % 32 == 0 && TN % 32 == 0, "consumer layout");
   static_assert(LPW * 8 * kWsProducers == ROWS, "tile rows / producers");
   static_assert(LPW * (STAGES - 1) < 64, "vmcnt range");
-  static_assert(LDS <= 160 * 1024, "LDS");
+  static_assert(BM % PH == 0 && PR * PITCH * 4 <= kLdsMax && LDS <= kLdsMax, "LDS");
 };
 
-// Epilogue over a parked BM x BN fp32 tile by the workgroup's 512 threads:
+// Epilogue over a parked BM x BN fp32 tile by the workgroup's NT threads:
 // thread (rs, cg) takes columns 4cg..4cg+3 of rows rs, rs + RPP, ...; the
 // inputs of 4 rows are loaded before their stores (Y may alias the residual).
-template <int BM, int BN>
+template <int BM, int BN, int NT = 512>
 __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* tile, int pitch, int m0, int n0,
                                      int tid) {
   constexpr int CG = BN / 4;      // 4-column groups per row
-  constexpr int RPP = 512 / CG;   // rows per pass
+  constexpr int RPP = NT / CG;    // rows per pass
   constexpr int PASSES = BM / RPP;
-  static_assert(RPP * CG == 512 && PASSES % 4 == 0, "epilogue thread map");
+  constexpr int G = PASSES % 4 == 0 ? 4 : 2;  // rows whose inputs are loaded before their stores
+  static_assert(RPP * CG == NT && PASSES % G == 0, "epilogue thread map");
   const int cg = tid % CG, rs = tid / CG;
   if (n0 + 4 * cg >= g.N) return;
   const bool raw = g.ksplit > 1;
   const Cols4 c(g, n0 + 4 * cg, raw);
 #pragma unroll 1
-  for (int p0 = 0; p0 < PASSES; p0 += 4) {
-    float v[4][4], r[4][4];
-    int64_t slot[4];
+  for (int p0 = 0; p0 < PASSES; p0 += G) {
+    float v[G][4], r[G][4];
+    int64_t slot[G];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < G; ++q) {
       const int lr = (p0 + q) * RPP + rs;
       const float4 t = *(const float4*)(tile + lr * pitch + 4 * cg);
       v[q][0] = t.x; v[q][1] = t.y; v[q][2] = t.z; v[q][3] = t.w;
       if (!raw && m0 + lr < g.M) c.load(g, m0 + lr, r[q], slot[q]);
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < G; ++q) {
       const int row = m0 + (p0 + q) * RPP + rs;
       if (row >= g.M) continue;
       if (raw) c.store_partial(g, kz, row, v[q]);
@@ -754,9 +764,9 @@ __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* til
   }
 }
 
-template <int BM, int BN, int STAGES, int REGS>
+template <int BM, int BN, int STAGES, int REGS, int WM>
 __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
-  typedef WsTile<BM, BN, STAGES> T;
+  typedef WsTile<BM, BN, STAGES, WM> T;
   constexpr int LPW = T::LPW, STAGE_BYTES = T::STAGE_BYTES, FM = T::FM, FN = T::FN;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::LDS];
 
@@ -769,6 +779,9 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WM, wn = wave / WM;  // consumer sub-tile (waves 0-3)
+  const int half = lane >> 5, l32 = lane & 31;
+  f32x16_t acc[FM][FN];
 
   if (wave >= 4) {
     // Producer: tile rows p*8*LPW .. of every stage (A rows first, then B).
@@ -855,13 +868,9 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
       }
     }
     asm volatile("s_barrier" ::: "memory");  // consumers done with the ring
-    asm volatile("s_barrier" ::: "memory");  // accumulators parked
   } else {
-    // Consumer: sub-tile (wm, wn) of 2 x 2.
+    // Consumer: sub-tile (wm, wn) of WM x (4 / WM).
     __builtin_amdgcn_s_setprio(2);
-    const int wm = wave & 1, wn = wave >> 1;
-    const int half = lane >> 5, l32 = lane & 31;
-    f32x16_t acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -901,26 +910,33 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
       }
     }
     __builtin_amdgcn_s_setprio(0);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    float* park = (float*)smem;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = wm * T::TM + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-          park[r * T::PITCH + wn * T::TN + j * 32 + l32] = acc[i][j][e];
-        }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // done with the ring
   }
-  epilogue_rows<BM, BN>(g, kz, (const float*)smem, T::PITCH, m0, n0, tid);
+  // Park the accumulators (PH blocks of PR rows) and finish them row-wise.
+  float* park = (float*)smem;
+#pragma unroll
+  for (int h = 0; h < T::PH; ++h) {
+    if (wave < 4) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int r = wm * T::TM + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3) - h * T::PR;
+            if (T::PH == 1 || (r >= 0 && r < T::PR)) park[r * T::PITCH + wn * T::TN + j * 32 + l32] = acc[i][j][e];
+          }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    epilogue_rows<T::PR, BN>(g, kz, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
+    if (h + 1 < T::PH) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
 }
 
-template <int BM, int BN, int STAGES, int REGS = 0>
+template <int BM, int BN, int STAGES, int REGS = 0, int WM = 2>
 int launch_ws(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
-  gemm_bf16_ws_kernel<BM, BN, STAGES, REGS><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
+  gemm_bf16_ws_kernel<BM, BN, STAGES, REGS, WM><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
   int rc = check_launch("cbis_gemm(bf16 ws)");
   if (rc || g.ksplit <= 1) return rc;
   splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
@@ -1126,26 +1142,32 @@ struct SplitPlan {
 };
 
 // Kernel for a bf16 x bf16 problem on the direct-to-LDS paths, from the
-// tile counts (measured on config 4's shapes at M = 1216):
+// tile counts (measured on config 4's shapes at M = 1216, TFLOP/s):
 //   < kCUs / 2 tiles of 128 x 128: gemm_bf16_dma_kernel, 64 x 64 tiles or
 //     128 x 128 with split-K (plan_dma_split);
 //   < kCUs tiles: wave-specialised 128 x 128, 3 stages (out-projection and
-//     fc2 shapes: 469 and 708 TFLOP/s against 452 and 646); with K of 96
-//     tiles or more, split-K 3 on the register-staged form instead (two
-//     workgroups per CU: the 3 x tiles run in one round, each on a third of K);
-//   otherwise wave-specialised 128 x 256 when its tiles fill their last
-//     round of kCUs workgroups to >= 3/4 (qkv 742 against 645, lm_head 796
-//     against 743), else wave-specialised 128 x 128 with register-staged
-//     producers and a 2-slot ring, two workgroups per CU (fc1: 699 against
-//     654 for gemm_bf16_dma_kernel and 576 for 320 tiles of 128 x 256).
-enum class Bf16Path { kSmall, kWs128, kWs128Split, kWs256, kWs128R };
+//     fc2 shapes: 469 and 708 against 452 and 646); with K of 96 tiles or
+//     more, split-K 3 on the register-staged form instead (two workgroups per
+//     CU: the 3 x tiles run in one round, each on a third of K);
+//   otherwise the wave-specialised tiling with the least estimated time:
+//     whole rounds of kCUs workgroups times the tile's work, 128 x 256 = 1,
+//     160 x 256 = 1.25, 128 x 128 register-staged (two per CU, 512 per
+//     round) = 1 with a 1.1 penalty for its lower efficiency; ties go to the
+//     larger tile.  qkv: 128 x 256 (742 against 645); fc1: 160 x 256, one
+//     round of 256 tiles (832 against 685 for 128 x 128 register-staged and
+//     577 for 128 x 256); lm_head: 160 x 256 (832 against 779).
+enum class Bf16Path { kSmall, kWs128, kWs128Split, kWs256, kWs160, kWs128R };
 
 Bf16Path choose_bf16(int M, int N, int K) {
   const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
   if (t128 < kCUs / 2) return Bf16Path::kSmall;
   if (t128 < kCUs) return K / 64 >= 96 ? Bf16Path::kWs128Split : Bf16Path::kWs128;
-  const int64_t last = (cdiv(M, 128) * cdiv(N, 256)) % kCUs;
-  return (last == 0 || 4 * last >= 3 * kCUs) ? Bf16Path::kWs256 : Bf16Path::kWs128R;
+  const double c160 = 1.25 * cdiv(cdiv(M, 160) * cdiv(N, 256), kCUs);
+  const double c256 = 1.0 * cdiv(cdiv(M, 128) * cdiv(N, 256), kCUs);
+  const double c128 = 1.1 * cdiv(t128, 2 * kCUs);
+  if (c160 <= c256 && c160 <= c128) return Bf16Path::kWs160;
+  if (c256 <= c128) return Bf16Path::kWs256;
+  return Bf16Path::kWs128R;
 }
 
 SplitPlan plan_dma_split(int M, int N, int K) {
@@ -1286,6 +1308,7 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
       }
       switch (path) {
         case Bf16Path::kWs256: return launch_ws<128, 256, 3>(g, s);
+        case Bf16Path::kWs160: return launch_ws<160, 256, 3, 0, 1>(g, s);
         case Bf16Path::kWs128: return launch_ws<128, 128, 3>(g, s);
         case Bf16Path::kWs128Split:
           return split ? launch_ws<128, 128, 2, 3>(g, s) : launch_ws<128, 128, 3>(g, s);
