@@ -1145,10 +1145,15 @@ struct SplitPlan {
 // tile counts (measured on config 4's shapes at M = 1216, TFLOP/s):
 //   < kCUs / 2 tiles of 128 x 128: gemm_bf16_dma_kernel, 64 x 64 tiles or
 //     128 x 128 with split-K (plan_dma_split);
-//   < kCUs tiles: wave-specialised 128 x 128, 3 stages (out-projection and
-//     fc2 shapes: 469 and 708 against 452 and 646); with K of 96 tiles or
-//     more, split-K 3 on the register-staged form instead (two workgroups per
-//     CU: the 3 x tiles run in one round, each on a third of K);
+//   < kCUs tiles and K of 96 tiles of 64 or more: split-K 3 on the
+//     register-staged 128 x 128 form (two workgroups per CU: the 3 x tiles
+//     run in one round, each on a third of K).  With weights cold in HBM, as
+//     in the step, more loads in flight beat larger tiles (fc2 at M = 1216:
+//     67 us against 79 for 96 x 128 whole-K; warm, 96 x 128 is faster);
+//   < kCUs tiles otherwise: wave-specialised 96 x 128 (1 x 4 consumers) when
+//     its tiles need no more rounds than 128 x 128 ones, else 128 x 128
+//     (out-projection: 208 tiles of 96 x 128, 535 TFLOP/s against 466 for
+//     160 tiles of 128 x 128);
 //   otherwise the wave-specialised tiling with the least estimated time:
 //     whole rounds of kCUs workgroups times the tile's work, 128 x 256 = 1,
 //     160 x 256 = 1.25, 128 x 128 register-staged (two per CU, 512 per
@@ -1156,12 +1161,16 @@ struct SplitPlan {
 //     larger tile.  qkv: 128 x 256 (742 against 645); fc1: 160 x 256, one
 //     round of 256 tiles (832 against 685 for 128 x 128 register-staged and
 //     577 for 128 x 256); lm_head: 160 x 256 (832 against 779).
-enum class Bf16Path { kSmall, kWs128, kWs128Split, kWs256, kWs160, kWs128R };
+enum class Bf16Path { kSmall, kWs128, kWs128Split, kWs96, kWs256, kWs160, kWs128R };
 
 Bf16Path choose_bf16(int M, int N, int K) {
   const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
   if (t128 < kCUs / 2) return Bf16Path::kSmall;
-  if (t128 < kCUs) return K / 64 >= 96 ? Bf16Path::kWs128Split : Bf16Path::kWs128;
+  if (t128 < kCUs && K / 64 >= 96) return Bf16Path::kWs128Split;
+  if (t128 < kCUs) {
+    const double c96 = 0.75 * cdiv(cdiv(M, 96) * cdiv(N, 128), kCUs);
+    return c96 < 1.0 ? Bf16Path::kWs96 : Bf16Path::kWs128;
+  }
   const double c160 = 1.25 * cdiv(cdiv(M, 160) * cdiv(N, 256), kCUs);
   const double c256 = 1.0 * cdiv(cdiv(M, 128) * cdiv(N, 256), kCUs);
   const double c128 = 1.1 * cdiv(t128, 2 * kCUs);
@@ -1310,8 +1319,9 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
         case Bf16Path::kWs256: return launch_ws<128, 256, 3>(g, s);
         case Bf16Path::kWs160: return launch_ws<160, 256, 3, 0, 1>(g, s);
         case Bf16Path::kWs128: return launch_ws<128, 128, 3>(g, s);
+        case Bf16Path::kWs96: return launch_ws<96, 128, 3, 0, 1>(g, s);
         case Bf16Path::kWs128Split:
-          return split ? launch_ws<128, 128, 2, 3>(g, s) : launch_ws<128, 128, 3>(g, s);
+          return split ? launch_ws<128, 128, 2, 3>(g, s) : launch_ws<96, 128, 3, 0, 1>(g, s);
         case Bf16Path::kWs128R: return launch_ws<128, 128, 2, 3>(g, s);
         case Bf16Path::kSmall: break;
       }

@@ -191,11 +191,13 @@ def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
     """Bias, GELU, and a residual that aliases Y, against the fp64 oracle, on
     the two bf16 tiled paths: grids of fewer than 128 tiles of 128 x 128
     cannot fill the GPU and split-K (fp32 partials in a caller workspace,
-    reduce + epilogue) must engage; larger ones (M=1216 with N=2048 or 2050)
-    run the wave-specialised kernel with its row-wise epilogue, whole-K
-    (no workspace) except at K=8192 (split-K 3, register-staged producers),
-    N=2050 ending in a ragged column group, N=8192 with register-staged
-    producers (config 4's fc1 with its GELU)."""
+    reduce + epilogue) must engage, as for grids of 128-255 such tiles with
+    K >= 6144 (split-K 3, register-staged wave-specialised kernel); the
+    others run the wave-specialised kernel whole-K (no workspace) with its
+    row-wise epilogue: M=1216 with N=2048 or 2050 and K=4096 on 96 x 128
+    tiles (ragged last M tile; N=2050 ends in a ragged column group), N=8192
+    on 160 x 256 tiles parked in two row blocks (config 4's fc1 with its
+    GELU)."""
     import torch
     X, x = bf16_dev(oracle.normal(15, 1, M * K).reshape(M, K), dev)
     W, w = bf16_dev(oracle.normal(15, 2, N * K, 0.02).reshape(N, K), dev)
