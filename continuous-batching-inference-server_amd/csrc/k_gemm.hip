@@ -1143,8 +1143,11 @@ struct SplitPlan {
 
 // Kernel for a bf16 x bf16 problem on the direct-to-LDS paths, from the
 // tile counts (measured on config 4's shapes at M = 1216, TFLOP/s):
-//   < kCUs / 2 tiles of 128 x 128: gemm_bf16_dma_kernel, 64 x 64 tiles or
-//     128 x 128 with split-K (plan_dma_split);
+//   < kCUs / 2 tiles of 128 x 128, or K < 512: gemm_bf16_dma_kernel, 64 x 64
+//     tiles or 128 x 128 with split-K (plan_dma_split); with under 8 K tiles
+//     the wave-specialised kernel's ring fill and parked epilogue cost more
+//     than they save (config 2, M = 4096, K = 256: 9.5 / 14.1 us against
+//     10.8 / 19.1);
 //   < kCUs tiles and K of 96 tiles of 64 or more: split-K 3 on the
 //     register-staged 128 x 128 form (two workgroups per CU: the 3 x tiles
 //     run in one round, each on a third of K).  With weights cold in HBM, as
@@ -1155,17 +1158,17 @@ struct SplitPlan {
 //     (out-projection: 208 tiles of 96 x 128, 535 TFLOP/s against 466 for
 //     160 tiles of 128 x 128);
 //   otherwise the wave-specialised tiling with the least estimated time:
-//     whole rounds of kCUs workgroups times the tile's work, 128 x 256 = 1,
-//     160 x 256 = 1.25, 128 x 128 register-staged (two per CU, 512 per
-//     round) = 1 with a 1.1 penalty for its lower efficiency; ties go to the
-//     larger tile.  qkv: 128 x 256 (742 against 645); fc1: 160 x 256, one
+//     the busiest CU's tiles (tiles spread over kCUs CUs) times a tile's
+//     work, 128 x 256 = 1, 160 x 256 = 1.25, 128 x 128 register-staged = 0.5
+//     with a 1.1 penalty for its lower efficiency (two share a CU); ties go
+//     to the larger tile.  qkv: 128 x 256 (742 against 645); fc1: 160 x 256, one
 //     round of 256 tiles (832 against 685 for 128 x 128 register-staged and
 //     577 for 128 x 256); lm_head: 160 x 256 (832 against 779).
 enum class Bf16Path { kSmall, kWs128, kWs128Split, kWs96, kWs256, kWs160, kWs128R };
 
 Bf16Path choose_bf16(int M, int N, int K) {
   const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
-  if (t128 < kCUs / 2) return Bf16Path::kSmall;
+  if (t128 < kCUs / 2 || K < 512) return Bf16Path::kSmall;
   if (t128 < kCUs && K / 64 >= 96) return Bf16Path::kWs128Split;
   if (t128 < kCUs) {
     const double c96 = 0.75 * cdiv(cdiv(M, 96) * cdiv(N, 128), kCUs);
@@ -1173,7 +1176,7 @@ Bf16Path choose_bf16(int M, int N, int K) {
   }
   const double c160 = 1.25 * cdiv(cdiv(M, 160) * cdiv(N, 256), kCUs);
   const double c256 = 1.0 * cdiv(cdiv(M, 128) * cdiv(N, 256), kCUs);
-  const double c128 = 1.1 * cdiv(t128, 2 * kCUs);
+  const double c128 = 0.55 * cdiv(t128, kCUs);
   if (c160 <= c256 && c160 <= c128) return Bf16Path::kWs160;
   if (c256 <= c128) return Bf16Path::kWs256;
   return Bf16Path::kWs128R;

@@ -339,9 +339,9 @@ def test_gemm_qkv_scatter_epilogue(cbis, oracle, dev, kv_dtype):
 @pytest.mark.parametrize("ydt", ["f32", "bf16"])
 def test_gemm_qkv_scatter_epilogue_wave_specialised(cbis, oracle, dev, M, D, ydt):
     """The fused QKV projection at sizes that run the wave-specialised kernel
-    (M=700, d=1024: 144 tiles of 128 x 128; M=1216, d=2048: config 4, tiles of
-    128 x 256): bf16 K/V straight into page slots, Q in fp32 or bf16, through
-    the row-wise epilogue."""
+    (M=700, d=1024: 96 x 128 tiles; M=1216, d=2048: config 4, 128 x 256
+    tiles): bf16 K/V straight into page slots, Q in fp32 or bf16, through the
+    row-wise epilogue."""
     import torch
     P = M // 16 + 8
     x = oracle.normal(16, 1, M * D).reshape(M, D)
