@@ -24,6 +24,7 @@
 // workgroups sharing a W column block share one L2.
 // Optional split-K (gridDim.z) writes fp32 partials to a caller workspace
 // and a second kernel reduces them and applies the epilogue.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1148,11 +1149,12 @@ struct SplitPlan {
 //     the wave-specialised kernel's ring fill and parked epilogue cost more
 //     than they save (config 2, M = 4096, K = 256: 9.5 / 14.1 us against
 //     10.8 / 19.1);
-//   < kCUs tiles and K of 96 tiles of 64 or more: split-K 3 on the
-//     register-staged 128 x 128 form (two workgroups per CU: the 3 x tiles
-//     run in one round, each on a third of K).  With weights cold in HBM, as
-//     in the step, more loads in flight beat larger tiles (fc2 at M = 1216:
-//     67 us against 79 for 96 x 128 whole-K; warm, 96 x 128 is faster);
+//   < kCUs tiles and K of 96 tiles of 64 or more: 160 x 256 tiles with
+//     split-K into up to 4 parts, about one workgroup per CU.  With weights
+//     cold in HBM, as in the step, this beats whole-K tilings (fc2 at
+//     M = 1216: 64 tiles x 4 splits, 62.4 us cold, against 68.2 for
+//     split-K 3 on 128 x 128 register-staged and 78.5 for 96 x 128 whole-K;
+//     warm, 96 x 128 would be faster);
 //   < kCUs tiles otherwise: wave-specialised 96 x 128 (1 x 4 consumers) when
 //     its tiles need no more rounds than 128 x 128 ones, else 128 x 128
 //     (out-projection: 208 tiles of 96 x 128, 535 TFLOP/s against 466 for
@@ -1164,12 +1166,19 @@ struct SplitPlan {
 //     to the larger tile.  qkv: 128 x 256 (742 against 645); fc1: 160 x 256, one
 //     round of 256 tiles (832 against 685 for 128 x 128 register-staged and
 //     577 for 128 x 256); lm_head: 160 x 256 (832 against 779).
-enum class Bf16Path { kSmall, kWs128, kWs128Split, kWs96, kWs256, kWs160, kWs128R };
+enum class Bf16Path { kSmall, kWs128, kWs160Split, kWs96, kWs256, kWs160, kWs128R };
+
+// Split-K parts for 160 x 256 tiles on a deep-K grid: about one workgroup per
+// CU, at most 4 parts, each of at least 16 K tiles.
+int ws160_splits(int M, int N, int K) {
+  const int64_t t160 = cdiv(M, 160) * cdiv(N, 256);
+  return (int)std::max<int64_t>(1, std::min<int64_t>({4, kCUs / t160, (K / 64) / 16}));
+}
 
 Bf16Path choose_bf16(int M, int N, int K) {
   const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
   if (t128 < kCUs / 2 || K < 512) return Bf16Path::kSmall;
-  if (t128 < kCUs && K / 64 >= 96) return Bf16Path::kWs128Split;
+  if (t128 < kCUs && K / 64 >= 96 && ws160_splits(M, N, K) >= 2) return Bf16Path::kWs160Split;
   if (t128 < kCUs) {
     const double c96 = 0.75 * cdiv(cdiv(M, 96) * cdiv(N, 128), kCUs);
     return c96 < 1.0 ? Bf16Path::kWs96 : Bf16Path::kWs128;
@@ -1188,8 +1197,9 @@ SplitPlan plan_dma_split(int M, int N, int K) {
   const int64_t tiles = cdiv(M, kDmaBM) * cdiv(N, kDmaBN);
   const int kt = K / 64;
   const Bf16Path path = choose_bf16(M, N, K);
-  if (path == Bf16Path::kWs128Split) {
-    const int per = (kt + 2) / 3;
+  if (path == Bf16Path::kWs160Split) {
+    const int ks = ws160_splits(M, N, K);
+    const int per = (kt + ks - 1) / ks;
     p.ksplit = (kt + per - 1) / per;
     p.k_per = per * 64;
     return p;
@@ -1323,8 +1333,8 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
         case Bf16Path::kWs160: return launch_ws<160, 256, 3, 0, 1>(g, s);
         case Bf16Path::kWs128: return launch_ws<128, 128, 3>(g, s);
         case Bf16Path::kWs96: return launch_ws<96, 128, 3, 0, 1>(g, s);
-        case Bf16Path::kWs128Split:
-          return split ? launch_ws<128, 128, 2, 3>(g, s) : launch_ws<96, 128, 3, 0, 1>(g, s);
+        case Bf16Path::kWs160Split:
+          return split ? launch_ws<160, 256, 3, 0, 1>(g, s) : launch_ws<96, 128, 3, 0, 1>(g, s);
         case Bf16Path::kWs128R: return launch_ws<128, 128, 2, 3>(g, s);
         case Bf16Path::kSmall: break;
       }

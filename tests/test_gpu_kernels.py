@@ -192,7 +192,7 @@ def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
     the two bf16 tiled paths: grids of fewer than 128 tiles of 128 x 128
     cannot fill the GPU and split-K (fp32 partials in a caller workspace,
     reduce + epilogue) must engage, as for grids of 128-255 such tiles with
-    K >= 6144 (split-K 3, register-staged wave-specialised kernel); the
+    K >= 6144 (wave-specialised 160 x 256 tiles, split-K up to 4); the
     others run the wave-specialised kernel whole-K (no workspace) with its
     row-wise epilogue: M=1216 with N=2048 or 2050 and K=4096 on 96 x 128
     tiles (ragged last M tile; N=2050 ends in a ragged column group), N=8192
