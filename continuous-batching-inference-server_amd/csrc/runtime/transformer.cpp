@@ -90,15 +90,27 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   std::unordered_map<int, int> index;
   std::vector<int> seqs;
   int width = 1;
+  // Slot of every row, as PagedKVCache::resolve_slot (the same exceptions for
+  // an unknown sequence or a position past its pages); the page list and
+  // table index are looked up once per run of rows of one sequence.
+  const int ps = cfg_.page_size;
+  const std::vector<int>* pages = nullptr;
+  int cur_seq = 0, cur_idx = -1;
   for (int i = 0; i < M; ++i) {
-    cache_.resolve_slot(seq[i], pos[i], &wpage[i], &woff[i]);  // throws like the reference
-    auto it = index.find(seq[i]);
-    if (it == index.end()) {
-      it = index.emplace(seq[i], (int)seqs.size()).first;
-      seqs.push_back(seq[i]);
-      width = std::max(width, (int)cache_.pages(seq[i]).size());
+    if (cur_idx < 0 || seq[i] != cur_seq) {
+      pages = &cache_.pages(seq[i]);  // throws std::out_of_range for an unknown sequence
+      cur_seq = seq[i];
+      auto it = index.find(cur_seq);
+      if (it == index.end()) {
+        it = index.emplace(cur_seq, (int)seqs.size()).first;
+        seqs.push_back(cur_seq);
+        width = std::max(width, (int)pages->size());
+      }
+      cur_idx = it->second;
     }
-    rowbt[i] = it->second;
+    wpage[i] = pages->at(pos[i] / ps);  // throws like the reference
+    woff[i] = pos[i] % ps;
+    rowbt[i] = cur_idx;
   }
   // Rows: runs of consecutive positions of one sequence go to the MFMA
   // prefill kernel (bf16 K/V), everything else to the split-KV decode kernel.
@@ -154,10 +166,11 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   if (!drows.empty()) std::memcpy(h + o_dr, drows.data(), drows.size() * 4);
   if (!tiles.empty()) std::memcpy(h + o_ti, tiles.data(), tiles.size() * 4);
   int* bt = h + o_bt;
-  std::memset(bt, 0, (size_t)n_seqs_ * width * 4);
   for (int s = 0; s < n_seqs_; ++s) {
     const auto& pg = cache_.pages(seqs[s]);
-    std::copy(pg.begin(), pg.end(), bt + (size_t)s * width);
+    int* row = bt + (size_t)s * width;
+    std::copy(pg.begin(), pg.end(), row);
+    std::fill(row + pg.size(), row + width, 0);
   }
   int* d = (int*)d_meta_;
   d_tok_ = d + o_tok; d_pos_ = d + o_pos; d_wpage_ = d + o_wp; d_woff_ = d + o_wo; d_rowbt_ = d + o_rb;
