@@ -167,6 +167,43 @@ __device__ inline float wave_max(float v) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// LayerNorm of one row held by a wave: lane's float4 i covers columns
+// (i * 64 + lane) * 4 .. + 3 (zeros past D); gg / bb are gamma / beta at the
+// same columns.  Mean, then the centred variance, each one wave sum
+// (python/model.py:23-29 with eps); y = (v - mean) * rstd * gamma + beta.
+template <int VPL, typename YT>
+__device__ inline void layernorm_row(const float4* v, const float4* gg, const float4* bb, int lane, int D, float eps,
+                                     YT* y) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  const float mean = wave_sum(s) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 4;
+    if (c < D) {
+      const float a0 = v[i].x - mean, a1 = v[i].y - mean, a2 = v[i].z - mean, a3 = v[i].w - mean;
+      q += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+    }
+  }
+  const float inv = rsqrtf(wave_sum(q) / (float)D + eps);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 4;
+    if (c >= D) continue;
+    const float o0 = (v[i].x - mean) * inv * gg[i].x + bb[i].x;
+    const float o1 = (v[i].y - mean) * inv * gg[i].y + bb[i].y;
+    const float o2 = (v[i].z - mean) * inv * gg[i].z + bb[i].z;
+    const float o3 = (v[i].w - mean) * inv * gg[i].w + bb[i].w;
+    if constexpr (sizeof(YT) == 4) {
+      *(float4*)(y + c) = make_float4(o0, o1, o2, o3);
+    } else {
+      *(uint2*)(y + c) = make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
+    }
+  }
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -500,6 +500,98 @@ inline unsigned splitk_reduce_blocks(const GemmArgs& g) {
   return (unsigned)cdiv((int64_t)g.M * cdiv(g.N, 4), 256);
 }
 
+// The split-K reduce fused with the LayerNorm of the finished rows (the
+// step's x += fc2(h); xn = LayerNorm(x)): one 256-thread workgroup per row of
+// N (a multiple of 4) columns.  The row's float4 chunk i (columns
+// 4 (64 i + lane) .. + 3, as in layernorm_kernel) belongs to wave i % 4, so
+// every wave has VPW chunks and all of a thread's loads -- the KS partials,
+// bias, residual, gamma, beta -- are issued before its first store.
+//
+// The results are bit-identical to splitk_reduce_kernel followed by
+// layernorm_kernel: each chunk is finished in the reduce's order (partials
+// summed z = 0, 1, ..., then bias, then residual) and the LayerNorm sums are
+// formed in layernorm_row's order -- per lane, the chunk terms of chunks
+// 0 .. nch - 1 in turn (nch = layernorm_kernel's chunk count; the mean's sum
+// takes every chunk, the variance's only those inside the row), exchanged
+// through LDS, then the same wave_sum -- with the same per-chunk expressions.
+template <int VPW, int KS, typename LT>
+__global__ __launch_bounds__(256) void splitk_layernorm_kernel(const GemmArgs g, const float* __restrict__ lw,
+                                                                const float* __restrict__ lb, float eps, int nch,
+                                                                LT* __restrict__ ln, int64_t ld_ln) {
+  constexpr int NCH = 4 * VPW;
+  __shared__ float terms[NCH][64];
+  const int row = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int N = g.N;
+  const int64_t MN = (int64_t)g.M * N;
+  const float* pp = g.partial + (int64_t)row * N;
+  const float* rp = g.residual ? g.residual + (int64_t)row * g.ldr : nullptr;
+  float4 v[VPW], p[KS - 1][VPW], bi[VPW], r[VPW], gg[VPW], bb[VPW];
+  // (Assignments under if, not conditional expressions: a ?: between a load
+  // and a local zero is compiled to a load through a selected pointer, the
+  // zero's in scratch memory.)
+#pragma unroll
+  for (int j = 0; j < VPW; ++j) {
+    const int c = ((j * 4 + wave) * 64 + lane) * 4;
+    v[j] = bi[j] = r[j] = gg[j] = bb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int z = 1; z < KS; ++z) p[z - 1][j] = v[j];
+    if (c < N) {
+      v[j] = *(const float4*)(pp + c);
+#pragma unroll
+      for (int z = 1; z < KS; ++z) p[z - 1][j] = *(const float4*)(pp + z * MN + c);
+      if (g.bias) bi[j] = *(const float4*)(g.bias + c);
+      if (rp) r[j] = *(const float4*)(rp + c);
+      gg[j] = *(const float4*)(lw + c);
+      bb[j] = *(const float4*)(lb + c);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < VPW; ++j) {
+    const int i = j * 4 + wave;
+    const int c = (i * 64 + lane) * 4;
+#pragma unroll
+    for (int z = 1; z < KS; ++z) {
+      v[j].x += p[z - 1][j].x; v[j].y += p[z - 1][j].y; v[j].z += p[z - 1][j].z; v[j].w += p[z - 1][j].w;
+    }
+    if (g.bias) { v[j].x += bi[j].x; v[j].y += bi[j].y; v[j].z += bi[j].z; v[j].w += bi[j].w; }
+    if (rp) { v[j].x += r[j].x; v[j].y += r[j].y; v[j].z += r[j].z; v[j].w += r[j].w; }
+    if (c < N) *(float4*)((float*)g.Y + (int64_t)row * g.ldy + c) = v[j];
+    terms[i][lane] = (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < nch; ++i) s += terms[i][lane];
+  const float mean = wave_sum(s) / (float)N;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < VPW; ++j) {
+    const int i = j * 4 + wave;
+    const float a0 = v[j].x - mean, a1 = v[j].y - mean, a2 = v[j].z - mean, a3 = v[j].w - mean;
+    terms[i][lane] = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+  }
+  __syncthreads();
+  float q = 0.f;
+  for (int i = 0; i < nch; ++i)
+    if ((i * 64 + lane) * 4 < N) q += terms[i][lane];
+  const float inv = rsqrtf(wave_sum(q) / (float)N + eps);
+  LT* y = ln + (int64_t)row * ld_ln;
+#pragma unroll
+  for (int j = 0; j < VPW; ++j) {
+    const int c = ((j * 4 + wave) * 64 + lane) * 4;
+    if (c >= N) continue;
+    const float o0 = (v[j].x - mean) * inv * gg[j].x + bb[j].x;
+    const float o1 = (v[j].y - mean) * inv * gg[j].y + bb[j].y;
+    const float o2 = (v[j].z - mean) * inv * gg[j].z + bb[j].z;
+    const float o3 = (v[j].w - mean) * inv * gg[j].w + bb[j].w;
+    if constexpr (sizeof(LT) == 4) {
+      *(float4*)(y + c) = make_float4(o0, o1, o2, o3);
+    } else {
+      *(uint2*)(y + c) = make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // bf16 x bf16 on a multi-stage LDS ring fed by direct-to-LDS loads.
 //
@@ -671,10 +763,7 @@ template <int BM, int BN, int WM, int WN, int STAGES>
 int launch_dma(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
   gemm_bf16_dma_kernel<BM, BN, WM, WN, STAGES><<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, 0, s>>>(g);
-  int rc = check_launch("cbis_gemm(bf16)");
-  if (rc || g.ksplit <= 1) return rc;
-  splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
-  return check_launch("cbis_gemm(split-k reduce)");
+  return check_launch("cbis_gemm(bf16)");
 }
 
 // ---------------------------------------------------------------------------
@@ -938,10 +1027,7 @@ template <int BM, int BN, int STAGES, int REGS = 0, int WM = 2>
 int launch_ws(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
   gemm_bf16_ws_kernel<BM, BN, STAGES, REGS, WM><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
-  int rc = check_launch("cbis_gemm(bf16 ws)");
-  if (rc || g.ksplit <= 1) return rc;
-  splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
-  return check_launch("cbis_gemm(split-k reduce)");
+  return check_launch("cbis_gemm(bf16 ws)");
 }
 
 // ---------------------------------------------------------------------------
@@ -1230,10 +1316,7 @@ int launch(const GemmArgs& g, hipStream_t s) {
     attr_set = true;
   }
   k<<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, lds, s>>>(g);
-  int rc = check_launch("cbis_gemm");
-  if (rc || g.ksplit <= 1) return rc;
-  splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
-  return check_launch("cbis_gemm(split-k reduce)");
+  return check_launch("cbis_gemm");
 }
 
 // Picks a tile shape from the problem size: the largest tile that still
@@ -1252,14 +1335,11 @@ int dispatch(const GemmArgs& g, hipStream_t s) {
   }
 }
 
-}  // namespace
-}  // namespace cbis
-
-using namespace cbis;
-
-extern "C" {
-
-int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
+// Validates the descriptor and launches the product kernel (no split-K
+// reduce); g receives the arguments it ran with (g.ksplit > 1: the raw sums
+// are in the workspace partials and still need their reduce).
+int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g) {
+  g.ksplit = 1;
   CBIS_REQUIRE(d, CBIS_ERR_INVALID, "cbis_gemm: null descriptor");
   CBIS_REQUIRE(d->M >= 0 && d->N > 0 && d->K > 0, CBIS_ERR_INVALID, "cbis_gemm: bad M/N/K %d/%d/%d", d->M, d->N, d->K);
   if (d->M == 0) return CBIS_OK;
@@ -1288,7 +1368,6 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
   }
   CBIS_REQUIRE(!(kv && d->kv_col0 == 0) ? (d->Y != nullptr) : true, CBIS_ERR_INVALID, "cbis_gemm: null Y");
 
-  GemmArgs g;
   g.M = d->M; g.N = d->N; g.K = d->K;
   g.X = d->X; g.ldx = d->ldx;
   g.W = d->W; g.ldw = d->ldw;
@@ -1306,7 +1385,6 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
   g.k_per = d->K;
   g.partial = nullptr;
 
-  hipStream_t s = (hipStream_t)stream;
   // Decode-sized M: weight streaming (K a multiple of 32 for bf16 and fp32,
   // of 64 for fp8; W rows 16-byte aligned).
   const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * we) % 16 == 0;
@@ -1348,6 +1426,74 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
     return dispatch<uint16_t, uint16_t>(g, s);
   }
   return dispatch<uint16_t, uint8_t>(g, s);
+}
+
+int splitk_reduce(const GemmArgs& g, hipStream_t s) {
+  splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
+  return check_launch("cbis_gemm(split-k reduce)");
+}
+}  // namespace
+}  // namespace cbis
+
+using namespace cbis;
+
+extern "C" {
+
+int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream) {
+  hipStream_t s = (hipStream_t)stream;
+  GemmArgs g;
+  const int rc = gemm_run(d, s, g);
+  if (rc || g.ksplit <= 1) return rc;
+  return splitk_reduce(g, s);
+}
+
+int cbis_gemm_layernorm(const cbis_gemm_desc* d, const float* ln_gamma, const float* ln_beta, float eps, int ln_dtype,
+                        void* ln_out, int64_t ld_ln, cbis_stream_t stream) {
+  CBIS_REQUIRE(d, CBIS_ERR_INVALID, "cbis_gemm_layernorm: null descriptor");
+  CBIS_REQUIRE(d->y_dtype == CBIS_F32 && d->k_pool == nullptr && d->Y, CBIS_ERR_INVALID,
+               "cbis_gemm_layernorm: needs an fp32 Y and no K/V scatter");
+  CBIS_REQUIRE(d->N % 4 == 0 && d->N <= 8192, CBIS_ERR_UNSUPPORTED,
+               "cbis_gemm_layernorm: row length %d (needs a multiple of 4, <= 8192)", d->N);
+  CBIS_REQUIRE(ln_gamma && ln_beta && ln_out, CBIS_ERR_INVALID, "cbis_gemm_layernorm: null LayerNorm pointer");
+  CBIS_REQUIRE(ln_dtype == CBIS_F32 || ln_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_gemm_layernorm: ln dtype");
+  CBIS_REQUIRE(ld_ln % 4 == 0 && ((uintptr_t)ln_out & (ln_dtype == CBIS_F32 ? 15u : 7u)) == 0 && d->ldy % 4 == 0 &&
+                   ((uintptr_t)d->Y & 15u) == 0,
+               CBIS_ERR_INVALID, "cbis_gemm_layernorm: misaligned rows");
+  hipStream_t s = (hipStream_t)stream;
+  GemmArgs g;
+  int rc = gemm_run(d, s, g);
+  if (rc || d->M == 0) return rc;
+  // layernorm_kernel's chunk count for this row length (its VPL).
+  int nch = 1;
+  while (nch < cdiv(d->N, 256)) nch *= 2;
+  const int vpw = (nch + 3) / 4;
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const bool fuse = g.ksplit > 1 && g.ksplit <= 4 && vpw <= 4 && !g.gelu && !g.w_scale && a16(g.partial) &&
+                    (!g.bias || a16(g.bias)) && (!g.residual || (a16(g.residual) && g.ldr % 4 == 0)) &&
+                    a16(ln_gamma) && a16(ln_beta);
+  if (!fuse) {
+    if (g.ksplit > 1 && (rc = splitk_reduce(g, s))) return rc;
+    return cbis_layernorm(d->M, d->N, (const float*)d->Y, d->ldy, ln_gamma, ln_beta, eps, ln_dtype, ln_out, ld_ln,
+                          stream);
+  }
+  const dim3 grid((unsigned)d->M);
+#define CBIS_SKLN(V, KS)                                                                                      \
+  if (ln_dtype == CBIS_F32)                                                                                   \
+    splitk_layernorm_kernel<V, KS, float><<<grid, 256, 0, s>>>(g, ln_gamma, ln_beta, eps, nch, (float*)ln_out, \
+                                                                ld_ln);                                       \
+  else                                                                                                        \
+    splitk_layernorm_kernel<V, KS, uint16_t><<<grid, 256, 0, s>>>(g, ln_gamma, ln_beta, eps, nch,              \
+                                                                   (uint16_t*)ln_out, ld_ln);
+#define CBIS_SKLN_KS(V)                      \
+  if (g.ksplit == 2) { CBIS_SKLN(V, 2) }     \
+  else if (g.ksplit == 3) { CBIS_SKLN(V, 3) } \
+  else { CBIS_SKLN(V, 4) }
+  if (vpw <= 1) { CBIS_SKLN_KS(1) }
+  else if (vpw <= 2) { CBIS_SKLN_KS(2) }
+  else { CBIS_SKLN_KS(4) }
+#undef CBIS_SKLN_KS
+#undef CBIS_SKLN
+  return check_launch("cbis_gemm_layernorm(split-k reduce + layernorm)");
 }
 
 size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {

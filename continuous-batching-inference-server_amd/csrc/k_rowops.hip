@@ -88,35 +88,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(int T, int D, const floa
     gg[i] = c < D ? *(const float4*)(g + c) : make_float4(0.f, 0.f, 0.f, 0.f);
     bb[i] = c < D ? *(const float4*)(b + c) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-  const float mean = wave_sum(s) / (float)D;
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int c = (i * 64 + lane) * 4;
-    if (c < D) {
-      const float a0 = v[i].x - mean, a1 = v[i].y - mean, a2 = v[i].z - mean, a3 = v[i].w - mean;
-      q += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
-    }
-  }
-  const float inv = rsqrtf(wave_sum(q) / (float)D + eps);
-  YT* y = Y + (int64_t)row * ldy;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int c = (i * 64 + lane) * 4;
-    if (c >= D) continue;
-    const float o0 = (v[i].x - mean) * inv * gg[i].x + bb[i].x;
-    const float o1 = (v[i].y - mean) * inv * gg[i].y + bb[i].y;
-    const float o2 = (v[i].z - mean) * inv * gg[i].z + bb[i].z;
-    const float o3 = (v[i].w - mean) * inv * gg[i].w + bb[i].w;
-    if constexpr (sizeof(YT) == 4) {
-      *(float4*)(y + c) = make_float4(o0, o1, o2, o3);
-    } else {
-      *(uint2*)(y + c) = make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
-    }
-  }
+  layernorm_row<VPL>(v, gg, bb, lane, D, eps, Y + (int64_t)row * ldy);
 }
 
 __global__ void gelu_kernel(float* X, int64_t n) {

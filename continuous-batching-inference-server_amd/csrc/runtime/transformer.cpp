@@ -215,9 +215,12 @@ void TransformerRunner::enqueue_forward() {
   a.workspace = d_ws_;
   a.workspace_bytes = ws_bytes_;
 
+  // LayerNorms that follow a residual GEMM (ln2 after the out-projection,
+  // the next layer's ln1 or ln_f after fc2) run with it (cbis_gemm_layernorm:
+  // fused with fc2's split-K reduce).
+  cbis_check(cbis_layernorm(M, D, d_x_, D, w_.layers[0].ln1_w, w_.layers[0].ln1_b, 1e-5f, act, d_xn_, D, s), "ln1");
   for (int l = 0; l < cfg_.n_layers; ++l) {
     const LayerWeights& L = w_.layers[l];
-    cbis_check(cbis_layernorm(M, D, d_x_, D, L.ln1_w, L.ln1_b, 1e-5f, act, d_xn_, D, s), "ln1");
     // QKV projection; K and V columns go straight to their page slots.
     g = cbis_gemm_desc{};
     g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
@@ -246,8 +249,7 @@ void TransformerRunner::enqueue_forward() {
     g.w_dtype = wd; g.W = L.wo; g.ldw = D; g.w_scale = L.so;
     g.bias = L.bo; g.residual = d_x_; g.ldr = D;
     g.y_dtype = CBIS_F32; g.Y = d_x_; g.ldy = D;
-    cbis_check(cbis_gemm(&g, s), "out-proj gemm");
-    cbis_check(cbis_layernorm(M, D, d_x_, D, L.ln2_w, L.ln2_b, 1e-5f, act, d_xn_, D, s), "ln2");
+    cbis_check(cbis_gemm_layernorm(&g, L.ln2_w, L.ln2_b, 1e-5f, act, d_xn_, D, s), "out-proj gemm + ln2");
     g = cbis_gemm_desc{};
     g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
     g.M = M; g.N = F; g.K = D;
@@ -263,9 +265,11 @@ void TransformerRunner::enqueue_forward() {
     g.w_dtype = wd; g.W = L.w2; g.ldw = F; g.w_scale = L.s2;
     g.bias = L.b2; g.residual = d_x_; g.ldr = D;
     g.y_dtype = CBIS_F32; g.Y = d_x_; g.ldy = D;
-    cbis_check(cbis_gemm(&g, s), "fc2 gemm");
+    const bool last = l + 1 == cfg_.n_layers;
+    const float* nw = last ? w_.ln_f_w : w_.layers[l + 1].ln1_w;
+    const float* nb = last ? w_.ln_f_b : w_.layers[l + 1].ln1_b;
+    cbis_check(cbis_gemm_layernorm(&g, nw, nb, 1e-5f, act, d_xn_, D, s), last ? "fc2 gemm + ln_f" : "fc2 gemm + ln1");
   }
-  cbis_check(cbis_layernorm(M, D, d_x_, D, w_.ln_f_w, w_.ln_f_b, 1e-5f, act, d_xn_, D, s), "ln_f");
   g = cbis_gemm_desc{};
   g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
   g.M = M; g.N = V; g.K = D;

@@ -139,6 +139,16 @@ size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d);
 
 int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream);
 
+/* cbis_gemm, then a row LayerNorm of its fp32 output Y [M, N] (gamma / beta
+ * of N values, eps) into ln_out (fp32 or bf16, row pitch ld_ln): the step's
+ * "x += h . W2^T + b2; xn = LayerNorm(x)" (src/transformer.cpp:88-89 with the
+ * next layer's layernorm_forward at :70, or the final one at :92).  When the
+ * GEMM splits K the split reduce and the LayerNorm run as one kernel; the
+ * results are those of cbis_gemm followed by cbis_layernorm.  Needs Y fp32
+ * without K/V scatter, N a multiple of 4 and <= 8192. */
+int cbis_gemm_layernorm(const cbis_gemm_desc* d, const float* ln_gamma, const float* ln_beta, float eps,
+                        int ln_dtype, void* ln_out, int64_t ld_ln, cbis_stream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* Paged attention.                                                          */
 /* ----------------------------------------------------------------------- */

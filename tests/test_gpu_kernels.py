@@ -215,6 +215,53 @@ def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
     assert np.abs(Y.cpu().numpy()[rows] - ref).max() < FP32_TOL * 4
 
 
+@pytest.mark.parametrize("M,K", [(1216, 8192), (192, 8192), (1216, 2048)])
+@pytest.mark.parametrize("ln_dt", ["f32", "bf16"])
+def test_gemm_layernorm_matches_gemm_then_layernorm(cbis, oracle, dev, M, K, ln_dt):
+    """cbis_gemm_layernorm (x += h . W^T + b, then LayerNorm(x)) against
+    cbis_gemm followed by cbis_layernorm on the same inputs: bit-identical x
+    and normalised rows, both where K is split (the reduce and the LayerNorm
+    fused: M=1216 and M=192 with K=8192) and where it is not (K=2048)."""
+    import torch
+    N = 2048
+    X, _ = bf16_dev(oracle.normal(17, 1, M * K).reshape(M, K), dev)
+    W, _ = bf16_dev(oracle.normal(17, 2, N * K, 0.02).reshape(N, K), dev)
+    b = to_dev(oracle.normal(17, 3, N, 0.02), dev)
+    x0 = oracle.normal(17, 4, M * N).reshape(M, N)
+    gam = to_dev(1.0 + oracle.normal(17, 5, N, 0.1), dev)
+    bet = to_dev(oracle.normal(17, 6, N, 0.1), dev)
+    code = cbis.F32 if ln_dt == "f32" else cbis.BF16
+    tdt = torch.float32 if ln_dt == "f32" else torch.bfloat16
+    outs = []
+    for fused in (True, False):
+        Y = to_dev(x0, dev)
+        d = cbis.GemmDesc()
+        d.M, d.N, d.K = M, N, K
+        d.x_dtype, d.X, d.ldx = cbis.BF16, ptr(X), K
+        d.w_dtype, d.W, d.ldw = cbis.BF16, ptr(W), K
+        d.bias = ptr(b)
+        d.residual, d.ldr = ptr(Y), N
+        d.y_dtype, d.Y, d.ldy = cbis.F32, ptr(Y), N
+        need = cbis.kernels().cbis_gemm_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+        d.workspace, d.workspace_bytes = ptr(ws), need
+        ln = torch.empty((M, N), dtype=tdt, device=dev)
+        if fused:
+            cbis.check(cbis.kernels().cbis_gemm_layernorm(ctypes.byref(d), ptr(gam), ptr(bet), 1e-5, code, ptr(ln), N,
+                                                           stream()), "cbis_gemm_layernorm")
+        else:
+            cbis.check(cbis.kernels().cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
+            cbis.check(cbis.kernels().cbis_layernorm(M, N, ptr(Y), N, ptr(gam), ptr(bet), 1e-5, code, ptr(ln), N,
+                                                     stream()), "cbis_layernorm")
+        sync()
+        outs.append((Y.cpu().numpy().view(np.uint32), ln.view(torch.int16 if ln_dt == "bf16" else torch.int32).cpu().numpy()))
+        if fused:
+            split = need > 0
+    assert split == (K == 8192)
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
+
+
 @pytest.mark.parametrize("M", [16, 200])
 def test_gemm_fp8_weights(cbis, oracle, dev, M):
     import torch
