@@ -18,13 +18,14 @@
 // log2(e) folded into q), merge through LDS, and either write the output
 // (single split) or fp32 partials (m, l, acc) that a merge kernel combines.
 //
-// Prefill kernel (MFMA).  One workgroup per (32-row query tile, head); its
-// four waves take the key blocks round-robin and merge at the end.  S^T = K Q^T on v_mfma_f32_32x32x16_bf16 with K read straight
+// Prefill kernel (MFMA).  One workgroup per (query tile of up to 64 rows,
+// head pair); a head's two waves take the key blocks round-robin and merge at
+// the end.  S^T = K Q^T on v_mfma_f32_32x32x16_bf16 with K read straight
 // from the pages in the A-operand layout, online softmax per query column,
 // O^T = V^T P^T with P taken from the S^T accumulators in registers (their
 // lane layout is the B-operand layout up to a fixed permutation of the key
-// index, applied to V^T as well) and V^T gathered from an LDS copy of the
-// 32-key V tile.
+// index, applied to V^T as well) and V^T read from an LDS copy of the 32-key
+// V tile with gfx950's transposing LDS read (ds_read_b64_tr_b16).
 #include "common.hpp"
 
 namespace cbis {
@@ -282,16 +283,32 @@ struct PrefillArgs {
   float qscale;  // log2(e) / sqrt(head_dim), applied to S in fp32
 };
 
-// Workgroup: one 32-query tile x HPW adjacent heads, 4 waves per head; a
-// head's 4 waves take its key blocks round-robin (block b goes to wave
-// b % 4) and merge their softmax states through LDS at the end.  A key's
-// head_dim slice is 64 bytes, so adjacent heads of one workgroup read the
-// same 128-byte lines at about the same time.
-constexpr int kPrefillWaves = 4;  // waves per head
-// K/V blocks per wave's register ring.  Two (one block in flight) beat four:
-// the deeper ring costs 32 VGPRs and with them a wave per SIMD (C4's prefill
-// chunks: 32.4 us against 35.7 with four, 35.4 with three).
+// Workgroup: one tile of up to 64 query rows x HPW adjacent heads,
+// kPrefillWaves waves per head.  A head's waves take its 32-key blocks
+// round-robin (block b goes to wave b % kPrefillWaves) and merge their
+// softmax states through LDS at the end.  Each wave runs the tile's rows as
+// kQG groups of 32 query columns against every key block it loads, so a K/V
+// block read from the pages serves 64 queries.  A key's head_dim slice is
+// 64 bytes, so adjacent heads of one workgroup read the same 128-byte lines
+// at about the same time.  Measured on config 4's two 512-row chunks (one
+// layer): 25.1 us against 27.3 for 32-row tiles with four waves per head,
+// 38 with eight.
+constexpr int kPrefillWaves = 2;  // waves per head
+constexpr int kQG = 2;            // 32-query groups per tile
+static_assert(32 * kQG == CBIS_PREFILL_TILE_ROWS, "prefill tile rows");
+// K/V blocks per wave's register ring: one block in flight while one is
+// computed (a deeper ring costs a wave per SIMD and measured slower).
 constexpr int kPrefillRing = 2;
+
+// The two 32-lane halves of v exchanged: each lane gets f(v, v of lane ^ 32)
+// through v_permlane32_swap (no LDS round trip).
+__device__ inline float2 halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 template <int HPW>
 __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel(const PrefillArgs a) {
@@ -306,14 +323,19 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel
   const int row0 = td.x, nvalid = td.y, pos0 = td.w;
   const int* bt = a.bt + (int64_t)td.z * a.bt_stride;
   const int D = a.n_heads * kHD;
-  const int col = lane & 31;  // query index within the tile (B / C column)
+  const int col = lane & 31;  // query index within a group (B / C column)
   const int half = lane >> 5;
 
-  // Q^T as the B operand: lane holds q[col][half*8 + 0..7] (MFMA 0) and
-  // q[col][16 + half*8 + 0..7] (MFMA 1), bf16.
-  bf16x8_t qb0, qb1;
-  {
-    const int qr = row0 + min(col, nvalid - 1);
+  // Q^T of group g as the B operand: lane holds q[32 g + col][half*8 + 0..7]
+  // (MFMA 0) and q[32 g + col][16 + half*8 + 0..7] (MFMA 1), bf16.  Rows past
+  // the tile's end repeat its last row (computed, never stored).
+  bf16x8_t qb0[kQG], qb1[kQG];
+  int qpos[kQG];
+#pragma unroll
+  for (int g = 0; g < kQG; ++g) {
+    const int qi = min(32 * g + col, nvalid - 1);
+    const int qr = row0 + qi;
+    qpos[g] = pos0 + qi;
     float f[16];
     if (a.q_bf16) {
       const uint16_t* qp = (const uint16_t*)a.q + (int64_t)qr * a.ldq + head * kHD;
@@ -332,19 +354,25 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      qb0[e] = (short)f32_to_bf16(f[e]);
-      qb1[e] = (short)f32_to_bf16(f[8 + e]);
+      qb0[g][e] = (short)f32_to_bf16(f[e]);
+      qb1[g][e] = (short)f32_to_bf16(f[8 + e]);
     }
   }
-  const int qpos = pos0 + min(col, nvalid - 1);  // this lane's query position
   const int kv_end = min(pos0 + nvalid, a.max_kv);  // keys [0, kv_end) needed by the tile
 
-  __shared__ uint16_t vt_all[HPW * kPrefillWaves][32][kHD + 2];  // per-wave V tile [key][dim], padded
+  // Per-wave V tile [key][dim], 64-byte rows (8-byte aligned for the
+  // transposing reads).
+  __shared__ __attribute__((aligned(16))) uint16_t vt_all[HPW * kPrefillWaves][32][kHD];
   auto& vt_w = vt_all[wave_id];
-  f32x16_t o;
+  f32x16_t o[kQG];
+  float m[kQG], l[kQG];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = 0.f;
-  float m = -INFINITY, l = 0.f;
+  for (int g = 0; g < kQG; ++g) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[g][i] = 0.f;
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+  }
 
   // K rows for keys j0 + col in the A-operand layout (lane = key, dims
   // half*8.. and 16 + half*8..) and this lane's half of the key's V row.
@@ -352,156 +380,184 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel
     bf16x8_t k0, k1;
     uint4 v0, v1;
   };
-  auto load_block = [&](int j0, KV& r) {
-    // The block's 32 keys span pages j0/16 and j0/16 + 1 (clamped to the
-    // last needed page): two uniform ids, read with scalar loads so the
-    // K/V loads in flight are not waited for.
-    j0 = __builtin_amdgcn_readfirstlane(min(j0, kv_end - 1));
-    const int pg0 = j0 / kPS, pg_last = (kv_end - 1) / kPS;
-    const int id0 = bt[pg0];
-    const int id1 = bt[min(pg0 + 1, pg_last)];
+  // A block's 32 keys span two pages.  Each lane reads the page id of its
+  // own key (id_of) one block before that block's K/V loads (load_block):
+  // the id load then has a whole block of compute to land in, and waiting
+  // for it never waits for the K/V loads in flight.
+  auto id_of = [&](int j0) { return bt[min(j0 + col, kv_end - 1) / kPS]; };
+  auto load_block = [&](int j0, int id, KV& r) {
     const int kc = min(j0 + col, kv_end - 1);
-    int phys = (kc / kPS == pg0) ? id0 : id1;
-    phys = min(max(phys, 0), a.num_pages - 1);
-    const int64_t slot = ((int64_t)phys * kPS + (kc % kPS)) * D + head * kHD;
+    const int phys = min(max(id, 0), a.num_pages - 1);
+    const int64_t slot = (int64_t)phys * (kPS * D) + (kc % kPS) * D + head * kHD;
     r.k0 = *(const bf16x8_t*)(a.kpool + slot + half * 8);
     r.k1 = *(const bf16x8_t*)(a.kpool + slot + 16 + half * 8);
     const uint4* vs = (const uint4*)(a.vpool + slot + half * 16);
     r.v0 = vs[0];
     r.v1 = vs[1];
   };
+  // ds_read_b64_tr_b16 reads in 16-lane groups: lane i of a group receives
+  // element i % 4 of the 8-byte rows addressed by lanes i / 4 + 4 e of the
+  // group, e = 0..3.  Lane (group gq, j) addresses key kr = 4 (gq / 2) + j / 4
+  // (+ 8, 16, 24), dims 16 (gq % 2) + 4 (j % 4) .. + 3, so lane (dim d, half h)
+  // receives V[4 h + e][d] (+ 8, 16, 24): the A-operand layout of V^T below.
+  const int kr = 4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2);
+  const int dc = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  auto vt_read = [&](int key) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4_t*)(__attribute__((address_space(3))) void*)&vt_w[key][dc]);
+  };
   auto compute_block = [&](int j0, const KV& r) {
-    // V tile into LDS: lane (key=col, half) holds dims half*16 .. +15.
     {
-      uint32_t* dst = (uint32_t*)&vt_w[col][half * 16];
-      dst[0] = r.v0.x; dst[1] = r.v0.y; dst[2] = r.v0.z; dst[3] = r.v0.w;
-      dst[4] = r.v1.x; dst[5] = r.v1.y; dst[6] = r.v1.z; dst[7] = r.v1.w;
+      uint4* dst = (uint4*)&vt_w[col][half * 16];  // this lane's key, 16 dims
+      dst[0] = r.v0;
+      dst[1] = r.v1;
     }
-    f32x16_t s;
+    bf16x8_t pb0[kQG], pb1[kQG];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
-    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k0, qb0, s, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k1, qb1, s, 0, 0, 0);
-    // s[i]: key j0 + 8*(i/4) + 4*half + (i%4), query col; raw q.k (the
-    // scale log2(e)/sqrt(hd) > 0 is applied in the exponent).  Only blocks
-    // reaching past the tile's first query position or past kv_end need the
-    // causal mask (uniform test).
-    if (j0 + 31 > pos0 || j0 + 31 >= kv_end) {
+    for (int g = 0; g < kQG; ++g) {
+      f32x16_t s;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] = 0.f;
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k0, qb0[g], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k1, qb1[g], s, 0, 0, 0);
+      // s[i]: key j0 + 8*(i/4) + 4*half + (i%4), query 32 g + col; raw q.k
+      // (the scale log2(e)/sqrt(hd) > 0 is applied in the exponent).  Only
+      // blocks reaching past the group's first query position or past kv_end
+      // need the causal mask (uniform test).
+      if (j0 + 31 > pos0 + 32 * g || j0 + 31 >= kv_end) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kj = j0 + 8 * (i >> 2) + 4 * half + (i & 3);
+          if (kj > qpos[g] || kj >= kv_end) s[i] = -INFINITY;
+        }
+      }
+      float smax = s[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) smax = fmaxf(smax, s[i]);
+      {
+        const float2 h = halves(smax);
+        smax = fmaxf(h.x, h.y);
+      }
+      const float mloc = smax * a.qscale;
+      // A wave's first blocks may hold no key <= qpos for some queries (it
+      // does not start at key 0, and group 1 starts 32 positions later):
+      // while m and mloc are both -inf, the exponents are taken against 0 so
+      // p = 0 and the (empty) state stays 0.
+      const float mn = fmaxf(m[g], mloc);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float corr = fast_exp2(m[g] - mref);
+      float lsum = 0.f;
+      float pf[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int kj = j0 + 8 * (i >> 2) + 4 * half + (i & 3);
-        if (kj > qpos || kj >= kv_end) s[i] = -INFINITY;
+        pf[i] = fast_exp2(fmaf(s[i], a.qscale, -mref));
+        lsum += pf[i];
       }
-    }
-    float smax = s[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) smax = fmaxf(smax, s[i]);
-    smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
-    const float mloc = smax * a.qscale;
-    // A wave's first blocks may hold no key <= qpos for some queries (it
-    // does not start at key 0): while m and mloc are both -inf, the
-    // exponents are taken against 0 so p = 0 and the (empty) state stays 0.
-    const float mn = fmaxf(m, mloc);
-    const float mref = mn == -INFINITY ? 0.f : mn;
-    const float corr = fast_exp2(m - mref);
-    float lsum = 0.f;
-    float pf[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      pf[i] = fast_exp2(fmaf(s[i], a.qscale, -mref));
-      lsum += pf[i];
-    }
-    bf16x8_t pb0, pb1;
-    {
       uint4 u0, u1;
       u0.x = pack_bf16x2(pf[0], pf[1]);   u0.y = pack_bf16x2(pf[2], pf[3]);
       u0.z = pack_bf16x2(pf[4], pf[5]);   u0.w = pack_bf16x2(pf[6], pf[7]);
       u1.x = pack_bf16x2(pf[8], pf[9]);   u1.y = pack_bf16x2(pf[10], pf[11]);
       u1.z = pack_bf16x2(pf[12], pf[13]); u1.w = pack_bf16x2(pf[14], pf[15]);
-      pb0 = __builtin_bit_cast(bf16x8_t, u0);
-      pb1 = __builtin_bit_cast(bf16x8_t, u1);
-    }
-    lsum += __shfl_xor(lsum, 32, 64);
-    l = l * corr + lsum;
-    m = mn;
+      pb0[g] = __builtin_bit_cast(bf16x8_t, u0);
+      pb1[g] = __builtin_bit_cast(bf16x8_t, u1);
+      {
+        const float2 h = halves(lsum);
+        lsum = h.x + h.y;
+      }
+      l[g] = l[g] * corr + lsum;
+      m[g] = mn;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] *= corr;
+      for (int i = 0; i < 16; ++i) o[g][i] *= corr;
+    }
     // V^T as the A operand: lane = dim (col), k-slot e of MFMA b holds key
     // 16*b + 8*(e/4) + 4*half + (e%4), matching P's register order.  The V
     // tile is this wave's own: its LDS writes are complete (lgkmcnt) before
     // its lanes read each other's entries.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
+    const short4_t a0 = vt_read(kr), a1 = vt_read(8 + kr), b0 = vt_read(16 + kr), b1 = vt_read(24 + kr);
     bf16x8_t va0, va1;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int kk = 8 * (e >> 2) + 4 * half + (e & 3);
-      va0[e] = (short)vt_w[kk][col];
-      va1[e] = (short)vt_w[16 + kk][col];
+    for (int e = 0; e < 4; ++e) {
+      va0[e] = a0[e]; va0[4 + e] = a1[e];
+      va1[e] = b0[e]; va1[4 + e] = b1[e];
     }
-    o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va0, pb0, o, 0, 0, 0);
-    o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va1, pb1, o, 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < kQG; ++g) {
+      o[g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va0, pb0[g], o[g], 0, 0, 0);
+      o[g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va1, pb1[g], o[g], 0, 0, 0);
+    }
     // The next block's V writes come after these reads in program order.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
   };
 
-  // This wave's key blocks (wave, wave + 4, ...) stream through a
-  // kPrefillRing-entry register ring: its block i + kPrefillRing - 1 is in
-  // flight while block i is computed.  Loads past the last block are clamped
-  // to key kv_end - 1 (in bounds) and left unused.
+  // This wave's key blocks (wave, wave + kPrefillWaves, ...) stream through
+  // a kPrefillRing-entry register ring: its block i + kPrefillRing - 1 is in
+  // flight while block i is computed, and the page ids of block
+  // i + kPrefillRing with it (ids[i % kPrefillRing]).  Loads past the last
+  // block are clamped to key kv_end - 1 (in bounds) and left unused.
   const int nblk = (kv_end + 31) / 32;
   const int nmine = nblk > wave ? (nblk - wave + kPrefillWaves - 1) / kPrefillWaves : 0;
   auto key0 = [&](int i) { return 32 * (wave + kPrefillWaves * i); };
-  KV ring[kPrefillRing];
+  constexpr int R = kPrefillRing;
+  KV ring[R];
+  int ids[R];
 #pragma unroll
-  for (int u = 0; u < kPrefillRing - 1; ++u) load_block(key0(u), ring[u]);
-  for (int i0 = 0; i0 < nmine; i0 += kPrefillRing) {
+  for (int u = 0; u < R; ++u) ids[u] = id_of(key0(u));
 #pragma unroll
-    for (int u = 0; u < kPrefillRing; ++u) {
-      load_block(key0(i0 + u + kPrefillRing - 1), ring[(u + kPrefillRing - 1) % kPrefillRing]);
+  for (int u = 0; u < R - 1; ++u) load_block(key0(u), ids[u], ring[u]);
+  for (int i0 = 0; i0 < nmine; i0 += R) {
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      ids[u] = id_of(key0(i0 + u + R));
+      load_block(key0(i0 + u + R - 1), ids[(u + R - 1) % R], ring[(u + R - 1) % R]);
       if (i0 + u < nmine) compute_block(key0(i0 + u), ring[u]);
     }
   }
 
   // Merge the waves' (m, l, o) per query column; a wave without blocks has
   // m = -inf and contributes nothing.  Wave 0 always holds key 0.
-  __shared__ float pm_all[HPW][kPrefillWaves][64], pl_all[HPW][kPrefillWaves][64];
-  __shared__ f32x16_t po_all[HPW][kPrefillWaves][64];
-  auto& pm = pm_all[hsub];
-  auto& pl = pl_all[hsub];
-  auto& po = po_all[hsub];
-  pm[wave][lane] = m;
-  pl[wave][lane] = l;
-  po[wave][lane] = o;
+  __shared__ float pm_all[HPW][kPrefillWaves][kQG][64], pl_all[HPW][kPrefillWaves][kQG][64];
+  __shared__ f32x16_t po_all[HPW][kPrefillWaves - 1][kQG][64];
+#pragma unroll
+  for (int g = 0; g < kQG; ++g) {
+    pm_all[hsub][wave][g][lane] = m[g];
+    pl_all[hsub][wave][g][lane] = l[g];
+    if (wave > 0) po_all[hsub][wave - 1][g][lane] = o[g];
+  }
   __syncthreads();
   if (wave != 0) return;
-  float M = m;
 #pragma unroll
-  for (int w = 1; w < kPrefillWaves; ++w) M = fmaxf(M, pm[w][lane]);
-  {
-    const float c0 = fast_exp2(m - M);
-    l *= c0;
+  for (int g = 0; g < kQG; ++g) {
+    float M = m[g];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] *= c0;
-  }
+    for (int w = 1; w < kPrefillWaves; ++w) M = fmaxf(M, pm_all[hsub][w][g][lane]);
+    {
+      const float c0 = fast_exp2(m[g] - M);
+      l[g] *= c0;
 #pragma unroll
-  for (int w = 1; w < kPrefillWaves; ++w) {
-    const float c = fast_exp2(pm[w][lane] - M);
-    l += pl[w][lane] * c;
-    const f32x16_t ow = po[w][lane];
+      for (int i = 0; i < 16; ++i) o[g][i] *= c0;
+    }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] += ow[i] * c;
-  }
-  // o[i]: dim 8*(i/4) + 4*half + (i%4) of query col.
-  if (col < nvalid) {
-    const float inv = 1.f / l;
-    const int64_t ob = (int64_t)(row0 + col) * a.ldo + head * kHD;
+    for (int w = 1; w < kPrefillWaves; ++w) {
+      const float c = fast_exp2(pm_all[hsub][w][g][lane] - M);
+      l[g] += pl_all[hsub][w][g][lane] * c;
+      const f32x16_t ow = po_all[hsub][w - 1][g][lane];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int d = 8 * (i >> 2) + 4 * half + (i & 3);
-      if (a.out_bf16) ((uint16_t*)a.out)[ob + d] = f32_to_bf16(o[i] * inv);
-      else ((float*)a.out)[ob + d] = o[i] * inv;
+      for (int i = 0; i < 16; ++i) o[g][i] += ow[i] * c;
+    }
+    // o[g][i]: dim 8*(i/4) + 4*half + (i%4) of query 32 g + col.
+    const int qi = 32 * g + col;
+    if (qi < nvalid) {
+      const float inv = 1.f / l[g];
+      const int64_t ob = (int64_t)(row0 + qi) * a.ldo + head * kHD;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = 8 * (i >> 2) + 4 * half + (i & 3);
+        if (a.out_bf16) ((uint16_t*)a.out)[ob + d] = f32_to_bf16(o[g][i] * inv);
+        else ((float*)a.out)[ob + d] = o[g][i] * inv;
+      }
     }
   }
 }
@@ -641,8 +697,7 @@ int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int
   a.n_heads = d->n_heads;
   a.max_kv = (int)std::min<int64_t>(d->bt_stride * kPS, 1 << 30);
   a.qscale = kLog2e / sqrtf((float)kHD);
-  // Two heads per workgroup measured best (C4 chunks: 36.7 us vs 42.2 with
-  // one head and 41.7 with four).
+  // Two heads per workgroup (four waves).
   const int hpw = d->n_heads % 2 == 0 ? 2 : 1;
   const int64_t grid = (int64_t)n_tiles * (d->n_heads / hpw);
   if (hpw == 2) paged_prefill_kernel<2><<<(unsigned)grid, 2 * kPrefillWaves * 64, 0, (hipStream_t)stream>>>(a);

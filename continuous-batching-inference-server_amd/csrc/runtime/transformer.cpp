@@ -24,7 +24,7 @@ namespace cbis {
 
 namespace {
 constexpr int kMinPrefillRun = 8;   // runs shorter than this use the decode kernel
-constexpr int kTileRows = 32;       // query rows per prefill tile
+constexpr int kTileRows = CBIS_PREFILL_TILE_ROWS;  // query rows per prefill tile
 constexpr size_t kMaxGraphs = 64;
 size_t align_ints(size_t n) { return (n + 3) & ~(size_t)3; }
 }  // namespace
@@ -137,6 +137,17 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   // order, so the long rows' splits start early and the short ones fill the
   // tail.
   std::stable_sort(drows.begin(), drows.end(), [&](int x, int y) { return pos[x] > pos[y]; });
+  // Likewise the prefill tiles, by their last key (a tile's work grows with it).
+  {
+    const int nt = (int)tiles.size() / 4;
+    std::vector<int> order(nt);
+    for (int t = 0; t < nt; ++t) order[t] = t;
+    auto last_key = [&](int t) { return tiles[4 * t + 3] + tiles[4 * t + 1]; };
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return last_key(x) > last_key(y); });
+    std::vector<int> sorted(tiles.size());
+    for (int t = 0; t < nt; ++t) std::copy_n(&tiles[4 * order[t]], 4, &sorted[4 * t]);
+    tiles.swap(sorted);
+  }
   M_ = M;
   n_decode_ = (int)drows.size();
   n_tiles_ = (int)tiles.size() / 4;

@@ -142,7 +142,8 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream);
 /* cbis_gemm, then a row LayerNorm of its fp32 output Y [M, N] (gamma / beta
  * of N values, eps) into ln_out (fp32 or bf16, row pitch ld_ln): the step's
  * "x += h . W2^T + b2; xn = LayerNorm(x)" (src/transformer.cpp:88-89 with the
- * next layer's layernorm_forward at :70, or the final one at :92).  When the
+ * next layer's layernorm_forward at :69, or the final one at :92; likewise the
+ * out-projection's :81-82 with :84).  When the
  * GEMM splits K the split reduce and the LayerNorm run as one kernel; the
  * results are those of cbis_gemm followed by cbis_layernorm.  Needs Y fp32
  * without K/V scatter, N a multiple of 4 and <= 8192. */
@@ -184,10 +185,14 @@ size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d);
 /* Split-KV decode attention: any set of rows, each with its own kv_len. */
 int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream);
 
-/* Prefill attention on MFMA for query tiles of <= 32 consecutive rows of one
- * sequence.  tiles is a device array [n_tiles][4] of {first_row, n_valid_rows,
- * block_table_row, first_position}; row i of a tile has position
- * first_position + i and attends causally to keys [0, position].
+/* Rows per prefill tile, at most. */
+#define CBIS_PREFILL_TILE_ROWS 64
+
+/* Prefill attention on MFMA for query tiles of <= CBIS_PREFILL_TILE_ROWS
+ * consecutive rows of one sequence.  tiles is a device array [n_tiles][4] of
+ * {first_row, n_valid_rows, block_table_row, first_position}; row i of a tile
+ * has position first_position + i and attends causally to keys [0, position].
+ * Rows of a tile past CBIS_PREFILL_TILE_ROWS are not computed.
  * d->rows / row_bt / row_pos / max_kv_len / split_tokens / workspace are
  * ignored.  Supports bf16 K/V, head_dim 32, page_size 16. */
 int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int* tiles,

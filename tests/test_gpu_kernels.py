@@ -773,10 +773,12 @@ def test_decode_attention_rejects_unsupported(cbis):
     assert cbis.kernels().cbis_paged_attention(ctypes.byref(d), None) == 3
 
 
-@pytest.mark.parametrize("cached,n_rows", [(0, 100), (37, 64), (512, 512)])
-def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows):
+@pytest.mark.parametrize("cached,n_rows,tile", [(0, 100, 64), (37, 64, 64), (512, 512, 64), (37, 70, 32),
+                                                (5, 9, 64)])
+def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows, tile):
     """A chunk of n_rows consecutive positions after `cached` cached tokens
-    (config 4's chunks are (0, 512) and (512, 512))."""
+    (config 4's chunks are (0, 512) and (512, 512)), in tiles of `tile` rows
+    (the runner's 64, ragged last tiles; 32-row tiles are valid too)."""
     import torch
     H, P = 64, 200
     total = cached + n_rows
@@ -790,8 +792,8 @@ def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows):
         cbis.check(K.cbis_fill_normal_fast(ptr(t), dt, t.numel(), s, 1.0, stream()))
     pos = (cached + np.arange(n_rows)).astype(np.int32)
     tiles = []
-    for r in range(0, n_rows, 32):
-        tiles += [r, min(32, n_rows - r), 0, cached + r]
+    for r in range(0, n_rows, tile):
+        tiles += [r, min(tile, n_rows - r), 0, cached + r]
     T = to_dev(np.array(tiles, np.int32), dev)
     out = torch.empty((n_rows, H * 32), dtype=torch.bfloat16, device=dev)
     d = _attn_desc(cbis, n_rows, H, q, kp, vp, P, to_dev(bt, dev), bt.shape[1], None, out, cbis.BF16,
