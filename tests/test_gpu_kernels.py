@@ -215,15 +215,16 @@ def test_gemm_bf16_split_k(cbis, oracle, dev, M, N, K, gelu):
     assert np.abs(Y.cpu().numpy()[rows] - ref).max() < FP32_TOL * 4
 
 
-@pytest.mark.parametrize("M,K", [(1216, 8192), (192, 8192), (1216, 2048)])
+@pytest.mark.parametrize("M,N,K", [(1216, 2048, 8192), (192, 2048, 8192), (1216, 2048, 2048), (300, 1000, 8192),
+                                   (96, 1536, 8192)])
 @pytest.mark.parametrize("ln_dt", ["f32", "bf16"])
-def test_gemm_layernorm_matches_gemm_then_layernorm(cbis, oracle, dev, M, K, ln_dt):
+def test_gemm_layernorm_matches_gemm_then_layernorm(cbis, oracle, dev, M, N, K, ln_dt):
     """cbis_gemm_layernorm (x += h . W^T + b, then LayerNorm(x)) against
     cbis_gemm followed by cbis_layernorm on the same inputs: bit-identical x
     and normalised rows, both where K is split (the reduce and the LayerNorm
-    fused: M=1216 and M=192 with K=8192) and where it is not (K=2048)."""
+    fused: K=8192) and where it is not (K=2048); N=1000 and N=1536 end inside
+    a lane chunk of the fused kernel (chunks past the row)."""
     import torch
-    N = 2048
     X, _ = bf16_dev(oracle.normal(17, 1, M * K).reshape(M, K), dev)
     W, _ = bf16_dev(oracle.normal(17, 2, N * K, 0.02).reshape(N, K), dev)
     b = to_dev(oracle.normal(17, 3, N, 0.02), dev)
