@@ -167,41 +167,55 @@ __device__ inline float wave_max(float v) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// LayerNorm of one row held by a wave: lane's float4 i covers columns
-// (i * 64 + lane) * 4 .. + 3 (zeros past D); gg / bb are gamma / beta at the
-// same columns.  Mean, then the centred variance, each one wave sum
-// (python/model.py:23-29 with eps); y = (v - mean) * rstd * gamma + beta.
-template <int VPL, typename YT>
-__device__ inline void layernorm_row(const float4* v, const float4* gg, const float4* bb, int lane, int D, float eps,
-                                     YT* y) {
+// LayerNorm of one row held by a 256-thread workgroup: the row's float4
+// chunk i (columns 4 (64 i + lane) .. + 3) is v[i / 4] of wave i % 4, gamma /
+// beta likewise.  The statistics are formed per lane over chunks 0 .. nch - 1
+// in turn -- the mean's sum over all of them (chunks past the row hold zeros),
+// the variance's over those inside the row -- exchanged through terms
+// (__shared__ [4 VPW][64]), then reduced across the wave with wave_sum.  Every
+// wave computes the same mean and variance and stores its own chunks.
+template <int VPW, typename YT>
+__device__ inline void ln_block_row(const float4* v, const float4* gg, const float4* bb, int wave, int lane, int N,
+                                    int nch, float eps, float (*terms)[64], YT* y) {
+#pragma unroll
+  for (int j = 0; j < VPW; ++j) terms[j * 4 + wave][lane] = (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  __syncthreads();
   float s = 0.f;
+  for (int i = 0; i < nch; ++i) s += terms[i][lane];
+  const float mean = wave_sum(s) / (float)N;
+  __syncthreads();
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-  const float mean = wave_sum(s) / (float)D;
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int c = (i * 64 + lane) * 4;
-    if (c < D) {
-      const float a0 = v[i].x - mean, a1 = v[i].y - mean, a2 = v[i].z - mean, a3 = v[i].w - mean;
-      q += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
-    }
+  for (int j = 0; j < VPW; ++j) {
+    const float a0 = v[j].x - mean, a1 = v[j].y - mean, a2 = v[j].z - mean, a3 = v[j].w - mean;
+    terms[j * 4 + wave][lane] = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
   }
-  const float inv = rsqrtf(wave_sum(q) / (float)D + eps);
+  __syncthreads();
+  float q = 0.f;
+  for (int i = 0; i < nch; ++i)
+    if ((i * 64 + lane) * 4 < N) q += terms[i][lane];
+  const float inv = rsqrtf(wave_sum(q) / (float)N + eps);
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int c = (i * 64 + lane) * 4;
-    if (c >= D) continue;
-    const float o0 = (v[i].x - mean) * inv * gg[i].x + bb[i].x;
-    const float o1 = (v[i].y - mean) * inv * gg[i].y + bb[i].y;
-    const float o2 = (v[i].z - mean) * inv * gg[i].z + bb[i].z;
-    const float o3 = (v[i].w - mean) * inv * gg[i].w + bb[i].w;
+  for (int j = 0; j < VPW; ++j) {
+    const int c = ((j * 4 + wave) * 64 + lane) * 4;
+    if (c >= N) continue;
+    const float o0 = (v[j].x - mean) * inv * gg[j].x + bb[j].x;
+    const float o1 = (v[j].y - mean) * inv * gg[j].y + bb[j].y;
+    const float o2 = (v[j].z - mean) * inv * gg[j].z + bb[j].z;
+    const float o3 = (v[j].w - mean) * inv * gg[j].w + bb[j].w;
     if constexpr (sizeof(YT) == 4) {
       *(float4*)(y + c) = make_float4(o0, o1, o2, o3);
     } else {
       *(uint2*)(y + c) = make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
     }
   }
+}
+
+// layernorm_kernel's and splitk_layernorm_kernel's chunk count for a row of N
+// columns (a power of two, <= 32 for N <= 8192).
+__host__ __device__ inline int ln_chunks(int N) {
+  int n = 1;
+  while (n * 256 < N) n *= 2;
+  return n;
 }
 
 constexpr float kLog2e = 1.4426950408889634f;

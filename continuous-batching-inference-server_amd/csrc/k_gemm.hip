@@ -503,17 +503,14 @@ inline unsigned splitk_reduce_blocks(const GemmArgs& g) {
 // The split-K reduce fused with the LayerNorm of the finished rows (the
 // step's x += fc2(h); xn = LayerNorm(x)): one 256-thread workgroup per row of
 // N (a multiple of 4) columns.  The row's float4 chunk i (columns
-// 4 (64 i + lane) .. + 3, as in layernorm_kernel) belongs to wave i % 4, so
+// 4 (64 i + lane) .. + 3, as in ln_block_row) belongs to wave i % 4, so
 // every wave has VPW chunks and all of a thread's loads -- the KS partials,
 // bias, residual, gamma, beta -- are issued before its first store.
 //
 // The results are bit-identical to splitk_reduce_kernel followed by
 // layernorm_kernel: each chunk is finished in the reduce's order (partials
-// summed z = 0, 1, ..., then bias, then residual) and the LayerNorm sums are
-// formed in layernorm_row's order -- per lane, the chunk terms of chunks
-// 0 .. nch - 1 in turn (nch = layernorm_kernel's chunk count; the mean's sum
-// takes every chunk, the variance's only those inside the row), exchanged
-// through LDS, then the same wave_sum -- with the same per-chunk expressions.
+// summed z = 0, 1, ..., then bias, then residual) and the row is normalised by
+// the same ln_block_row, with layernorm_kernel's chunk count nch.
 template <int VPW, int KS, typename LT>
 __global__ __launch_bounds__(256) void splitk_layernorm_kernel(const GemmArgs g, const float* __restrict__ lw,
                                                                 const float* __restrict__ lb, float eps, int nch,
@@ -557,39 +554,8 @@ __global__ __launch_bounds__(256) void splitk_layernorm_kernel(const GemmArgs g,
     if (g.bias) { v[j].x += bi[j].x; v[j].y += bi[j].y; v[j].z += bi[j].z; v[j].w += bi[j].w; }
     if (rp) { v[j].x += r[j].x; v[j].y += r[j].y; v[j].z += r[j].z; v[j].w += r[j].w; }
     if (c < N) *(float4*)((float*)g.Y + (int64_t)row * g.ldy + c) = v[j];
-    terms[i][lane] = (v[j].x + v[j].y) + (v[j].z + v[j].w);
   }
-  __syncthreads();
-  float s = 0.f;
-  for (int i = 0; i < nch; ++i) s += terms[i][lane];
-  const float mean = wave_sum(s) / (float)N;
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < VPW; ++j) {
-    const int i = j * 4 + wave;
-    const float a0 = v[j].x - mean, a1 = v[j].y - mean, a2 = v[j].z - mean, a3 = v[j].w - mean;
-    terms[i][lane] = (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
-  }
-  __syncthreads();
-  float q = 0.f;
-  for (int i = 0; i < nch; ++i)
-    if ((i * 64 + lane) * 4 < N) q += terms[i][lane];
-  const float inv = rsqrtf(wave_sum(q) / (float)N + eps);
-  LT* y = ln + (int64_t)row * ld_ln;
-#pragma unroll
-  for (int j = 0; j < VPW; ++j) {
-    const int c = ((j * 4 + wave) * 64 + lane) * 4;
-    if (c >= N) continue;
-    const float o0 = (v[j].x - mean) * inv * gg[j].x + bb[j].x;
-    const float o1 = (v[j].y - mean) * inv * gg[j].y + bb[j].y;
-    const float o2 = (v[j].z - mean) * inv * gg[j].z + bb[j].z;
-    const float o3 = (v[j].w - mean) * inv * gg[j].w + bb[j].w;
-    if constexpr (sizeof(LT) == 4) {
-      *(float4*)(y + c) = make_float4(o0, o1, o2, o3);
-    } else {
-      *(uint2*)(y + c) = make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
-    }
-  }
+  ln_block_row<VPW>(v, gg, bb, wave, lane, N, nch, eps, terms, ln + (int64_t)row * ld_ln);
 }
 
 // ---------------------------------------------------------------------------
@@ -1464,8 +1430,7 @@ int cbis_gemm_layernorm(const cbis_gemm_desc* d, const float* ln_gamma, const fl
   int rc = gemm_run(d, s, g);
   if (rc || d->M == 0) return rc;
   // layernorm_kernel's chunk count for this row length (its VPL).
-  int nch = 1;
-  while (nch < cdiv(d->N, 256)) nch *= 2;
+  const int nch = ln_chunks(d->N);
   const int vpw = (nch + 3) / 4;
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
   const bool fuse = g.ksplit > 1 && g.ksplit <= 4 && vpw <= 4 && !g.gelu && !g.w_scale && a16(g.partial) &&

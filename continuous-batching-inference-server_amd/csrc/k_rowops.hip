@@ -68,27 +68,29 @@ __global__ __launch_bounds__(256) void embed_kernel(int T, int D, const int* __r
 }
 
 // ---------------------------------------------------------------------------
-// LayerNorm: one wave per row; VPL float4 per lane held in registers.
+// LayerNorm: one 256-thread workgroup per row (ln_block_row); every load of
+// the row, gamma and beta is issued before the first reduction.
 // ---------------------------------------------------------------------------
-template <int VPL, typename YT>
-__global__ __launch_bounds__(256) void layernorm_kernel(int T, int D, const float* __restrict__ X, int64_t ldx,
+template <int VPW, typename YT>
+__global__ __launch_bounds__(256) void layernorm_kernel(int D, int nch, const float* __restrict__ X, int64_t ldx,
                                                         const float* __restrict__ g, const float* __restrict__ b,
                                                         float eps, YT* __restrict__ Y, int64_t ldy) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= T) return;
-  const int lane = threadIdx.x & 63;
+  __shared__ float terms[4 * VPW][64];
+  const int row = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float* x = X + (int64_t)row * ldx;
-  float4 v[VPL], gg[VPL], bb[VPL];
-  // gamma / beta are loaded with the row, not after the two reductions, so
-  // the kernel pays one memory round trip before its stores.
+  float4 v[VPW], gg[VPW], bb[VPW];
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int c = (i * 64 + lane) * 4;
-    v[i] = c < D ? *(const float4*)(x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    gg[i] = c < D ? *(const float4*)(g + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    bb[i] = c < D ? *(const float4*)(b + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j = 0; j < VPW; ++j) {
+    const int c = ((j * 4 + wave) * 64 + lane) * 4;
+    v[j] = gg[j] = bb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c < D) {
+      v[j] = *(const float4*)(x + c);
+      gg[j] = *(const float4*)(g + c);
+      bb[j] = *(const float4*)(b + c);
+    }
   }
-  layernorm_row<VPL>(v, gg, bb, lane, D, eps, Y + (int64_t)row * ldy);
+  ln_block_row<VPW>(v, gg, bb, wave, lane, D, nch, eps, terms, Y + (int64_t)row * ldy);
 }
 
 __global__ void gelu_kernel(float* X, int64_t n) {
@@ -298,20 +300,18 @@ int cbis_layernorm(int T, int D, const float* X, int64_t ldx, const float* g, co
   CBIS_REQUIRE(X && g && b && Y, CBIS_ERR_INVALID, "cbis_layernorm: null pointer");
   CBIS_REQUIRE(ldx % 4 == 0 && ldy % 4 == 0 && aligned16(X), CBIS_ERR_INVALID, "cbis_layernorm: misaligned rows");
   hipStream_t s = (hipStream_t)stream;
-  dim3 grid((unsigned)cdiv(T, 4));
-  const int vpl = (int)cdiv(D, 256);
+  const dim3 grid((unsigned)T);
+  const int nch = ln_chunks(D);
 #define CBIS_LN(V)                                                                                         \
   if (y_dtype == CBIS_F32)                                                                                 \
-    layernorm_kernel<V, float><<<grid, 256, 0, s>>>(T, D, X, ldx, g, b, eps, (float*)Y, ldy);             \
+    layernorm_kernel<V, float><<<grid, 256, 0, s>>>(D, nch, X, ldx, g, b, eps, (float*)Y, ldy);           \
   else                                                                                                     \
-    layernorm_kernel<V, uint16_t><<<grid, 256, 0, s>>>(T, D, X, ldx, g, b, eps, (uint16_t*)Y, ldy);
+    layernorm_kernel<V, uint16_t><<<grid, 256, 0, s>>>(D, nch, X, ldx, g, b, eps, (uint16_t*)Y, ldy);
   CBIS_REQUIRE(y_dtype == CBIS_F32 || y_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_layernorm: y dtype");
-  if (vpl <= 1) { CBIS_LN(1) }
-  else if (vpl <= 2) { CBIS_LN(2) }
-  else if (vpl <= 4) { CBIS_LN(4) }
-  else if (vpl <= 8) { CBIS_LN(8) }
-  else if (vpl <= 16) { CBIS_LN(16) }
-  else { CBIS_LN(32) }
+  if (nch <= 4) { CBIS_LN(1) }
+  else if (nch <= 8) { CBIS_LN(2) }
+  else if (nch <= 16) { CBIS_LN(4) }
+  else { CBIS_LN(8) }
 #undef CBIS_LN
   return check_launch("cbis_layernorm");
 }
