@@ -142,8 +142,12 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
 
   const int p_first = t0 / kPS, p_last = (t1 - 1) / kPS;
+  // The page id of a wave's next page is loaded with the current page's K/V,
+  // so its round trip overlaps theirs.
+  int id_next = p_first + wave <= p_last ? bt[p_first + wave] : 0;
   for (int p = p_first + wave; p <= p_last; p += NW) {
-    int phys = bt[p];
+    int phys = id_next;
+    if (p + NW <= p_last) id_next = bt[p + NW];
     phys = min(max(phys, 0), a.num_pages - 1);
     const KVT* kp = kbase + (int64_t)phys * page_stride;
     const KVT* vp = vbase + (int64_t)phys * page_stride;
