@@ -137,13 +137,17 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   // order, so the long rows' splits start early and the short ones fill the
   // tail.
   std::stable_sort(drows.begin(), drows.end(), [&](int x, int y) { return pos[x] > pos[y]; });
-  // Likewise the prefill tiles, by their last key (a tile's work grows with it).
+  // Likewise the prefill tiles, by their last key (a tile's work grows with
+  // it), with the lighter half reversed: when the grid fits one round of
+  // resident workgroups, workgroup w and w + grid/2 share a CU, so the
+  // heaviest tile shares its CU with the lightest (config 4: 25.5 -> 23.3 us).
   {
     const int nt = (int)tiles.size() / 4;
     std::vector<int> order(nt);
     for (int t = 0; t < nt; ++t) order[t] = t;
     auto last_key = [&](int t) { return tiles[4 * t + 3] + tiles[4 * t + 1]; };
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return last_key(x) > last_key(y); });
+    std::reverse(order.begin() + nt / 2, order.end());
     std::vector<int> sorted(tiles.size());
     for (int t = 0; t < nt; ++t) std::copy_n(&tiles[4 * order[t]], 4, &sorted[4 * t]);
     tiles.swap(sorted);
