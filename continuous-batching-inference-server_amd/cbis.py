@@ -95,6 +95,7 @@ KERNEL_SYMBOLS = {
     "cbis_paged_attention_workspace_size": (_SZ, [ctypes.POINTER(AttnDesc)]),
     "cbis_paged_attention": (_I, [ctypes.POINTER(AttnDesc), _P]),
     "cbis_paged_prefill_attention": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
+    "cbis_paged_attention_mixed": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
     "cbis_embed": (_I, [_I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P]),
     "cbis_layernorm": (_I, [_I, _I, _P, _I64, _P, _P, _F, _I, _P, _I64, _P]),
     "cbis_argmax_rows": (_I, [_I, _I, _P, _I64, _P, _P]),

@@ -232,9 +232,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
   }
 }
 
-// Combines split partials: one thread per (row, head, dim).
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a, int n_rows) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// Combines split partials: one thread per (row, head, dim), gid in
+// [0, n_rows * n_heads * head_dim).
+__device__ inline void decode_merge(const DecodeArgs& a, int n_rows, int64_t gid) {
   const int d = (int)(gid % kHD);
   const int64_t rh = gid / kHD;
   const int head = (int)(rh % a.n_heads);
@@ -264,6 +264,10 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArg
   const int64_t o = (int64_t)row * a.ldo + head * kHD + d;
   if (a.out_bf16) ((uint16_t*)a.out)[o] = f32_to_bf16(r);
   else ((float*)a.out)[o] = r;
+}
+
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a, int n_rows) {
+  decode_merge(a, n_rows, (int64_t)blockIdx.x * 256 + threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -314,8 +318,17 @@ __device__ inline float2 halves(float v) {
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
+// Workgroups from prefill_blocks on run the decode rows' split merge
+// (decode_merge over merge_rows rows) instead: the merge then shares the
+// prefill launch, which is independent of it, in place of a launch of its own.
 template <int HPW>
-__global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel(const PrefillArgs a,
+                                                                               const DecodeArgs merge, int merge_rows,
+                                                                               unsigned prefill_blocks) {
+  if (blockIdx.x >= prefill_blocks) {
+    decode_merge(merge, merge_rows, (int64_t)(blockIdx.x - prefill_blocks) * blockDim.x + threadIdx.x);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int wave_id = threadIdx.x >> 6;
   const int wave = wave_id % kPrefillWaves;  // key-block lane of this head
@@ -612,35 +625,17 @@ int validate(const cbis_attn_desc* d, const char* who) {
   return CBIS_OK;
 }
 
-}  // namespace
-}  // namespace cbis
-
-using namespace cbis;
-
-extern "C" {
-
-size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d) {
-  if (!d || d->head_dim != kHD || d->n_heads <= 0) return 0;
-  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
-  int ns = 1;
-  resolve_split(d, std::max(1, d->n_heads / hpb), &ns);
-  if (ns <= 1) return 0;
-  return (size_t)d->n_rows * ns * d->n_heads * kWS * sizeof(float);
-}
-
-int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream) {
-  int rc = validate(d, "cbis_paged_attention");
-  if (rc) return rc;
-  CBIS_REQUIRE(d->row_pos, CBIS_ERR_INVALID, "cbis_paged_attention: null row_pos");
-  if (d->n_rows == 0) return CBIS_OK;
+// Launches the decode kernel for d's rows (d validated, n_rows > 0); *m gets
+// its arguments and *ns its split count -- the split merge is the caller's.
+int decode_launch(const cbis_attn_desc* d, hipStream_t s, DecodeArgs* m, int* ns_out, const char* who) {
   const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
   const int hblocks = d->n_heads / hpb;
   int ns = 1;
   const int split = resolve_split(d, hblocks, &ns);
   if (ns > 1) {
     const size_t need = (size_t)d->n_rows * ns * d->n_heads * kWS * sizeof(float);
-    CBIS_REQUIRE(d->workspace && d->workspace_bytes >= need, CBIS_ERR_WORKSPACE,
-                 "cbis_paged_attention: workspace %zu bytes, need %zu", d->workspace_bytes, need);
+    CBIS_REQUIRE(d->workspace && d->workspace_bytes >= need, CBIS_ERR_WORKSPACE, "%s: workspace %zu bytes, need %zu",
+                 who, d->workspace_bytes, need);
   }
   DecodeArgs a;
   a.rows = d->rows;
@@ -665,26 +660,34 @@ int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream) {
   a.max_kv = (int)std::min<int64_t>(d->bt_stride * kPS, 1 << 30);
   a.qscale = kLog2e / sqrtf((float)kHD);
   const int64_t grid = (int64_t)d->n_rows * ns * hblocks;
-  CBIS_REQUIRE(grid < (1LL << 31), CBIS_ERR_UNSUPPORTED, "cbis_paged_attention: grid too large");
-  hipStream_t s = (hipStream_t)stream;
+  CBIS_REQUIRE(grid < (1LL << 31), CBIS_ERR_UNSUPPORTED, "%s: grid too large", who);
   if (d->kv_dtype == CBIS_F32) paged_decode_kernel<float, 8><<<(unsigned)grid, 512, 0, s>>>(a);
   else paged_decode_kernel<uint16_t, 8><<<(unsigned)grid, 512, 0, s>>>(a);
-  rc = check_launch("cbis_paged_attention");
-  if (rc || ns <= 1) return rc;
-  const int64_t threads = (int64_t)d->n_rows * d->n_heads * kHD;
-  paged_decode_merge_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, s>>>(a, d->n_rows);
+  *m = a;
+  *ns_out = ns;
+  return check_launch(who);
+}
+
+int merge_launch(const DecodeArgs& m, int n_rows, hipStream_t s) {
+  const int64_t threads = (int64_t)n_rows * m.n_heads * kHD;
+  paged_decode_merge_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, s>>>(m, n_rows);
   return check_launch("cbis_paged_attention(merge)");
 }
 
-int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int* tiles, cbis_stream_t stream) {
-  int rc = validate(d, "cbis_paged_prefill_attention");
-  if (rc) return rc;
-  CBIS_REQUIRE(d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_paged_prefill_attention: needs bf16 K/V");
-
-  CBIS_REQUIRE(n_tiles >= 0, CBIS_ERR_INVALID, "cbis_paged_prefill_attention: n_tiles < 0");
+int check_tiles(const cbis_attn_desc* d, int n_tiles, const int* tiles, const char* who) {
+  CBIS_REQUIRE(n_tiles >= 0, CBIS_ERR_INVALID, "%s: n_tiles < 0", who);
   if (n_tiles == 0) return CBIS_OK;
+  CBIS_REQUIRE(d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: prefill tiles need bf16 K/V", who);
   CBIS_REQUIRE(tiles && ((uintptr_t)tiles & 15u) == 0, CBIS_ERR_INVALID,
-               "cbis_paged_prefill_attention: tiles must be a 16-byte aligned device array");
+               "%s: tiles must be a 16-byte aligned device array", who);
+  return CBIS_OK;
+}
+
+// Launches the prefill kernel for n_tiles > 0 tiles; with merge_rows > 0 the
+// launch also runs the split merge of the decode kernel launched before it
+// (arguments *m).
+int prefill_launch(const cbis_attn_desc* d, int n_tiles, const int* tiles, hipStream_t s, const DecodeArgs* m,
+                   int merge_rows, const char* who) {
   PrefillArgs a;
   a.tiles = tiles;
   a.q = d->q;
@@ -703,10 +706,71 @@ int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int
   a.qscale = kLog2e / sqrtf((float)kHD);
   // Two heads per workgroup (four waves).
   const int hpw = d->n_heads % 2 == 0 ? 2 : 1;
-  const int64_t grid = (int64_t)n_tiles * (d->n_heads / hpw);
-  if (hpw == 2) paged_prefill_kernel<2><<<(unsigned)grid, 2 * kPrefillWaves * 64, 0, (hipStream_t)stream>>>(a);
-  else paged_prefill_kernel<1><<<(unsigned)grid, kPrefillWaves * 64, 0, (hipStream_t)stream>>>(a);
-  return check_launch("cbis_paged_prefill_attention");
+  const int block = hpw * kPrefillWaves * 64;
+  const int64_t pgrid = (int64_t)n_tiles * (d->n_heads / hpw);
+  const DecodeArgs none = {};
+  const int64_t mgrid = merge_rows > 0 ? cdiv((int64_t)merge_rows * m->n_heads * kHD, block) : 0;
+  CBIS_REQUIRE(pgrid + mgrid < (1LL << 31), CBIS_ERR_UNSUPPORTED, "%s: grid too large", who);
+  const DecodeArgs& mm = merge_rows > 0 ? *m : none;
+  if (hpw == 2) paged_prefill_kernel<2><<<(unsigned)(pgrid + mgrid), block, 0, s>>>(a, mm, merge_rows, (unsigned)pgrid);
+  else paged_prefill_kernel<1><<<(unsigned)(pgrid + mgrid), block, 0, s>>>(a, mm, merge_rows, (unsigned)pgrid);
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace cbis
+
+using namespace cbis;
+
+extern "C" {
+
+size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d) {
+  if (!d || d->head_dim != kHD || d->n_heads <= 0) return 0;
+  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
+  int ns = 1;
+  resolve_split(d, std::max(1, d->n_heads / hpb), &ns);
+  if (ns <= 1) return 0;
+  return (size_t)d->n_rows * ns * d->n_heads * kWS * sizeof(float);
+}
+
+int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream) {
+  int rc = validate(d, "cbis_paged_attention");
+  if (rc) return rc;
+  CBIS_REQUIRE(d->row_pos, CBIS_ERR_INVALID, "cbis_paged_attention: null row_pos");
+  if (d->n_rows == 0) return CBIS_OK;
+  DecodeArgs m;
+  int ns = 1;
+  hipStream_t s = (hipStream_t)stream;
+  rc = decode_launch(d, s, &m, &ns, "cbis_paged_attention");
+  if (rc || ns <= 1) return rc;
+  return merge_launch(m, d->n_rows, s);
+}
+
+int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int* tiles, cbis_stream_t stream) {
+  int rc = validate(d, "cbis_paged_prefill_attention");
+  if (rc) return rc;
+  rc = check_tiles(d, n_tiles, tiles, "cbis_paged_prefill_attention");
+  if (rc || n_tiles == 0) return rc;
+  return prefill_launch(d, n_tiles, tiles, (hipStream_t)stream, nullptr, 0, "cbis_paged_prefill_attention");
+}
+
+int cbis_paged_attention_mixed(const cbis_attn_desc* d, int n_tiles, const int* tiles, cbis_stream_t stream) {
+  const char* who = "cbis_paged_attention_mixed";
+  int rc = validate(d, who);
+  if (rc) return rc;
+  rc = check_tiles(d, n_tiles, tiles, who);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  DecodeArgs m = {};
+  int ns = 1;
+  if (d->n_rows > 0) {
+    CBIS_REQUIRE(d->row_pos, CBIS_ERR_INVALID, "%s: null row_pos", who);
+    rc = decode_launch(d, s, &m, &ns, who);
+    if (rc) return rc;
+  }
+  const int merge_rows = ns > 1 ? d->n_rows : 0;
+  if (n_tiles > 0) return prefill_launch(d, n_tiles, tiles, s, &m, merge_rows, who);
+  return merge_rows ? merge_launch(m, merge_rows, s) : CBIS_OK;
 }
 
 int cbis_fused_paged_causal_attention(const float* Q, const float* kp, const float* vp, const int* row_page_table,

@@ -250,12 +250,11 @@ void TransformerRunner::enqueue_forward() {
     cbis_check(cbis_gemm(&g, s), "qkv gemm");
     a.k_pool = cache_.k_base(l);
     a.v_pool = cache_.v_base(l);
-    if (n_decode_ > 0) {
-      a.n_rows = n_decode_;
-      a.rows = d_drows_;
-      cbis_check(cbis_paged_attention(&a, s), "decode attention");
-    }
-    if (n_tiles_ > 0) cbis_check(cbis_paged_prefill_attention(&a, n_tiles_, d_tiles_, s), "prefill attention");
+    // Single rows on the split-KV decode kernel, runs of rows on the MFMA
+    // prefill kernel (whose launch also merges the decode rows' splits).
+    a.n_rows = n_decode_;
+    a.rows = d_drows_;
+    cbis_check(cbis_paged_attention_mixed(&a, n_tiles_, d_tiles_, s), "attention");
     // out-projection + bias + residual, in place on x
     g = cbis_gemm_desc{};
     g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;

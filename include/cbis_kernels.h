@@ -198,6 +198,14 @@ int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream);
 int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int* tiles,
                                  cbis_stream_t stream);
 
+/* A step's attention in two launches: cbis_paged_attention over d's rows (the
+ * single decode rows) then cbis_paged_prefill_attention over the tiles, with
+ * the decode rows' split merge run inside the prefill launch instead of a
+ * launch of its own.  Results are those of the two calls.  The forms of
+ * src/transformer.cpp:77-79 (fused_paged_causal_attention over every row of
+ * the step) the runner uses.  Either part may be empty (n_rows / n_tiles 0). */
+int cbis_paged_attention_mixed(const cbis_attn_desc* d, int n_tiles, const int* tiles, cbis_stream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* Row ops.                                                                  */
 /* ----------------------------------------------------------------------- */

@@ -774,6 +774,68 @@ def test_decode_attention_rejects_unsupported(cbis):
     assert cbis.kernels().cbis_paged_attention(ctypes.byref(d), None) == 3
 
 
+@pytest.mark.parametrize("n_dec,with_prefill", [(40, True), (40, False), (0, True)])
+def test_paged_attention_mixed_matches_two_calls(cbis, dev, n_dec, with_prefill):
+    """cbis_paged_attention_mixed (decode rows + prefill tiles, the decode
+    split merge folded into the prefill launch) against cbis_paged_attention
+    followed by cbis_paged_prefill_attention: bit-identical outputs; with and
+    without tiles (the merge then runs on its own) and without decode rows."""
+    import torch
+    H, cached, n_pf = 64, 37, 100
+    kv = rng(11).integers(100, 3000, n_dec).astype(np.int32)
+    n_pages = [int(k + 15) // 16 for k in kv] + [(cached + n_pf + 15) // 16]
+    P = sum(n_pages) + 8
+    perm = rng(12).permutation(P).astype(np.int32)
+    width = max(n_pages)
+    bt = np.zeros((n_dec + 1, width), np.int32)
+    off = 0
+    for i, n in enumerate(n_pages):
+        bt[i, :n] = perm[off:off + n]
+        off += n
+    n_rows = n_dec + n_pf
+    pos = np.concatenate([kv - 1, cached + np.arange(n_pf)]).astype(np.int32)
+    row_bt = np.concatenate([np.arange(n_dec), np.full(n_pf, n_dec)]).astype(np.int32)
+    kp = torch.empty((P, 16, H, 32), dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((n_rows, H * 32), dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    for t, sd, dt in ((kp, 41, cbis.BF16), (vp, 42, cbis.BF16), (q, 43, cbis.F32)):
+        cbis.check(K.cbis_fill_normal_fast(ptr(t), dt, t.numel(), sd, 1.0, stream()))
+    tiles = []
+    if with_prefill:
+        for r in range(0, n_pf, 64):
+            tiles += [n_dec + r, min(64, n_pf - r), n_dec, cached + r]
+    T = to_dev(np.array(tiles or [0, 0, 0, 0], np.int32), dev)
+    BT, POS, RBT = to_dev(bt, dev), to_dev(pos, dev), to_dev(row_bt, dev)
+    ROWS = to_dev(np.arange(max(1, n_dec), dtype=np.int32), dev)
+    outs = []
+    for mixed in (True, False):
+        out = torch.zeros((n_rows, H * 32), dtype=torch.bfloat16, device=dev)
+        d = _attn_desc(cbis, n_dec, H, q, kp, vp, P, BT, width, POS, out, cbis.BF16, out_dtype=cbis.BF16, rows=ROWS,
+                       row_bt=RBT, max_kv=int(kv.max()) if n_dec else 0)
+        need = K.cbis_paged_attention_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+        d.workspace, d.workspace_bytes = ptr(ws), need
+        d.keep_alive = d.keep_alive + (ws,)
+        if n_dec:
+            assert need > 0  # the decode rows split: the merge path is exercised
+        nt = len(tiles) // 4
+        if mixed:
+            cbis.check(K.cbis_paged_attention_mixed(ctypes.byref(d), nt, ptr(T), stream()), "mixed")
+        else:
+            if n_dec:
+                cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream()), "decode")
+            cbis.check(K.cbis_paged_prefill_attention(ctypes.byref(d), nt, ptr(T), stream()), "prefill")
+        sync()
+        outs.append(out.view(torch.int16).cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    written = np.zeros(n_rows, bool)
+    written[:n_dec] = True
+    if with_prefill:
+        written[n_dec:] = True
+    assert (outs[0][written] != 0).any(axis=1).all()
+
+
 @pytest.mark.parametrize("cached,n_rows,tile", [(0, 100, 64), (37, 64, 64), (512, 512, 64), (37, 70, 32),
                                                 (5, 9, 64)])
 def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows, tile):
