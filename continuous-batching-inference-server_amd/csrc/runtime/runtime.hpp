@@ -200,7 +200,7 @@ class TransformerRunner {
 
   // current step
   int M_ = 0;
-  int n_decode_ = 0, n_tiles_ = 0, n_seqs_ = 0, bt_width_ = 0, max_kv_ = 0;
+  int n_decode_ = 0, n_tiles_ = 0, n_seqs_ = 0, bt_width_ = 0, max_kv_ = 0, split_tokens_ = 0;
   size_t meta_bytes_ = 0;
   int *d_tok_ = nullptr, *d_pos_ = nullptr, *d_wpage_ = nullptr, *d_woff_ = nullptr, *d_rowbt_ = nullptr,
       *d_drows_ = nullptr, *d_tiles_ = nullptr, *d_bt_ = nullptr;

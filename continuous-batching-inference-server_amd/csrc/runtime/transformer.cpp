@@ -117,6 +117,7 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   const bool prefill_ok = cfg_.kv_dtype == CBIS_BF16;
   std::vector<int> drows, tiles;
   int max_kv = 1;
+  int64_t sum_kv = 0;
   for (int i = 0; i < M;) {
     int j = i + 1;
     while (j < M && seq[j] == seq[i] && pos[j] == pos[j - 1] + 1) ++j;
@@ -129,6 +130,7 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
       for (int r = i; r < j; ++r) {
         drows.push_back(r);
         max_kv = std::max(max_kv, pos[r] + 1);
+        sum_kv += pos[r] + 1;
       }
     }
     i = j;
@@ -158,6 +160,18 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   n_seqs_ = (int)seqs.size();
   bt_width_ = width;
   max_kv_ = (max_kv + 255) / 256 * 256;  // coarse, so steps share split shapes (and graphs)
+  // Decode rows in one pass each (no split-KV partials, no merge) when they
+  // give at least 1.5 rounds of resident decode workgroups (two per CU, one
+  // per row and head block) and no row is more than twice the mean length:
+  // the rows go longest first and the pass then fills the GPU to the end
+  // (config 4, 768 workgroups: 531 us against 549 with the automatic
+  // 1408-token splits).  Otherwise the attention library splits.
+  {
+    const int hpb = cfg_.kv_dtype == CBIS_BF16 ? 16 : 8;
+    const int64_t units = (int64_t)drows.size() * (cfg_.n_heads / hpb);
+    const bool one_pass = units >= 3 * 512 / 2 && (int64_t)max_kv * (int64_t)drows.size() <= 2 * sum_kv;
+    split_tokens_ = one_pass ? (1 << 30) : 0;
+  }
 
   const size_t o_tok = 0, o_pos = o_tok + align_ints(M), o_wp = o_pos + align_ints(M), o_wo = o_wp + align_ints(M),
                o_rb = o_wo + align_ints(M), o_dr = o_rb + align_ints(M), o_ti = o_dr + align_ints(drows.size()),
@@ -195,7 +209,7 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
 }
 
 std::vector<int> TransformerRunner::signature() const {
-  return {M_, n_decode_, n_tiles_, n_seqs_, bt_width_, max_kv_};
+  return {M_, n_decode_, n_tiles_, n_seqs_, bt_width_, max_kv_, split_tokens_};
 }
 
 void TransformerRunner::enqueue_forward() {
@@ -227,6 +241,7 @@ void TransformerRunner::enqueue_forward() {
   a.out = d_attn_;
   a.ldo = D;
   a.max_kv_len = max_kv_;
+  a.split_tokens = split_tokens_;
   a.workspace = d_ws_;
   a.workspace_bytes = ws_bytes_;
 
