@@ -166,6 +166,10 @@ def decode_attention_timing(cbis, st, iters):
     d.block_table, d.bt_stride, d.row_pos = BT.data_ptr(), width, POS.data_ptr()
     d.out_dtype, d.out, d.ldo = cbis.BF16, out.data_ptr(), H * 32
     d.max_kv_len = int(kv.max())
+    # As TransformerRunner runs these rows: one pass per row (192 rows x 4 head
+    # blocks = 768 workgroups >= 1.5 rounds, no row over twice the mean length).
+    assert n * (H // 16) >= 768 and int(kv.max()) * n <= 2 * int(kv.sum())
+    d.split_tokens = 1 << 30
     need = cbis.kernels().cbis_paged_attention_workspace_size(ctypes.byref(d))
     ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
     d.workspace, d.workspace_bytes = ws.data_ptr(), need
@@ -369,7 +373,7 @@ def run_c4(args, cbis, oracle):
         "config": {"workload": "c4_mixed_step", "model": "gpt-mid L16 d2048 h64x32 mlp8192 V32000",
                    "decode_rows": 192, "decode_kv_len": "U[256,4096]", "prefill_chunks": "2x512 (pos 0, 512)",
                    "rows_per_step": 1216, "page_size": 16, "page_table": "shuffled", "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "kernel": "paged_decode_kernel<bf16> + split merge, one layer",
+        "roofline": {"bound": "hbm", "kernel": "paged_decode_kernel<bf16>, one layer, one pass per row",
                      "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(att_gbs / HBM_PEAK_GBS, 4),
                      "traffic": recorded_traffic("paged_decode_c4_hbm_traffic.md"),
