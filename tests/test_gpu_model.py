@@ -175,6 +175,33 @@ def test_mid_size_mixed_step(cbis, oracle, wdt):
     assert err < 2e-2, err
 
 
+def test_mid_size_step_one_pass_decode_rows(cbis, oracle):
+    """The runner's one-pass decode attention: 192 decode rows (192 x 4 head
+    blocks = 768 workgroups, no row over twice the mean length, as at config
+    4) plus a prefill chunk, on the reduced config-4 model, against the
+    oracle's forward."""
+    cfg, w, cache, om = _mid_setup(cbis, oracle, "bf16", max_pages=1800)
+    ocache = oracle.PagedKVCacheOracle(1800, pages_per_seq=256)
+    runner = cbis.TransformerRunner(w, cache, 512)
+    dec_kv = oracle.uniform_int(6, 4002, 192, 60, 110)
+    tok, pos, sid, osid = [], [], [], []
+    ids = oracle.uniform_int(6, 4003, 300, 0, 31999)
+    k = 0
+    for kv in dec_kv:
+        kv = int(kv)
+        s, o = cache.allocate_sequence(), ocache.allocate_sequence()
+        assert cache.ensure_capacity(s, kv - 1) and ocache.ensure_capacity(o, kv - 1)
+        tok.append(int(ids[k % 300])); pos.append(kv - 1); sid.append(s); osid.append(o); k += 1
+    s, o = cache.allocate_sequence(), ocache.allocate_sequence()
+    assert cache.ensure_capacity(s, 63) and ocache.ensure_capacity(o, 63)
+    for p in range(16, 64):
+        tok.append(int(ids[k % 300])); pos.append(p); sid.append(s); osid.append(o); k += 1
+    got = runner.forward_step(tok, pos, sid)
+    ref = oracle.forward_step_with_cache(om, ocache, tok, pos, osid)
+    err = row_rel_err(got, ref)
+    assert err < 2e-2, err
+
+
 def test_fp8_decode_greedy_tokens(cbis, oracle):
     """Config 5's decode shape, reduced: fp8 weights, bf16 K/V, 4 sequences
     with long synthetic contexts, 4 greedy steps; tokens must match the
