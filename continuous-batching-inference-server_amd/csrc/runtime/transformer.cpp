@@ -161,16 +161,31 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   bt_width_ = width;
   max_kv_ = (max_kv + 255) / 256 * 256;  // coarse, so steps share split shapes (and graphs)
   // Decode rows in one pass each (no split-KV partials, no merge) when they
-  // give at least 1.5 rounds of resident decode workgroups (two per CU, one
-  // per row and head block) and no row is more than twice the mean length:
-  // the rows go longest first and the pass then fills the GPU to the end
-  // (config 4, 768 workgroups: 531 us against 549 with the automatic
-  // 1408-token splits).  Otherwise the attention library splits.
+  // give at least 1.5 rounds of resident decode workgroups (kDecodeSlots: two
+  // per CU, one per row and head block) and no row is more than twice the
+  // mean length: the rows go longest first and the pass then fills the GPU
+  // to the end (config 4, 768 workgroups: 531 us against 549 with 1408-token
+  // splits).  Otherwise splits of about one resident workgroup's share of
+  // the rows' tokens, rounded up to a power of two (config 5, 16 rows x 32k tokens: 4096-token splits, 633
+  // us against 649 with 1024), lengthened until the split partials fit the
+  // workspace (rows x splits <= 2048 + max_rows).  Calls with less than 1024
+  // tokens per resident workgroup keep the attention library's own choice.
   {
+    constexpr int64_t kDecodeSlots = 512;
     const int hpb = cfg_.kv_dtype == CBIS_BF16 ? 16 : 8;
-    const int64_t units = (int64_t)drows.size() * (cfg_.n_heads / hpb);
-    const bool one_pass = units >= 3 * 512 / 2 && (int64_t)max_kv * (int64_t)drows.size() <= 2 * sum_kv;
-    split_tokens_ = one_pass ? (1 << 30) : 0;
+    const int64_t rows = (int64_t)drows.size(), units = rows * (cfg_.n_heads / hpb);
+    split_tokens_ = 0;
+    if (rows > 0 && units >= 3 * kDecodeSlots / 2 && (int64_t)max_kv * rows <= 2 * sum_kv) {
+      split_tokens_ = 1 << 30;
+    } else if (const int64_t share = (sum_kv * (cfg_.n_heads / hpb) + kDecodeSlots - 1) / kDecodeSlots;
+               rows > 0 && share >= 1024) {
+      // A power of two: the split (and with it the step's graph) stays put
+      // while the rows grow by a token per step.
+      int64_t split = 64;
+      while (split < share) split *= 2;
+      while (split < max_kv_ && rows * ((max_kv_ + split - 1) / split) > 2048 + max_rows_) split *= 2;
+      split_tokens_ = (int)std::min<int64_t>(split, 1 << 30);
+    }
   }
 
   const size_t o_tok = 0, o_pos = o_tok + align_ints(M), o_wp = o_pos + align_ints(M), o_wo = o_wp + align_ints(M),
