@@ -7,8 +7,8 @@
 // j % page_size of physical page table[j / page_size] (:79-83), scores are
 // scaled by 1/sqrt(head_dim) (:72) and softmax-normalised (python/model.py:40-44).
 //
-// Decode kernel (HBM-bound).  A workgroup of NW = 8 waves owns one
-// (row, head block, kv split).  A head block is the heads whose head_dim
+// Decode kernel (HBM-bound).  A workgroup of NW = 8 waves (16 for one-pass
+// calls) owns one (row, head block, kv split).  A head block is the heads whose head_dim
 // slices of one token row form 1 KiB: 8 heads for fp32 K/V, 16 for bf16, so
 // one 16-byte-per-lane wave load reads one token's slice of the block fully
 // coalesced, and a 16-token page is 16 such loads at the token stride.  Each
