@@ -165,20 +165,21 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   // per CU, one per row and head block) and no row is more than twice the
   // mean length: the rows go longest first and the pass then fills the GPU
   // to the end (config 4, 768 workgroups: 531 us against 549 with 1408-token
-  // splits).  Otherwise splits of about one resident workgroup's share of
-  // the rows' tokens, rounded up to a power of two (config 5, 16 rows x 32k tokens: 4096-token splits, 633
-  // us against 649 with 1024), lengthened until the split partials fit the
-  // workspace (rows x splits <= 2048 + max_rows).  Calls with less than 1024
-  // tokens per resident workgroup keep the attention library's own choice.
+  // splits).  Otherwise splits of about one CU's share of the rows' tokens,
+  // rounded up to a power of two (config 5, 16 rows x 32k tokens: 8192-token
+  // splits, 256 workgroups: 624 us against 632 with 4096, 639 with 2048 and
+  // 649 with the library's 1024), lengthened until the split partials fit the
+  // workspace (rows x splits <= 2048 + max_rows).  Calls with less than 2048
+  // tokens per CU keep the attention library's own choice.
   {
-    constexpr int64_t kDecodeSlots = 512;
+    constexpr int64_t kDecodeSlots = 512, kCUs = 256;
     const int hpb = cfg_.kv_dtype == CBIS_BF16 ? 16 : 8;
     const int64_t rows = (int64_t)drows.size(), units = rows * (cfg_.n_heads / hpb);
     split_tokens_ = 0;
     if (rows > 0 && units >= 3 * kDecodeSlots / 2 && (int64_t)max_kv * rows <= 2 * sum_kv) {
       split_tokens_ = 1 << 30;
-    } else if (const int64_t share = (sum_kv * (cfg_.n_heads / hpb) + kDecodeSlots - 1) / kDecodeSlots;
-               rows > 0 && share >= 1024) {
+    } else if (const int64_t share = (sum_kv * (cfg_.n_heads / hpb) + kCUs - 1) / kCUs;
+               rows > 0 && share >= 2048) {
       // A power of two: the split (and with it the step's graph) stays put
       // while the rows grow by a token per step.
       int64_t split = 64;
