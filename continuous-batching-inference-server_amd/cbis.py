@@ -136,6 +136,7 @@ RUNTIME_SYMBOLS = {
     "cbis_runner_logits_device": (_P, [_P]),
     "cbis_runner_stream": (_P, [_P]),
     "cbis_runner_set_graphs": (None, [_P, _I]),
+    "cbis_runner_last_plan": (_I, [_P, _IP, _I]),
     "cbis_run_continuous": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _IP, ctypes.POINTER(ctypes.c_double), _I]),
     "cbis_eviction_params_default": (None, [ctypes.POINTER(EvictionParams)]),
     "cbis_tiered_create": (_P, [_I, _I, _I, _I, _I, ctypes.c_char_p, _SZ, _SZ, ctypes.POINTER(EvictionParams)]),
@@ -389,6 +390,15 @@ class TransformerRunner:
 
     def set_graphs(self, enable: bool) -> None:
         runtime().cbis_runner_set_graphs(self._h, int(enable))
+
+    PLAN_FIELDS = ("rows", "decode_rows", "prefill_tiles", "sequences", "bt_width", "max_kv", "split_tokens")
+
+    def last_plan(self) -> dict:
+        """How the last step ran; split_tokens 1 << 30 = one pass per decode
+        row, 0 = the attention library's automatic split."""
+        out = (ctypes.c_int * len(self.PLAN_FIELDS))()
+        n = _rt_check(runtime().cbis_runner_last_plan(self._h, out, len(out)), "last_plan")
+        return dict(zip(self.PLAN_FIELDS, list(out[:n])))
 
 
 TIERS = {"GPU": 0, "DRAM": 1, "NVME": 2}

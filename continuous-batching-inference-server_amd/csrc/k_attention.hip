@@ -9,7 +9,8 @@
 //
 // Decode kernel (HBM-bound).  A workgroup of NW = 8 waves (16 for one-pass
 // calls) owns one (row, head block, kv split).  A head block is the heads whose head_dim
-// slices of one token row form 1 KiB: 8 heads for fp32 K/V, 16 for bf16, so
+// slices of one token row form 1 KiB: 8 heads for fp32 K/V, 16 for bf16 (the
+// last block of a head count that is not a multiple is partial), so
 // one 16-byte-per-lane wave load reads one token's slice of the block fully
 // coalesced, and a 16-token page is 16 such loads at the token stride.  Each
 // lane holds 4 (fp32) or 8 (bf16) dims of one head; q.k is finished with
@@ -115,10 +116,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
   const int nsplit_row = min((kv_len + a.split_tokens - 1) / a.split_tokens, a.n_splits);
   const int* bt = a.bt + (int64_t)(a.row_bt ? a.row_bt[row] : row) * a.bt_stride;
 
+  // The last head block may be partial (n_heads not a multiple of HPB): its
+  // lanes past the last head read that head's slice (in bounds) and store
+  // nothing.
   const int head = hb * HPB + lane / G;
+  const bool head_ok = head < a.n_heads;
   const int sub = lane % G;
   const int D = a.n_heads * kHD;
-  const int lane_off = head * kHD + sub * EPL;
+  const int lane_off = min(head, a.n_heads - 1) * kHD + sub * EPL;
 
   float q[EPL];
   if (a.q_bf16) {
@@ -210,6 +215,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
 #pragma unroll
     for (int e = 0; e < EPL; ++e) O[e] += sacc[w][e][lane] * c;
   }
+  if (!head_ok) return;
   if (nsplit_row == 1) {
     const float inv = 1.f / L;
     if (a.out_bf16) {
@@ -607,14 +613,21 @@ int resolve_split(const cbis_attn_desc* d, int hblocks, int* n_splits) {
   return split;
 }
 
+// Head blocks of a decode call: 1 KiB of one token's K (or V) row each, 8
+// heads of fp32 or 16 of bf16; the last one may be partial.
+int head_blocks(const cbis_attn_desc* d) {
+  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
+  return (int)cdiv(d->n_heads, hpb);
+}
+
 int validate(const cbis_attn_desc* d, const char* who) {
   CBIS_REQUIRE(d, CBIS_ERR_INVALID, "%s: null descriptor", who);
   CBIS_REQUIRE(d->head_dim == kHD && d->page_size == kPS, CBIS_ERR_UNSUPPORTED,
                "%s: head_dim %d / page_size %d (this build supports 32 / 16)", who, d->head_dim, d->page_size);
   CBIS_REQUIRE(d->kv_dtype == CBIS_F32 || d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: kv dtype", who);
-  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
-  CBIS_REQUIRE(d->n_heads > 0 && d->n_heads % hpb == 0, CBIS_ERR_UNSUPPORTED,
-               "%s: n_heads %d must be a multiple of %d for this K/V dtype", who, d->n_heads, hpb);
+  CBIS_REQUIRE(d->n_heads > 0, CBIS_ERR_INVALID, "%s: n_heads %d", who, d->n_heads);
+  CBIS_REQUIRE(d->split_tokens <= 0 || d->split_tokens % kPS == 0, CBIS_ERR_INVALID,
+               "%s: split_tokens %d must be a multiple of page_size %d", who, d->split_tokens, kPS);
   CBIS_REQUIRE(d->q_dtype == CBIS_F32 || d->q_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: q dtype", who);
   CBIS_REQUIRE(d->out_dtype == CBIS_F32 || d->out_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: out dtype", who);
   CBIS_REQUIRE(d->n_rows >= 0 && d->num_pages > 0 && d->bt_stride > 0, CBIS_ERR_INVALID, "%s: bad sizes", who);
@@ -628,8 +641,7 @@ int validate(const cbis_attn_desc* d, const char* who) {
 // Launches the decode kernel for d's rows (d validated, n_rows > 0); *m gets
 // its arguments and *ns its split count -- the split merge is the caller's.
 int decode_launch(const cbis_attn_desc* d, hipStream_t s, DecodeArgs* m, int* ns_out, const char* who) {
-  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
-  const int hblocks = d->n_heads / hpb;
+  const int hblocks = head_blocks(d);
   int ns = 1;
   const int split = resolve_split(d, hblocks, &ns);
   if (ns > 1) {
@@ -735,9 +747,9 @@ extern "C" {
 
 size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d) {
   if (!d || d->head_dim != kHD || d->n_heads <= 0) return 0;
-  const int hpb = d->kv_dtype == CBIS_F32 ? 8 : 16;
+  if (d->split_tokens > 0 && d->split_tokens % kPS != 0) return 0;  // refused by the launch
   int ns = 1;
-  resolve_split(d, std::max(1, d->n_heads / hpb), &ns);
+  resolve_split(d, head_blocks(d), &ns);
   if (ns <= 1) return 0;
   return (size_t)d->n_rows * ns * d->n_heads * kWS * sizeof(float);
 }

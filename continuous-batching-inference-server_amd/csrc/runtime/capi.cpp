@@ -240,6 +240,14 @@ void* cbis_runner_stream(cbis_runner* r) { return (void*)r->impl->stream(); }
 
 void cbis_runner_set_graphs(cbis_runner* r, int enable) { r->impl->set_graphs(enable != 0); }
 
+int cbis_runner_last_plan(const cbis_runner* r, int* out, int capacity) {
+  return guard([&] {
+    const std::vector<int> p = r->impl->last_plan();
+    for (int i = 0; i < capacity && i < (int)p.size(); ++i) out[i] = p[i];
+    return (int)p.size();
+  });
+}
+
 namespace {
 std::vector<Request> make_requests(int n_requests, const int* prompt_lens, const int* prompt_tokens,
                                    const int* decode_lens) {

@@ -187,9 +187,20 @@ std::unique_ptr<ModelWeights> ModelWeights::synthetic(const ModelConfig& cfg, ui
 }
 
 std::unique_ptr<ModelWeights> ModelWeights::load(const std::string& path, const ModelConfig& cfg) {
+  cfg.validate();
   std::ifstream f(path, std::ios::binary | std::ios::ate);
   if (!f) throw std::runtime_error("cannot open " + path);
   const size_t nbytes = (size_t)f.tellg();
+  // The file is the config's fp32 tensors back to back, nothing else
+  // (python/export_weights.py:42-66): a size that differs means other dims.
+  {
+    const size_t D = cfg.d_model, F = cfg.mlp, V = cfg.vocab, S = cfg.max_seq;
+    const size_t per_layer = 2 * D + 4 * (D * D + D) + 2 * D + F * D + F + D * F + D;
+    const size_t want = (V * D + S * D + cfg.n_layers * per_layer + 2 * D + V * D) * 4;
+    if (nbytes != want)
+      throw std::runtime_error("weights.bin: " + std::to_string(nbytes) + " bytes, the config's tensors are " +
+                               std::to_string(want) + " bytes");
+  }
   f.seekg(0);
   std::vector<float> buf(nbytes / 4);
   f.read(reinterpret_cast<char*>(buf.data()), (std::streamsize)(buf.size() * 4));

@@ -166,9 +166,12 @@ class TransformerRunner {
   const float* logits_device() const { return d_logits_; }
   hipStream_t stream() const { return stream_; }
   void set_graphs(bool on) { use_graphs_ = on; }
+  // How the last step ran: {rows, decode rows, prefill tiles, sequences,
+  // block-table width, max_kv bound, decode split_tokens (1 << 30: one pass
+  // per row; 0: the attention library's own split)}.
+  std::vector<int> last_plan() const { return signature(); }
 
  private:
-  struct StepPlan;
   void prepare(const int* tok, const int* pos, const int* seq, int M);
   void enqueue_forward();
   void run_step(bool greedy);

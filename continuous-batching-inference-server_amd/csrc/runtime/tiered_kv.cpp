@@ -306,6 +306,20 @@ void TieredKVBlockManager::restore_batch(const std::vector<uint64_t>& ids, Paged
     if (!seen_ids.insert(ids[i]).second) throw std::invalid_argument("restore: block listed twice");
     if (!seen_pages.insert(pages[i]).second) throw std::invalid_argument("restore: destination page listed twice");
   }
+  // A GPU-resident block of the batch is read from its current page before
+  // any page is written.  One restore() after another would read it after
+  // the earlier blocks' writes, so a batch in which an earlier block's
+  // destination is a later moved block's current page (whose bytes those
+  // calls would lose) is refused rather than given other data.
+  {
+    std::set<int> written;
+    for (size_t i = 0; i < ids.size(); ++i) {
+      const BlockMeta& m = meta_.at(ids[i]);
+      if (m.tier == Tier::GPU && m.cache == &cache && written.count(m.physical_page))
+        throw std::invalid_argument("restore: a block's current page is an earlier block's destination");
+      written.insert(pages[i]);
+    }
+  }
   const size_t chunk = std::max<size_t>(1, kStageBytes / raw_block_bytes_);
   for (size_t c0 = 0; c0 < ids.size(); c0 += chunk) {
     const size_t n = std::min(chunk, ids.size() - c0);
@@ -333,10 +347,22 @@ void TieredKVBlockManager::restore_batch(const std::vector<uint64_t>& ids, Paged
       else if (m.tier == Tier::NVME) inflate_block(from_disk[i].data(), from_disk[i].size(), dst, raw_block_bytes_);
       else std::memcpy(dst, moved[i].data(), raw_block_bytes_);
     }
-    // 2. One copy and one scatter into the destination pages.
-    scatter_from_host(cache, std::vector<int>(pages.begin() + c0, pages.begin() + c0 + n));
-    // 3. Bookkeeping in order, as one restore() after another
-    //    (src/tiered_kv_manager.cpp:173-208).
+    // 2. Scatter into the destination pages and do the bookkeeping in order,
+    //    as one restore() after another (src/tiered_kv_manager.cpp:173-208):
+    //    block i's page is written, then a full GPU tier evicts a victim,
+    //    which reads its page.  The writes of blocks [w, i] are issued as one
+    //    copy and one scatter right before such an eviction (so a victim
+    //    whose page is a later block's destination still spills its own
+    //    bytes), the remaining ones at the end of the chunk.  Staging slots
+    //    below w are done with: the victim's spill may reuse slot 0.
+    size_t w = 0;
+    auto flush = [&](size_t upto) {
+      if (upto <= w) return;
+      // scatter_from_host sends staging slots 0.. : move slots [w, upto) down.
+      if (w > 0) std::memmove(host_stage_, host_stage_ + w * raw_block_bytes_, (upto - w) * raw_block_bytes_);
+      scatter_from_host(cache, std::vector<int>(pages.begin() + c0 + w, pages.begin() + c0 + upto));
+      w = upto;
+    };
     for (size_t i = 0; i < n; ++i) {
       BlockMeta& m = meta_.at(ids[c0 + i]);
       const bool was_gpu = m.tier == Tier::GPU;
@@ -345,7 +371,10 @@ void TieredKVBlockManager::restore_batch(const std::vector<uint64_t>& ids, Paged
         m.dram_bytes.clear();
         m.dram_bytes.shrink_to_fit();
       }
-      if (!was_gpu && gpu_resident_count_ >= gpu_capacity_blocks_) evict_one(now_step);
+      if (!was_gpu && gpu_resident_count_ >= gpu_capacity_blocks_) {
+        flush(i + 1);
+        evict_one(now_step);
+      }
       m.tier = Tier::GPU;
       m.cache = &cache;
       m.physical_page = pages[c0 + i];
@@ -353,6 +382,7 @@ void TieredKVBlockManager::restore_batch(const std::vector<uint64_t>& ids, Paged
       m.last_access_step = now_step;
       if (!was_gpu) ++gpu_resident_count_;
     }
+    flush(n);
   }
 }
 

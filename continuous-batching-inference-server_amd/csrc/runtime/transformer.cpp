@@ -37,11 +37,8 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
       cache.page_size() != cfg_.page_size || cache.kv_dtype() != cfg_.kv_dtype)
     throw std::invalid_argument("TransformerRunner: cache geometry does not match the model config");
   if (!cache.has_device()) throw std::invalid_argument("TransformerRunner: cache has no device pools");
-  // The attention kernels read a page row in 1 KiB head blocks: 8 heads of
-  // fp32 or 16 heads of bf16 (head_dim 32).
-  if (cfg_.head_dim != 32 || cfg_.n_heads % (cfg_.kv_dtype == CBIS_BF16 ? 16 : 8) != 0)
-    throw std::invalid_argument("TransformerRunner: attention needs head_dim 32 and n_heads a multiple of 8 (fp32 "
-                                "K/V) or 16 (bf16 K/V)");
+  // The attention kernels are built for head_dim 32 (any head count).
+  if (cfg_.head_dim != 32) throw std::invalid_argument("TransformerRunner: attention needs head_dim 32");
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
   const size_t R = max_total_rows, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
   const size_t ae = dtype_size(cfg_.act_dtype());
@@ -174,11 +171,12 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
   {
     constexpr int64_t kDecodeSlots = 512, kCUs = 256;
     const int hpb = cfg_.kv_dtype == CBIS_BF16 ? 16 : 8;
-    const int64_t rows = (int64_t)drows.size(), units = rows * (cfg_.n_heads / hpb);
+    const int64_t hblocks = (cfg_.n_heads + hpb - 1) / hpb;
+    const int64_t rows = (int64_t)drows.size(), units = rows * hblocks;
     split_tokens_ = 0;
     if (rows > 0 && units >= 3 * kDecodeSlots / 2 && (int64_t)max_kv * rows <= 2 * sum_kv) {
       split_tokens_ = 1 << 30;
-    } else if (const int64_t share = (sum_kv * (cfg_.n_heads / hpb) + kCUs - 1) / kCUs;
+    } else if (const int64_t share = (sum_kv * hblocks + kCUs - 1) / kCUs;
                rows > 0 && share >= 2048) {
       // A power of two: the split (and with it the step's graph) stays put
       // while the rows grow by a token per step.

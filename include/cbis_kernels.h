@@ -90,7 +90,7 @@ int cbis_scatter_kv_to_cache(const float* K_proj, const float* V_proj, float* k_
  * Replaces fused_paged_causal_attention, include/attention.hpp:29-33
  * (kernels/attention.cu:57-127).  Runs the wave64 decode kernel in a single
  * pass per (row, head block): it needs no workspace.  Supported: head_dim 32,
- * page_size 16, n_heads a multiple of 8. */
+ * page_size 16, any n_heads (the reference's grid(total_rows, n_heads)). */
 int cbis_fused_paged_causal_attention(const float* Q_proj, const float* k_pages, const float* v_pages,
                                       const int* row_page_table, const int* row_query_pos, float* attn_out,
                                       int total_rows, int n_heads, int head_dim, int page_size,
@@ -173,7 +173,8 @@ typedef struct cbis_attn_desc {
   void* out;               /* [*, n_heads*head_dim], row stride ldo elements */
   int64_t ldo;
   int max_kv_len;          /* host upper bound of pos+1 over the rows */
-  int split_tokens;        /* tokens per split-KV chunk (multiple of page_size), 0 = auto */
+  int split_tokens;        /* tokens per split-KV chunk, 0 = auto; a multiple of
+                              page_size, else the call fails with CBIS_ERR_INVALID */
   void* workspace;         /* fp32 partials when a row needs more than one split */
   size_t workspace_bytes;
 } cbis_attn_desc;

@@ -101,6 +101,11 @@ const float* cbis_runner_logits_device(cbis_runner* r);
 void* cbis_runner_stream(cbis_runner* r);
 /* Enable / disable HIP-graph replay of steps whose shape repeats. */
 void cbis_runner_set_graphs(cbis_runner* r, int enable);
+/* How the last step ran (no reference counterpart: a diagnostic):
+ * {rows, decode rows, prefill tiles, sequences, block-table width, max_kv
+ * bound, decode split_tokens (1 << 30 = one pass per row, 0 = the attention
+ * library's automatic split)}.  Writes min(capacity, 7) ints; returns 7. */
+int cbis_runner_last_plan(const cbis_runner* r, int* out, int capacity);
 
 /* ---- Three-tier KV block manager (include/tiered_kv_manager.hpp:21-151,
  *      include/block_storage.hpp:9-64) --------------------------------------

@@ -583,3 +583,14 @@ def c1_requests(seed: int = 0, n: int = 8, vocab: int = 512, lo: int = 16, hi: i
         toks = uniform_int(seed, STREAM_C1_TOKENS, int(lens[i]), 0, vocab - 1, start=i * 4096)
         reqs.append(Request([int(t) for t in toks], decode_len))
     return reqs
+
+
+def scatter_kv(K, V, kpool, vpool, wpage, woff, page_size, kv_dtype=0) -> None:
+    """In place: kpool/vpool[page][slot] = K/V rows (kernels/attention.cu:7-19);
+    pools float32 (kv_dtype 0) or uint16 bf16 bits (kv_dtype 1)."""
+    Kd = np.ascontiguousarray(K, dtype=np.float64)
+    Vd = np.ascontiguousarray(V, dtype=np.float64)
+    M, D = Kd.shape
+    assert kpool.flags.c_contiguous and vpool.flags.c_contiguous
+    lib().orc_scatter_kv(M, D, _ptr(Kd), _ptr(Vd), _ptr(kpool), _ptr(vpool), kv_dtype, _ptr(_i32(wpage)),
+                         _ptr(_i32(woff)), page_size)

@@ -46,3 +46,18 @@ def row_rel_err(got, ref):
 
 def rng(seed):
     return np.random.default_rng(seed)
+
+
+def write_weights_bin(path, weights):
+    """Writes oracle Weights' fp32 master tensors as the reference's
+    weights.bin: python/export_weights.py:42-66 order, raw little-endian fp32,
+    nothing else."""
+    spec, m = weights.spec, weights.master
+    names = ["tok_emb", "pos_emb"]
+    for l in range(spec.n_layers):
+        names += [f"l{l}.{n}" for n in ("ln1_w", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+                                         "ln2_w", "ln2_b", "fc1", "b1", "fc2", "b2")]
+    names += ["ln_f_w", "ln_f_b", "lm_head"]
+    with open(path, "wb") as f:
+        for n in names:
+            f.write(np.ascontiguousarray(m[n], dtype="<f4").tobytes())

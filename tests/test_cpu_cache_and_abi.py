@@ -163,6 +163,16 @@ def test_abi_validation_without_gpu(cbis):
     assert K.cbis_paged_attention(ctypes.byref(a), None) == 3  # needs a workspace
     need = K.cbis_paged_attention_workspace_size(ctypes.byref(a))
     assert need == 4 * 64 * 8 * 36 * 4
-    a.n_heads = 12  # not a multiple of the 8-head block for fp32 K/V
-    assert K.cbis_paged_attention(ctypes.byref(a), None) == 2
+    a.n_heads = 12  # a partial last head block (8 fp32 heads per block) is fine
+    assert K.cbis_paged_attention_workspace_size(ctypes.byref(a)) == 4 * 64 * 12 * 36 * 4
+    assert K.cbis_paged_attention(ctypes.byref(a), None) == 3  # still only the workspace is missing
+    # A split that is not a whole number of pages would count the keys of its
+    # first page twice: refused.
+    a.split_tokens = 100
+    assert K.cbis_paged_attention_workspace_size(ctypes.byref(a)) == 0
+    assert K.cbis_paged_attention(ctypes.byref(a), None) == 1
+    assert b"multiple of page_size" in K.cbis_last_error()
+    a.n_heads = 0
+    a.split_tokens = 64
+    assert K.cbis_paged_attention(ctypes.byref(a), None) == 1
     assert K.cbis_layernorm(4, 10000, 4096, 10000, 4096, 4096, 1e-5, 0, 4096, 10000, None) == 2

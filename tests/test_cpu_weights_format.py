@@ -132,3 +132,30 @@ def test_malformed_file_rejected(cbis, tmp_path, kind, match):
 def test_missing_file(cbis, tmp_path):
     with pytest.raises(RuntimeError, match="cannot open"):
         cbis.ModelWeights.load_packed(str(tmp_path / "none.cbisw"))
+
+
+# The reference's weights.bin (ModelWeights::load, src/model_weights.cpp:41-75)
+
+def test_weights_bin_size_must_match_config(cbis, oracle, tmp_path):
+    """A weights.bin of exactly the config's tensors reaches the device
+    allocation; one byte-count off in either direction (other dims, trailing
+    bytes, truncation) is refused before it."""
+    from helpers import write_weights_bin
+    spec = oracle.ModelSpec(vocab=64, d_model=64, n_heads=2, n_layers=2, mlp=256, max_seq=32)
+    cfg = cbis.ModelConfig.make(vocab=64, d_model=64, n_heads=2, n_layers=2, mlp=256, max_seq=32)
+    p = tmp_path / "weights.bin"
+    write_weights_bin(p, oracle.synthetic_weights(spec, seed=0))
+    good = p.read_bytes()
+    D, F, V, S = 64, 256, 64, 32
+    assert len(good) == 4 * (2 * V * D + S * D + 2 * (9 * D + 4 * D * D + 2 * F * D + F) + 2 * D)
+    with pytest.raises(RuntimeError, match="hipMalloc"):
+        cbis.ModelWeights.load(str(p), cfg)
+    for blob in (good[:-4], good + b"\0\0\0\0", good[:-1]):
+        p.write_bytes(blob)
+        with pytest.raises(RuntimeError, match="the config's tensors are") as ei:
+            cbis.ModelWeights.load(str(p), cfg)
+        assert "hipMalloc" not in str(ei.value)
+    p.write_bytes(good)
+    other = cbis.ModelConfig.make(vocab=64, d_model=64, n_heads=2, n_layers=3, mlp=256, max_seq=32)
+    with pytest.raises(RuntimeError, match="the config's tensors are"):
+        cbis.ModelWeights.load(str(p), other)

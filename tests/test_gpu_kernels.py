@@ -866,5 +866,93 @@ def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows, tile):
     ref = oracle.paged_attention(q.cpu().numpy(), bits_u16(kp), bits_u16(vp), np.repeat(bt, n_rows, 0), pos, H, 32,
                                  16, kv_dtype=1)
     got = out.float().cpu().numpy()
-    assert row_rel_err(got.reshape(n_rows * H, 32), ref.reshape(n_rows * H, 32)) < LOWP_TOL * 2
+    # north_star's bf16 metric: per row, ||d||_inf / ||ref||_inf over the
+    # row's H * head_dim outputs.  Q and P are rounded to bf16 for the MFMAs.
+    err_row = row_rel_err(got, ref)
+    err_head = row_rel_err(got.reshape(n_rows * H, 32), ref.reshape(n_rows * H, 32))
+    print(f"prefill cached={cached} rows={n_rows} tile={tile}: per-row rel {err_row:.3e}, "
+          f"per-(row, head) rel {err_head:.3e}", flush=True)
+    assert err_row < LOWP_TOL
+    assert err_head < LOWP_TOL * 2   # stricter slicing: each head against its own maximum
     assert np.abs(got - ref).mean() < 2e-3
+
+
+@pytest.mark.parametrize("kv_dtype,H", [("f32", 12), ("f32", 4), ("bf16", 24), ("bf16", 8)])
+def test_decode_attention_any_head_count(cbis, oracle, dev, kv_dtype, H):
+    """Head counts that do not fill the last 1 KiB head block (8 fp32 or 16
+    bf16 heads), as the reference's grid(total_rows, n_heads) allows
+    (kernels/attention.cu:113-127): through the reference-signature entry
+    point (fp32) and the split-KV entry point with partials and merge."""
+    import torch
+    S, P = 10, 900
+    kv = np.array([1, 16, 17, 40, 333, 700, 1200, 64, 5, 999], np.int32)
+    npages = (kv + 15) // 16
+    perm = rng(21).permutation(P).astype(np.int32)
+    bt = np.zeros((S, int(npages.max())), np.int32)
+    off = 0
+    for i in range(S):
+        bt[i, : npages[i]] = perm[off: off + npages[i]]
+        off += npages[i]
+    tdt, cdt, kd = (torch.float32, cbis.F32, 0) if kv_dtype == "f32" else (torch.bfloat16, cbis.BF16, 1)
+    kp = torch.empty((P, 16, H, 32), dtype=tdt, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((S, H * 32), dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    for t, sd, dt in ((kp, 51, cdt), (vp, 52, cdt), (q, 53, cbis.F32)):
+        cbis.check(K.cbis_fill_normal_fast(ptr(t), dt, t.numel(), sd, 1.0, stream()))
+    pos = kv - 1
+    BT, POS = to_dev(bt, dev), to_dev(pos, dev)
+    host = (lambda t: t.cpu().numpy()) if kd == 0 else bits_u16
+    ref = oracle.paged_attention(q.cpu().numpy(), host(kp), host(vp), bt, pos, H, 32, 16, kv_dtype=kd)
+    outs = []
+    if kd == 0:
+        o = torch.full((S, H * 32), 7.0, dtype=torch.float32, device=dev)
+        cbis.check(K.cbis_fused_paged_causal_attention(ptr(q), ptr(kp), ptr(vp), ptr(BT), ptr(POS), ptr(o), S, H, 32,
+                                                       16, bt.shape[1], stream()))
+        outs.append(o)
+    for split in (64, 0):
+        o = torch.full((S, H * 32), 7.0, dtype=torch.float32, device=dev)
+        d = _attn_desc(cbis, S, H, q, kp, vp, P, BT, bt.shape[1], POS, o, cdt, max_kv=int(kv.max()), split=split)
+        need = K.cbis_paged_attention_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+        d.workspace, d.workspace_bytes = ptr(ws), need
+        d.keep_alive = d.keep_alive + (ws,)
+        if split == 64:
+            assert need == S * ((int(kv.max()) + 63) // 64) * H * 36 * 4
+        cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream()))
+        sync()
+        outs.append(o)
+    sync()
+    for o in outs:
+        got = o.cpu().numpy()
+        if kd == 0:
+            assert np.abs(got - ref).max() < FP32_TOL
+        else:
+            assert row_rel_err(got, ref) < LOWP_TOL
+        assert (got != 7.0).all()   # every head of every row written, nothing past the last head
+
+
+@pytest.mark.parametrize("n_heads", [8, 12])
+def test_scatter_kv_to_cache_reference_signature(cbis, oracle, dev, n_heads):
+    """cbis_scatter_kv_to_cache (include/attention.hpp:8-12) bit-exact
+    against the oracle's restatement of kernels/attention.cu:7-19: rows go
+    to permuted (page, slot) pairs, every other slot keeps its bytes."""
+    import torch
+    D, P, M = n_heads * 32, 37, 150
+    slots = rng(31).permutation(P * 16)[:M]
+    wpage, woff = (slots // 16).astype(np.int32), (slots % 16).astype(np.int32)
+    kv_rows = oracle.normal(31, 1, 2 * M * D).reshape(2, M, D)
+    k_host = oracle.normal(31, 2, P * 16 * D).reshape(P, 16, n_heads, 32)
+    v_host = oracle.normal(31, 3, P * 16 * D).reshape(P, 16, n_heads, 32)
+    kp, vp = to_dev(k_host, dev), to_dev(v_host, dev)
+    Kr, Vr, WP, WO = to_dev(kv_rows[0], dev), to_dev(kv_rows[1], dev), to_dev(wpage, dev), to_dev(woff, dev)
+    K = cbis.kernels()
+    cbis.check(K.cbis_scatter_kv_to_cache(ptr(Kr), ptr(Vr), ptr(kp), ptr(vp), ptr(WP), ptr(WO), M, D, 16, n_heads, 32,
+                                          stream()))
+    sync()
+    ek, ev = k_host.copy(), v_host.copy()
+    oracle.scatter_kv(kv_rows[0], kv_rows[1], ek, ev, wpage, woff, 16)
+    assert np.array_equal(kp.cpu().numpy().view(np.uint32), ek.view(np.uint32))
+    assert np.array_equal(vp.cpu().numpy().view(np.uint32), ev.view(np.uint32))
+    assert K.cbis_scatter_kv_to_cache(ptr(Kr), ptr(Vr), ptr(kp), ptr(vp), ptr(WP), ptr(WO), M, D + 1, 16, n_heads, 32,
+                                      stream()) == 1

@@ -298,12 +298,222 @@ def test_packed_checkpoint_round_trip(cbis, tmp_path, wdt):
         cbis.ModelWeights.load_packed(str(p2))
 
 
+# --------------------------------------------------------------------------
+# Whole steps at the BASELINE configs' own workloads (1-2 of their 16
+# layers), the counterpart of src/correctness_check.cpp:55-94 (a full step
+# diffed against the model).
+# --------------------------------------------------------------------------
 
-def test_runner_rejects_unsupported_head_blocks(cbis):
-    """bf16 K/V pages are read in 16-head blocks: an 8-head bf16 model is
-    refused when the runner is built, not in the middle of a step."""
-    cfg = cbis.ModelConfig.make(vocab=512, n_layers=1, max_seq=1024, weight_dtype="bf16", kv_dtype="bf16")
-    w = cbis.ModelWeights.synthetic(cfg, seed=1)
-    cache = cbis.PagedKVCache(1, 8, 16, 8, 32, "bf16", pages_per_seq=64)
-    with pytest.raises(cbis.CbisError, match="n_heads a multiple"):
-        cbis.TransformerRunner(w, cache, 16)
+def _shuffle_free_lists(caches, n_pages, seed):
+    """Hands every cache the same shuffled free list through the reference
+    API alone (as bench.py does for configs 4 and 5): n_pages one-page
+    sequences take pages 0..n-1 and are freed in a random order, so later
+    allocations pop physical pages in that order."""
+    perm = np.random.default_rng(seed).permutation(n_pages)
+    for c in caches:
+        dummies = []
+        for _ in range(n_pages):
+            s = c.allocate_sequence()
+            assert c.ensure_capacity(s, 0)
+            dummies.append(s)
+        for i in perm:
+            c.free_sequence(dummies[i])
+
+
+def _big_setup(cbis, oracle, wdt, n_layers, max_pages, max_seq, fill_seed):
+    spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=n_layers, mlp=8192,
+                            max_seq=max_seq, weight_dtype=wdt, kv_dtype="bf16")
+    cfg = cbis.ModelConfig.make(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=n_layers, mlp=8192,
+                                max_seq=max_seq, weight_dtype=wdt, kv_dtype="bf16")
+    w = cbis.ModelWeights.synthetic(cfg, seed=0)
+    cache = cbis.PagedKVCache(n_layers, max_pages, 16, 64, 32, "bf16", pages_per_seq=max_seq // 16)
+    cache.fill_normal(seed=fill_seed, std=1.0)  # synthetic cached K/V for positions before the step
+    om = oracle.OracleModel(oracle.synthetic_weights(spec, seed=0), max_pages=max_pages)
+    for l in range(n_layers):
+        _d2h(om.kpools[l], cache.k_base(l))
+        _d2h(om.vpools[l], cache.v_base(l))
+    ocache = oracle.PagedKVCacheOracle(max_pages, pages_per_seq=max_seq // 16)
+    _shuffle_free_lists([cache, ocache], max_pages, fill_seed)
+    return w, cache, om, ocache
+
+
+def _check_logits(got, ref, what):
+    """north_star's bf16/fp8 bar: per row ||d||_inf / ||ref||_inf <= 2e-2,
+    and the greedy token equal wherever the oracle's top-2 margin exceeds
+    twice the row's measured error."""
+    err = row_rel_err(got, ref)
+    abs_err = np.abs(got - ref).max(axis=1)
+    srt = np.sort(ref, axis=1)
+    margin = srt[:, -1] - srt[:, -2]
+    sure = margin > 2 * abs_err
+    agree = got.argmax(axis=1) == ref.argmax(axis=1)
+    print(f"{what}: rows={len(got)} per-row rel err {err:.3e}, max abs {abs_err.max():.3e}, "
+          f"argmax agrees on {int(agree.sum())}/{len(got)} ({int(sure.sum())} with margin > 2 err)", flush=True)
+    assert err < 2e-2, err
+    assert agree[sure].all()
+    return ref.argmax(axis=1)
+
+
+def test_c4_step_at_config_workload(cbis, oracle):
+    """BASELINE config 4's step exactly as bench.py builds it, on 2 of the 16
+    layers: 192 decode rows with kv U[256, 4096] (the seed-0 draw) over a
+    shuffled page table plus two 512-row prefill chunks (a fresh sequence at
+    positions 0..511 and one with 512 cached tokens at 512..1023), M = 1216.
+    The runner's one-pass decode rows, 64-row snake-ordered prefill tiles and
+    the wave-specialised bf16 GEMMs at M = 1216 run as in the bench."""
+    kv = oracle.uniform_int(0, 5001, 192, 256, 4096)
+    max_pages = int(((kv + 15) // 16).sum()) + 32 + 64 + 64
+    w, cache, om, ocache = _big_setup(cbis, oracle, "bf16", 2, max_pages, 4096, 1)
+    runner = cbis.TransformerRunner(w, cache, 1216)
+    toks = oracle.uniform_int(0, 5002, 1216, 0, 31999)
+    tok, pos, sid, osid = [], [], [], []
+    for i in range(192):
+        s, o = cache.allocate_sequence(), ocache.allocate_sequence()
+        assert cache.ensure_capacity(s, int(kv[i]) - 1) and ocache.ensure_capacity(o, int(kv[i]) - 1)
+        tok.append(int(toks[i])); pos.append(int(kv[i]) - 1); sid.append(s); osid.append(o)
+    for start in (0, 512):
+        s, o = cache.allocate_sequence(), ocache.allocate_sequence()
+        assert cache.ensure_capacity(s, start + 511) and ocache.ensure_capacity(o, start + 511)
+        for p in range(start, start + 512):
+            tok.append(int(toks[len(tok)])); pos.append(p); sid.append(s); osid.append(o)
+    assert len(tok) == 1216
+    for s, o in zip(sid, osid):
+        assert cache.pages(s) == ocache.seq_pages[o]   # bit-exact allocation on the shuffled list
+    got = runner.forward_step(tok, pos, sid)
+    plan = runner.last_plan()
+    assert plan["decode_rows"] == 192 and plan["prefill_tiles"] == 16 and plan["split_tokens"] == 1 << 30
+    ref = oracle.forward_step_with_cache(om, ocache, tok, pos, osid)
+    _check_logits(got, ref, "config 4 step (2 layers)")
+    # The greedy form of the same step: device argmax of the same logits.
+    cache2_tokens = runner.forward_step_greedy(tok, pos, sid)
+    assert cache2_tokens == [int(t) for t in got.argmax(axis=1)]
+
+
+def test_c5_decode_at_config_workload(cbis, oracle):
+    """BASELINE config 5's decode on 1 of the 16 layers: fp8-e4m3 weights
+    with per-channel scales, bf16 K/V, 16 sequences whose caches hold 32704
+    synthetic tokens, greedy steps at positions 32704, 32705, 32706 through
+    the runner's own split choice (8192-token splits: one CU's share of the
+    rows' tokens) and the skinny fp8 GEMMs; teacher-forced on the oracle's
+    tokens."""
+    n_seq, ctx = 16, 32768 - 64
+    max_pages = n_seq * 2048 + 64
+    w, cache, om, ocache = _big_setup(cbis, oracle, "fp8", 1, max_pages, 32768, 5)
+    runner = cbis.TransformerRunner(w, cache, 64)
+    seqs, oseqs = [], []
+    for _ in range(n_seq):
+        s, o = cache.allocate_sequence(), ocache.allocate_sequence()
+        assert cache.ensure_capacity(s, 32767) and ocache.ensure_capacity(o, 32767)
+        assert cache.pages(s) == ocache.seq_pages[o]
+        seqs.append(s); oseqs.append(o)
+    toks = [int(t) for t in oracle.uniform_int(0, 5003, n_seq, 0, 31999)]
+    for step in range(3):
+        pos = [ctx + step] * n_seq
+        got = runner.forward_step(toks, pos, seqs)
+        assert runner.last_plan()["split_tokens"] == 8192
+        ref = oracle.forward_step_with_cache(om, ocache, toks, pos, oseqs)
+        want = _check_logits(got, ref, f"config 5 step {step} (1 layer)")
+        toks = [int(t) for t in want]
+
+
+def test_runner_split_kv_decode_rows_with_prefill(cbis, oracle):
+    """The runner's split sizing for decode rows that cannot fill the GPU in
+    one pass but carry >= 2048 tokens per CU: 24 rows at kv U[7000, 8192]
+    (one CU's share ~2850 tokens) get power-of-two 4096-token splits, two per
+    row, whose merge runs inside the prefill launch of the step's 100-row
+    chunk; 2 of the 16 layers of the config-4 model, shuffled page table."""
+    kv = oracle.uniform_int(3, 4101, 24, 7000, 8192)
+    max_pages = int(((kv + 15) // 16).sum()) + 16 + 64
+    w, cache, om, ocache = _big_setup(cbis, oracle, "bf16", 2, max_pages, 8192, 3)
+    runner = cbis.TransformerRunner(w, cache, 256)
+    ids = oracle.uniform_int(3, 4102, 200, 0, 31999)
+    tok, pos, sid, osid = [], [], [], []
+    for i, k in enumerate(kv):
+        s, o = cache.allocate_sequence(), ocache.allocate_sequence()
+        assert cache.ensure_capacity(s, int(k) - 1) and ocache.ensure_capacity(o, int(k) - 1)
+        tok.append(int(ids[i])); pos.append(int(k) - 1); sid.append(s); osid.append(o)
+    s, o = cache.allocate_sequence(), ocache.allocate_sequence()
+    assert cache.ensure_capacity(s, 139) and ocache.ensure_capacity(o, 139)
+    for p in range(40, 140):
+        tok.append(int(ids[len(tok)])); pos.append(p); sid.append(s); osid.append(o)
+    got = runner.forward_step(tok, pos, sid)
+    plan = runner.last_plan()
+    assert plan["decode_rows"] == 24 and plan["prefill_tiles"] == 2 and plan["split_tokens"] == 4096, plan
+    assert (kv > 4096).sum() >= 20   # most rows take two splits and the merge
+    ref = oracle.forward_step_with_cache(om, ocache, tok, pos, osid)
+    _check_logits(got, ref, "split-KV decode rows + prefill chunk (2 layers)")
+
+
+@pytest.mark.parametrize("wdt,kvdt,H", [("f32", "f32", 12), ("bf16", "bf16", 8), ("bf16", "bf16", 20)])
+def test_runner_any_head_count(cbis, oracle, wdt, kvdt, H):
+    """Head counts that leave the attention kernels' last 1 KiB head block
+    partial (8 fp32 / 16 bf16 heads per block): a step with a prefill chunk
+    and decode rows, then a decode step, against the oracle."""
+    D = 32 * H
+    spec = oracle.ModelSpec(vocab=512, d_model=D, n_heads=H, n_layers=2, mlp=4 * D, max_seq=512, weight_dtype=wdt,
+                            kv_dtype=kvdt)
+    cfg = cbis.ModelConfig.make(vocab=512, d_model=D, n_heads=H, n_layers=2, mlp=4 * D, max_seq=512, weight_dtype=wdt,
+                                kv_dtype=kvdt)
+    w = cbis.ModelWeights.synthetic(cfg, seed=2)
+    cache = cbis.PagedKVCache(2, 64, 16, H, 32, kvdt, pages_per_seq=32)
+    runner = cbis.TransformerRunner(w, cache, 128)
+    om = oracle.OracleModel(oracle.synthetic_weights(spec, seed=2), max_pages=64)
+    ocache = oracle.PagedKVCacheOracle(64, pages_per_seq=32)
+    lens = [50, 3, 20]
+    seqs, oseqs = [], []
+    tok, pos, sid, osid = [], [], [], []
+    ids = oracle.uniform_int(2, 77, 100, 0, 511)
+    for n in lens:
+        s, o = cache.allocate_sequence(), ocache.allocate_sequence()
+        seqs.append(s); oseqs.append(o)
+        for p in range(n):
+            assert cache.ensure_capacity(s, p) and ocache.ensure_capacity(o, p)
+            tok.append(int(ids[len(tok)])); pos.append(p); sid.append(s); osid.append(o)
+    tol = (lambda g, r: float(np.abs(g - r).max()) < 1e-4) if wdt == "f32" else \
+        (lambda g, r: row_rel_err(g, r) < 2e-2)
+    got = runner.forward_step(tok, pos, sid)
+    ref = oracle.forward_step_with_cache(om, ocache, tok, pos, osid)
+    assert tol(got, ref)
+    dpos = list(lens)
+    for s, o, q in zip(seqs, oseqs, dpos):
+        assert cache.ensure_capacity(s, q) and ocache.ensure_capacity(o, q)
+    nxt = [1, 2, 3]
+    got = runner.forward_step(nxt, dpos, seqs)
+    ref = oracle.forward_step_with_cache(om, ocache, nxt, dpos, oseqs)
+    assert tol(got, ref)
+
+
+def test_weights_bin_loader_reproduces_model_py(cbis, oracle, tmp_path):
+    """ModelWeights::load (src/model_weights.cpp:41-75) on a weights.bin
+    written in python/export_weights.py:42-66 order from the seed-0 weights
+    of the reference dims: the G1 batch of src/correctness_check.cpp gives
+    python/model.py's logits (tests/golden/g1_refmodel.npz) within 1e-4, and
+    the same logits bit for bit as the synthetic weights it was written from."""
+    from helpers import write_weights_bin
+    g = np.load(os.path.join(GOLDEN, "g1_refmodel.npz"))
+    path = tmp_path / "weights.bin"
+    write_weights_bin(path, oracle.synthetic_weights(oracle.ModelSpec(), seed=0))
+    cfg, w_syn = _ref_model(cbis)
+    w_bin = cbis.ModelWeights.load(str(path), cfg)
+    assert w_bin.device_bytes() == w_syn.device_bytes()
+    outs = {}
+    for name, w in (("bin", w_bin), ("syn", w_syn)):
+        cache = cbis.PagedKVCache(4, 8 * 6 + 8, 16, 8, 32, "f32", pages_per_seq=2048)
+        runner = cbis.TransformerRunner(w, cache, 128)
+        res = []
+        for i in range(len(g["lens"])):
+            ids = [int(t) for t in g[f"ids{i}"]]
+            s = cache.allocate_sequence()
+            for p in range(len(ids)):
+                assert cache.ensure_capacity(s, p)
+            res.append(runner.forward_step(ids, list(range(len(ids))), [s] * len(ids)))
+            cache.free_sequence(s)
+        outs[name] = res
+        runner.close()
+        cache.close()
+    worst = 0.0
+    for i in range(len(g["lens"])):
+        assert np.array_equal(outs["bin"][i], outs["syn"][i])
+        worst = max(worst, float(np.abs(outs["bin"][i] - g[f"logits{i}"]).max()))
+    print(f"weights.bin G1 max abs vs model.py {worst:.3e}", flush=True)
+    assert worst < 1e-4, worst

@@ -203,6 +203,48 @@ def test_batch_matches_single_calls(cbis, mgr_factory, kv, heads):
     assert np.array_equal(read_page(caches[0], 30), originals[9])
 
 
+def test_batch_destination_aliases_evicted_victim(cbis, mgr_factory):
+    """A restore batch whose later destination page is the current page of a
+    block the batch's own earlier restore evicts: as with one restore() after
+    another, the victim spills its own bytes before that page is written."""
+    caches = [_cache(cbis, 16), _cache(cbis, 16)]
+    mgrs = [mgr_factory(2, 8), mgr_factory(2, 8)]
+    orig = {}
+    for cache, mgr in zip(caches, mgrs):
+        for b, page in ((1, 0), (2, 1), (3, 2), (4, 3)):
+            orig[b] = fill_page(cache, page, 50 + b)
+            mgr.admit_gpu_resident(b, cache, page, b)
+        for b in (3, 4):   # blocks 1, 2 went to DRAM when 3, 4 arrived; now 3, 4 follow
+            mgr.spill(b, "DRAM", 10)
+        mgr.restore(2, cache, 1, 11)                   # GPU: 2 (page 1)
+        fill_page(cache, 7, 99)
+        mgr.admit_gpu_resident(5, cache, 7, 12)         # GPU: 2, 5 -- tier full
+        orig[5] = read_page(cache, 7)
+    # Restoring 3 evicts 2 (stalest, page 1); 4 is then written into page 1.
+    mgrs[0].restore_batch([3, 4], caches[0], [9, 1], 20)
+    mgrs[1].restore(3, caches[1], 9, 20)
+    mgrs[1].restore(4, caches[1], 1, 20)
+    assert mgrs[0].tier_of(2) == "DRAM" and mgrs[0].stats() == mgrs[1].stats()
+    for cache, mgr in zip(caches, mgrs):
+        assert np.array_equal(read_page(cache, 9), orig[3]) and np.array_equal(read_page(cache, 1), orig[4])
+        mgr.restore(2, cache, 12, 30)                   # the victim's spilled bytes are its own
+        assert np.array_equal(read_page(cache, 12), orig[2])
+
+
+def test_batch_refuses_overwriting_a_later_moved_block(cbis, mgr_factory):
+    """One restore() after another would overwrite a GPU-resident block's
+    page before moving it; the batch refuses that order instead."""
+    cache = _cache(cbis, 8)
+    mgr = mgr_factory(4, 4)
+    for b, page in ((1, 0), (2, 1)):
+        fill_page(cache, page, b)
+        mgr.admit_gpu_resident(b, cache, page, 0)
+    with pytest.raises(cbis.CbisError, match="earlier block's destination"):
+        mgr.restore_batch([1, 2], cache, [1, 5], 1)
+    assert mgr.tier_of(1) == "GPU" and mgr.tier_of(2) == "GPU"
+    mgr.restore_batch([2, 1], cache, [5, 1], 1)         # the order that moves 2 first is fine
+
+
 def test_restore_moves_gpu_resident_block(cbis, mgr_factory):
     cache = _cache(cbis, 8)
     mgr = mgr_factory(4, 4)
