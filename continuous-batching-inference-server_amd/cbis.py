@@ -94,6 +94,7 @@ KERNEL_SYMBOLS = {
     "cbis_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "cbis_paged_attention_workspace_size": (_SZ, [ctypes.POINTER(AttnDesc)]),
     "cbis_paged_attention": (_I, [ctypes.POINTER(AttnDesc), _P]),
+    "cbis_paged_attention_static": (_I, [ctypes.POINTER(AttnDesc), _P]),
     "cbis_paged_prefill_attention": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
     "cbis_paged_attention_mixed": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
     "cbis_embed": (_I, [_I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P]),

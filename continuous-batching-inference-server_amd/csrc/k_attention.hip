@@ -27,6 +27,8 @@
 // lane layout is the B-operand layout up to a fixed permutation of the key
 // index, applied to V^T as well) and V^T read from an LDS copy of the 32-key
 // V tile with gfx950's transposing LDS read (ds_read_b64_tr_b16).
+#include <mutex>
+
 #include "common.hpp"
 
 namespace cbis {
@@ -638,16 +640,18 @@ int validate(const cbis_attn_desc* d, const char* who) {
   return CBIS_OK;
 }
 
-// Launches the decode kernel for d's rows (d validated, n_rows > 0); *m gets
+// Launches the decode kernel for d's rows (d validated, n_rows > 0) with the
+// split partials in ws (ws_bytes long; d->workspace is not read); *m gets
 // its arguments and *ns its split count -- the split merge is the caller's.
-int decode_launch(const cbis_attn_desc* d, hipStream_t s, DecodeArgs* m, int* ns_out, const char* who) {
+int decode_launch(const cbis_attn_desc* d, void* ws, size_t ws_bytes, hipStream_t s, DecodeArgs* m, int* ns_out,
+                  const char* who) {
   const int hblocks = head_blocks(d);
   int ns = 1;
   const int split = resolve_split(d, hblocks, &ns);
   if (ns > 1) {
     const size_t need = (size_t)d->n_rows * ns * d->n_heads * kWS * sizeof(float);
-    CBIS_REQUIRE(d->workspace && d->workspace_bytes >= need, CBIS_ERR_WORKSPACE, "%s: workspace %zu bytes, need %zu",
-                 who, d->workspace_bytes, need);
+    CBIS_REQUIRE(ws && ws_bytes >= need, CBIS_ERR_WORKSPACE, "%s: workspace %zu bytes, need %zu", who, ws_bytes,
+                 need);
   }
   DecodeArgs a;
   a.rows = d->rows;
@@ -664,7 +668,7 @@ int decode_launch(const cbis_attn_desc* d, hipStream_t s, DecodeArgs* m, int* ns
   a.out = d->out;
   a.ldo = d->ldo;
   a.out_bf16 = d->out_dtype == CBIS_BF16;
-  a.ws = (float*)d->workspace;
+  a.ws = (float*)ws;
   a.n_heads = d->n_heads;
   a.n_hblocks = hblocks;
   a.n_splits = ns;
@@ -693,6 +697,52 @@ int merge_launch(const DecodeArgs& m, int n_rows, hipStream_t s) {
   const int64_t threads = (int64_t)n_rows * m.n_heads * kHD;
   paged_decode_merge_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, s>>>(m, n_rows);
   return check_launch("cbis_paged_attention(merge)");
+}
+
+// Split-KV decode over d's rows with the partials in ws: the decode launch,
+// then the merge launch when a row takes more than one split.
+int paged_attention_ws(const cbis_attn_desc* d, void* ws, size_t ws_bytes, hipStream_t s, const char* who) {
+  int rc = validate(d, who);
+  if (rc) return rc;
+  CBIS_REQUIRE(d->row_pos, CBIS_ERR_INVALID, "%s: null row_pos", who);
+  if (d->n_rows == 0) return CBIS_OK;
+  DecodeArgs m;
+  int ns = 1;
+  rc = decode_launch(d, ws, ws_bytes, s, &m, &ns, who);
+  if (rc || ns <= 1) return rc;
+  return merge_launch(m, d->n_rows, s);
+}
+
+// Split-KV partials of cbis_paged_attention_static: a file-scope device
+// array, so that entry point allocates nothing.  Each GPU the library runs
+// on holds its own copy (32 MiB) until the process ends.  In host code the
+// array's name is not a device address: its address on the current device
+// is looked up once per device with hipGetSymbolAddress and kept in
+// g_scratch_dev, and only that address reaches the kernels.  The decode
+// kernel writes every partial the merge reads in the same call, so nothing
+// in it needs to start at zero.
+constexpr size_t kStaticScratchBytes = CBIS_ATTN_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+int static_scratch(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  CBIS_REQUIRE(e == hipSuccess, CBIS_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  CBIS_REQUIRE(dev >= 0 && dev < kMaxDevices, CBIS_ERR_UNSUPPORTED, "%s: device %d", who, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    CBIS_REQUIRE(e == hipSuccess && p, CBIS_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                 hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return CBIS_OK;
 }
 
 int check_tiles(const cbis_attn_desc* d, int n_tiles, const int* tiles, const char* who) {
@@ -755,16 +805,21 @@ size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d) {
 }
 
 int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream) {
-  int rc = validate(d, "cbis_paged_attention");
+  return paged_attention_ws(d, d ? d->workspace : nullptr, d ? d->workspace_bytes : 0, (hipStream_t)stream,
+                            "cbis_paged_attention");
+}
+
+int cbis_paged_attention_static(const cbis_attn_desc* d, cbis_stream_t stream) {
+  const char* who = "cbis_paged_attention_static";
+  int rc = validate(d, who);
   if (rc) return rc;
-  CBIS_REQUIRE(d->row_pos, CBIS_ERR_INVALID, "cbis_paged_attention: null row_pos");
-  if (d->n_rows == 0) return CBIS_OK;
-  DecodeArgs m;
-  int ns = 1;
-  hipStream_t s = (hipStream_t)stream;
-  rc = decode_launch(d, s, &m, &ns, "cbis_paged_attention");
-  if (rc || ns <= 1) return rc;
-  return merge_launch(m, d->n_rows, s);
+  void* ws = nullptr;
+  if ((rc = static_scratch(&ws, who))) return rc;
+  const size_t need = cbis_paged_attention_workspace_size(d);
+  CBIS_REQUIRE(need <= kStaticScratchBytes, CBIS_ERR_WORKSPACE,
+               "%s: the call's split partials take %zu bytes, more than the %zu-byte static scratch", who, need,
+               kStaticScratchBytes);
+  return paged_attention_ws(d, ws, kStaticScratchBytes, (hipStream_t)stream, who);
 }
 
 int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int* tiles, cbis_stream_t stream) {
@@ -786,7 +841,7 @@ int cbis_paged_attention_mixed(const cbis_attn_desc* d, int n_tiles, const int* 
   int ns = 1;
   if (d->n_rows > 0) {
     CBIS_REQUIRE(d->row_pos, CBIS_ERR_INVALID, "%s: null row_pos", who);
-    rc = decode_launch(d, s, &m, &ns, who);
+    rc = decode_launch(d, d->workspace, d->workspace_bytes, s, &m, &ns, who);
     if (rc) return rc;
   }
   const int merge_rows = ns > 1 ? d->n_rows : 0;

@@ -186,6 +186,21 @@ size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d);
 /* Split-KV decode attention: any set of rows, each with its own kv_len. */
 int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc):
+ * cbis_paged_attention with the split-KV partials in a library-owned static
+ * device buffer of CBIS_ATTN_STATIC_SCRATCH_BYTES per GPU instead of a caller
+ * workspace (d->workspace / workspace_bytes are ignored); same kernels, same
+ * results.  It calls no hipMalloc / hipFree.  A call whose partials
+ * (cbis_paged_attention_workspace_size) exceed the buffer fails with
+ * CBIS_ERR_WORKSPACE.  Every call on one GPU shares that GPU's buffer: calls
+ * that overlap on one GPU (on different streams, or from several threads)
+ * race and may return wrong results; calls ordered on one stream do not.  The
+ * buffer keeps the last call's contents; nothing in it needs to start at
+ * zero.  The first call on a device looks up the buffer's address there. */
+#define CBIS_ATTN_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
+int cbis_paged_attention_static(const cbis_attn_desc* d, cbis_stream_t stream);
+
 /* Rows per prefill tile, at most. */
 #define CBIS_PREFILL_TILE_ROWS 64
 
