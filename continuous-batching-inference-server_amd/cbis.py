@@ -92,6 +92,8 @@ KERNEL_SYMBOLS = {
     "cbis_kv_pages_gather": (_I, [_P, _P, _I, _I, ctypes.c_int64, _P, _I, _P]),
     "cbis_kv_pages_scatter": (_I, [_P, _P, _I, _I, ctypes.c_int64, _P, _I, _P]),
     "cbis_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
+    "cbis_gemm_argmax_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
+    "cbis_gemm_argmax": (_I, [ctypes.POINTER(GemmDesc), _P, _P, _P, _SZ, _P]),
     "cbis_paged_attention_workspace_size": (_SZ, [ctypes.POINTER(AttnDesc)]),
     "cbis_paged_attention": (_I, [ctypes.POINTER(AttnDesc), _P]),
     "cbis_paged_attention_static": (_I, [ctypes.POINTER(AttnDesc), _P]),
@@ -138,6 +140,7 @@ RUNTIME_SYMBOLS = {
     "cbis_runner_stream": (_P, [_P]),
     "cbis_runner_set_graphs": (None, [_P, _I]),
     "cbis_runner_last_plan": (_I, [_P, _IP, _I]),
+    "cbis_runner_last_margins": (_I, [_P, ctypes.POINTER(ctypes.c_float), _I]),
     "cbis_run_continuous": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _IP, ctypes.POINTER(ctypes.c_double), _I]),
     "cbis_eviction_params_default": (None, [ctypes.POINTER(EvictionParams)]),
     "cbis_tiered_create": (_P, [_I, _I, _I, _I, _I, ctypes.c_char_p, _SZ, _SZ, ctypes.POINTER(EvictionParams)]),
@@ -382,6 +385,14 @@ class TransformerRunner:
         _rt_check(runtime().cbis_runner_forward_step_greedy(self._h, n, _iarr(token_ids), _iarr(positions),
                                                             _iarr(seq_ids), out), "forward_step_greedy")
         return list(out[:n])
+
+    def last_margins(self):
+        """Top-2 margins of the last forward_step_greedy's rows (numpy fp32)."""
+        n = _rt_check(runtime().cbis_runner_last_margins(self._h, None, 0), "last_margins")
+        out = np.empty(max(1, n), dtype=np.float32)
+        _rt_check(runtime().cbis_runner_last_margins(self._h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n),
+                  "last_margins")
+        return out[:n]
 
     def logits_device(self) -> int:
         return runtime().cbis_runner_logits_device(self._h)

@@ -54,7 +54,47 @@ struct GemmArgs {
   int ksplit;     // gridDim.z
   int k_per;      // K elements per split (multiple of BK)
   float* partial; // [ksplit][M][N] when ksplit > 1
+  // Greedy mode (cbis_gemm_argmax): instead of storing Y, each workgroup
+  // writes per row of its tile the tile's top-2 partial {max, second max,
+  // index of the max (bits), 0} to amax[row * amax_ld + column tile].
+  float4* amax;
+  int amax_ld;
 };
+
+// Top-2 of a row: the maximum m1 at the lowest index i1 among equal maxima
+// (the strict-> scan of src/bench_batching.cpp:66-73), and the largest value
+// m2 at any other index (m2 == m1 when the maximum is tied).  NaN never
+// wins.  Start from m1 = m2 = -inf, i1 = INT_MAX.
+__device__ inline void top2_push(float& m1, float& m2, int& i1, float v, int c) {
+  if (v > m1 || (v == m1 && c < i1)) {
+    m2 = m1;
+    m1 = v;
+    i1 = c;
+  } else {
+    m2 = fmaxf(m2, v);
+  }
+}
+// Merges another partial (b1, b2, bi) of disjoint columns; order-free.
+__device__ inline void top2_merge(float& m1, float& m2, int& i1, float b1, float b2, int bi) {
+  if (b1 > m1 || (b1 == m1 && bi < i1)) {
+    m2 = fmaxf(m1, b2);
+    m1 = b1;
+    i1 = bi;
+  } else {
+    m2 = fmaxf(m2, b1);
+  }
+}
+// Merges across the lanes l ^ 1, l ^ 2, ... l ^ (W / 2): every lane of a
+// W-lane group ends with the group's top-2.
+template <int W>
+__device__ inline void top2_lanes(float& m1, float& m2, int& i1) {
+#pragma unroll
+  for (int off = W / 2; off > 0; off >>= 1) {
+    const float b1 = __shfl_xor(m1, off, 64), b2 = __shfl_xor(m2, off, 64);
+    const int bi = __shfl_xor(i1, off, 64);
+    top2_merge(m1, m2, i1, b1, b2, bi);
+  }
+}
 
 // Exact-form GELU 0.5 v (1 + erf(v / sqrt 2)) (kernels/elementwise.cu:64),
 // with erf from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7):
@@ -820,6 +860,41 @@ __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* til
   }
 }
 
+// Greedy-mode epilogue over a parked BM x BN fp32 tile: wave w takes rows
+// w, w + 8, ...; lane l the columns l, l + 64, ...; each value gets the
+// channel scale and bias exactly as Cols4::finish applies them (so it equals
+// the logit the store path would write), then the row's top-2 partial of the
+// tile is written for column tile n0 / BN.
+template <int BM, int BN, int NT = 512>
+__device__ inline void epilogue_top2(const GemmArgs& g, const float* tile, int pitch, int m0, int n0, int tid) {
+  constexpr int CPL = BN / 64;  // columns per lane
+  static_assert(CPL * 64 == BN, "epilogue_top2 tile width");
+  const int wave = tid >> 6, lane = tid & 63;
+  float sc[CPL], bi[CPL];
+  bool ok[CPL];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = n0 + lane + 64 * k;
+    ok[k] = c < g.N;
+    sc[k] = (g.w_scale && ok[k]) ? g.w_scale[c] : 1.f;
+    bi[k] = (g.bias && ok[k]) ? g.bias[c] : 0.f;
+  }
+  for (int r = wave; r < BM && m0 + r < g.M; r += NT / 64) {
+    float m1 = -INFINITY, m2 = -INFINITY;
+    int i1 = 0x7FFFFFFF;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      if (!ok[k]) continue;
+      float v = tile[r * pitch + lane + 64 * k];
+      if (g.w_scale) v *= sc[k];
+      if (g.bias) v += bi[k];
+      top2_push(m1, m2, i1, v, n0 + lane + 64 * k);
+    }
+    top2_lanes<64>(m1, m2, i1);
+    if (lane == 0) g.amax[(int64_t)(m0 + r) * g.amax_ld + n0 / BN] = make_float4(m1, m2, __int_as_float(i1), 0.f);
+  }
+}
+
 template <int BM, int BN, int STAGES, int REGS, int WM>
 __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
   typedef WsTile<BM, BN, STAGES, WM> T;
@@ -963,6 +1038,18 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
 #pragma unroll
           for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fb][i], bf[fb][j], acc[i][j], 0, 0, 0);
+        // Issue the next sub-step's fragment reads between this sub-step's
+        // MFMAs, one read after each MFMA, so they land while the MFMAs run
+        // (left to itself the scheduler sinks them below the MFMAs and the
+        // next sub-step waits on them: qkv 41.3 -> 40.1 us, fc1 50.4 -> 48.5).
+        constexpr int kReads = FM + FN, kMfma = FM * FN, kPairs = kReads < kMfma ? kReads : kMfma;
+#pragma unroll
+        for (int q = 0; q < kPairs; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        }
+        if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+        if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
       }
     }
     __builtin_amdgcn_s_setprio(0);
@@ -984,7 +1071,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
           }
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    epilogue_rows<T::PR, BN>(g, kz, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
+    if (g.amax) epilogue_top2<T::PR, BN>(g, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
+    else epilogue_rows<T::PR, BN>(g, kz, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
     if (h + 1 < T::PH) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 }
@@ -1161,11 +1249,60 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
     f32x4_t v = part[0][i][lane];
 #pragma unroll
     for (int w = 1; w < kSkinnyWaves; ++w) v += part[w][i][lane];
+    if (g.amax) {
+      // Greedy mode: the row's top-2 over this workgroup's 16 columns (lanes
+      // 16 q .. 16 q + 15 hold the same rows), value = sum * scale + bias as
+      // epilogue_store computes it.
+      const bool ok = col < g.N;
+      const float sc = (g.w_scale && ok) ? g.w_scale[col] : 1.f;
+      const float bi = (g.bias && ok) ? g.bias[col] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x = v[e];
+        if (g.w_scale) x *= sc;
+        if (g.bias) x += bi;
+        float m1 = ok ? x : -INFINITY, m2 = -INFINITY;
+        int i1 = ok ? col : 0x7FFFFFFF;
+        top2_lanes<16>(m1, m2, i1);
+        const int row = i * 16 + 4 * q + e;
+        if (c16 == 0 && row < g.M)
+          g.amax[(int64_t)row * g.amax_ld + blockIdx.x] = make_float4(m1, m2, __int_as_float(i1), 0.f);
+      }
+      continue;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = i * 16 + 4 * q + e;
       if (row < g.M && col < g.N) epilogue_store(g, row, col, v[e]);
     }
+  }
+}
+
+// Greedy-mode reduce: one wave per row folds the row's n_parts top-2
+// partials (RAW: the row's fp32 values themselves) in any order -- the merge
+// keeps the lowest index among equal maxima -- and writes the index (0 for a
+// row with no maximum, as the strict-> scan leaves it) and the top-2 margin.
+template <bool RAW>
+__global__ __launch_bounds__(256) void top2_reduce_kernel(const void* src, int n_parts, int64_t ld, int M,
+                                                          int* __restrict__ next, float* __restrict__ margin) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  float m1 = -INFINITY, m2 = -INFINITY;
+  int i1 = 0x7FFFFFFF;
+  if constexpr (RAW) {
+    const float* r = (const float*)src + (int64_t)row * ld;
+    for (int c = lane; c < n_parts; c += 64) top2_push(m1, m2, i1, r[c], c);
+  } else {
+    const float4* r = (const float4*)src + (int64_t)row * ld;
+    for (int c = lane; c < n_parts; c += 64) {
+      const float4 p = r[c];
+      top2_merge(m1, m2, i1, p.x, p.y, __float_as_int(p.z));
+    }
+  }
+  top2_lanes<64>(m1, m2, i1);
+  if (lane == 0) {
+    next[row] = i1 == 0x7FFFFFFF ? 0 : i1;
+    if (margin) margin[row] = m1 - m2;
   }
 }
 
@@ -1301,10 +1438,34 @@ int dispatch(const GemmArgs& g, hipStream_t s) {
   }
 }
 
+// Column-tile width of the greedy-mode partials for d's GEMM path: the
+// kernels that reduce in their epilogue are the skinny one (16 columns per
+// workgroup) and the wave-specialised bf16 ones (their BN); 0 for the others
+// (fp32 or fp8 weights at M > 64, small bf16 grids), whose logits
+// cbis_gemm_argmax stores and reduces instead.  Follows gemm_run's choice.
+int argmax_tile_cols(const cbis_gemm_desc* d) {
+  const int we = d->w_dtype == CBIS_F32 ? 4 : (d->w_dtype == CBIS_BF16 ? 2 : 1);
+  const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * we) % 16 == 0;
+  if (d->M <= kSkinnyMaxM && w_al && d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0) return 16;
+  if (d->x_dtype != CBIS_BF16 || d->w_dtype != CBIS_BF16 || !dma_eligible(d)) return 0;
+  switch (choose_bf16(d->M, d->N, d->K)) {
+    case Bf16Path::kWs256:
+    case Bf16Path::kWs160: return 256;
+    case Bf16Path::kWs128:
+    case Bf16Path::kWs96:
+    case Bf16Path::kWs160Split:  // unsplit in greedy mode: 96 x 128 tiles
+    case Bf16Path::kWs128R: return 128;
+    case Bf16Path::kSmall: break;
+  }
+  return 0;
+}
+
 // Validates the descriptor and launches the product kernel (no split-K
 // reduce); g receives the arguments it ran with (g.ksplit > 1: the raw sums
-// are in the workspace partials and still need their reduce).
-int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g) {
+// are in the workspace partials and still need their reduce).  With amax the
+// kernel runs in greedy mode (no Y; never split): the caller checked that
+// argmax_tile_cols(d) > 0 and sized amax [M][cdiv(N, that)].
+int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax = nullptr) {
   g.ksplit = 1;
   CBIS_REQUIRE(d, CBIS_ERR_INVALID, "cbis_gemm: null descriptor");
   CBIS_REQUIRE(d->M >= 0 && d->N > 0 && d->K > 0, CBIS_ERR_INVALID, "cbis_gemm: bad M/N/K %d/%d/%d", d->M, d->N, d->K);
@@ -1332,7 +1493,8 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g) {
                  CBIS_ERR_INVALID, "cbis_gemm: K/V scatter needs kv_col0 + 2*kv_width == N and slot arrays");
     CBIS_REQUIRE(d->kv_dtype == CBIS_F32 || d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "cbis_gemm: kv dtype");
   }
-  CBIS_REQUIRE(!(kv && d->kv_col0 == 0) ? (d->Y != nullptr) : true, CBIS_ERR_INVALID, "cbis_gemm: null Y");
+  // Y may be absent only in greedy mode or when every column goes to the K/V pages.
+  CBIS_REQUIRE(amax || (kv && d->kv_col0 == 0) || d->Y, CBIS_ERR_INVALID, "cbis_gemm: null Y");
 
   g.M = d->M; g.N = d->N; g.K = d->K;
   g.X = d->X; g.ldx = d->ldx;
@@ -1350,6 +1512,8 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g) {
   g.ksplit = 1;
   g.k_per = d->K;
   g.partial = nullptr;
+  g.amax = amax;
+  g.amax_ld = amax ? (int)cdiv(d->N, argmax_tile_cols(d)) : 0;
 
   // Decode-sized M: weight streaming (K a multiple of 32 for bf16 and fp32,
   // of 64 for fp8; W rows 16-byte aligned).
@@ -1366,7 +1530,7 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g) {
       const Bf16Path path = choose_bf16(d->M, d->N, d->K);
       const SplitPlan p = plan_dma_split(d->M, d->N, d->K);
       const size_t need = (size_t)p.ksplit * d->M * d->N * sizeof(float);
-      const bool split = p.ksplit > 1 && d->workspace && d->workspace_bytes >= need;
+      const bool split = !amax && p.ksplit > 1 && d->workspace && d->workspace_bytes >= need;
       if (split) {
         g.ksplit = p.ksplit;
         g.k_per = p.k_per;
@@ -1459,6 +1623,54 @@ int cbis_gemm_layernorm(const cbis_gemm_desc* d, const float* ln_gamma, const fl
 #undef CBIS_SKLN_KS
 #undef CBIS_SKLN
   return check_launch("cbis_gemm_layernorm(split-k reduce + layernorm)");
+}
+
+size_t cbis_gemm_argmax_workspace_size(const cbis_gemm_desc* d) {
+  if (!d || d->M <= 0 || d->N <= 0 || d->K <= 0) return 0;
+  const int cols = argmax_tile_cols(d);
+  if (cols > 0) return (size_t)d->M * cdiv(d->N, cols) * sizeof(float4);
+  // The logits (unless d->Y takes them) and the split-K partials.
+  const bool y_given = d->Y && d->y_dtype == CBIS_F32 && d->ldy >= d->N;
+  return (y_given ? 0 : (size_t)d->M * d->N * sizeof(float)) + cbis_gemm_workspace_size(d);
+}
+
+int cbis_gemm_argmax(const cbis_gemm_desc* d, int* next_token, float* margin, void* workspace,
+                     size_t workspace_bytes, cbis_stream_t stream) {
+  const char* who = "cbis_gemm_argmax";
+  CBIS_REQUIRE(d, CBIS_ERR_INVALID, "%s: null descriptor", who);
+  CBIS_REQUIRE(d->epilogue == CBIS_EPI_NONE && !d->residual && !d->k_pool, CBIS_ERR_INVALID,
+               "%s: the greedy epilogue takes the scale and bias only (no GELU, residual or K/V scatter)", who);
+  CBIS_REQUIRE(next_token, CBIS_ERR_INVALID, "%s: null next_token", who);
+  if (d->M == 0) return CBIS_OK;
+  const size_t need = cbis_gemm_argmax_workspace_size(d);
+  CBIS_REQUIRE(workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15u) == 0, CBIS_ERR_WORKSPACE,
+               "%s: workspace %zu bytes (16-byte aligned), need %zu", who, workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned blocks = (unsigned)cdiv(d->M, 4);
+  const int cols = argmax_tile_cols(d);
+  if (cols > 0) {
+    GemmArgs g;
+    const int rc = gemm_run(d, s, g, (float4*)workspace);
+    if (rc) return rc;
+    top2_reduce_kernel<false><<<blocks, 256, 0, s>>>(workspace, g.amax_ld, g.amax_ld, d->M, next_token, margin);
+    return check_launch(who);
+  }
+  // Paths without a greedy epilogue: the logits into d->Y (when it is an fp32
+  // [M, N] buffer) or the workspace, then the same reduce over them.
+  cbis_gemm_desc e = *d;
+  const bool y_given = d->Y && d->y_dtype == CBIS_F32 && d->ldy >= d->N;
+  const size_t lg = y_given ? 0 : (size_t)d->M * d->N * sizeof(float);
+  if (!y_given) {
+    e.y_dtype = CBIS_F32;
+    e.Y = workspace;
+    e.ldy = d->N;
+  }
+  e.workspace = (char*)workspace + lg;
+  e.workspace_bytes = workspace_bytes - lg;
+  const int rc = cbis_gemm(&e, stream);
+  if (rc) return rc;
+  top2_reduce_kernel<true><<<blocks, 256, 0, s>>>(e.Y, d->N, e.ldy, d->M, next_token, margin);
+  return check_launch(who);
 }
 
 size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {

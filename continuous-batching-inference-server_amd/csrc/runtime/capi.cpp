@@ -240,6 +240,14 @@ void* cbis_runner_stream(cbis_runner* r) { return (void*)r->impl->stream(); }
 
 void cbis_runner_set_graphs(cbis_runner* r, int enable) { r->impl->set_graphs(enable != 0); }
 
+int cbis_runner_last_margins(const cbis_runner* r, float* out, int capacity) {
+  return guard([&] {
+    const std::vector<float>& m = r->impl->last_margins();
+    for (int i = 0; i < capacity && i < (int)m.size(); ++i) out[i] = m[i];
+    return (int)m.size();
+  });
+}
+
 int cbis_runner_last_plan(const cbis_runner* r, int* out, int capacity) {
   return guard([&] {
     const std::vector<int> p = r->impl->last_plan();

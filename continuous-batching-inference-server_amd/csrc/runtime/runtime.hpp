@@ -160,9 +160,14 @@ class TransformerRunner {
   // Returns row-major [rows, vocab] logits (the reference's contract).
   std::vector<float> forward_step(const std::vector<int>& token_ids, const std::vector<int>& positions,
                                   const std::vector<int>& seq_ids);
-  // Same step; returns the greedy next token of every row (device argmax).
+  // Same step; returns the greedy next token of every row.  lm_head runs
+  // fused with the row argmax (cbis_gemm_argmax): the logits are not stored
+  // where its kernel reduces them in the epilogue.  last_margins() then holds
+  // each row's top-2 margin (max logit minus the runner-up).
   std::vector<int> forward_step_greedy(const std::vector<int>& token_ids, const std::vector<int>& positions,
                                        const std::vector<int>& seq_ids);
+  const std::vector<float>& last_margins() const { return margins_; }
+  // Device logits of the last forward_step (not of a greedy step).
   const float* logits_device() const { return d_logits_; }
   hipStream_t stream() const { return stream_; }
   void set_graphs(bool on) { use_graphs_ = on; }
@@ -173,7 +178,7 @@ class TransformerRunner {
 
  private:
   void prepare(const int* tok, const int* pos, const int* seq, int M);
-  void enqueue_forward();
+  void enqueue_forward(bool greedy);
   void run_step(bool greedy);
 
   const ModelWeights& w_;
@@ -196,6 +201,10 @@ class TransformerRunner {
   void* d_h_ = nullptr;
   float* d_logits_ = nullptr;
   int* d_next_ = nullptr;
+  float* d_margin_ = nullptr;
+  void* d_amax_ws_ = nullptr;  // cbis_gemm_argmax partials
+  size_t amax_ws_bytes_ = 0;
+  std::vector<float> margins_;
   void* d_ws_ = nullptr;
   size_t ws_bytes_ = 0;
   void* d_gemm_ws_ = nullptr;

@@ -13,7 +13,8 @@
 //    one sequence -> out-projection GEMM with bias + residual epilogue ->
 //    LayerNorm -> fc1 GEMM with bias + GELU -> fc2 GEMM with bias + residual;
 //  * steps whose shape repeats replay a captured HIP graph;
-//  * forward_step_greedy takes the argmax on the device.
+//  * forward_step_greedy runs lm_head fused with the row argmax and top-2
+//    margin on the device (no logits stored where the GEMM reduces them).
 #include <algorithm>
 #include <cstring>
 #include <unordered_map>
@@ -49,6 +50,7 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   hip_check(hipMalloc(&d_h_, R * F * ae), "hipMalloc h");
   hip_check(hipMalloc((void**)&d_logits_, R * V * 4), "hipMalloc logits");
   hip_check(hipMalloc((void**)&d_next_, R * 4), "hipMalloc next");
+  hip_check(hipMalloc((void**)&d_margin_, R * 4), "hipMalloc margin");
   // Split-KV partials: the automatic split keeps rows * splits <= 2048 + rows.
   ws_bytes_ = (2048 + R) * (size_t)cfg_.n_heads * (cfg_.head_dim + 4) * 4;
   hip_check(hipMalloc(&d_ws_, ws_bytes_), "hipMalloc attention workspace");
@@ -65,13 +67,23 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
       gemm_ws_bytes_ = std::max(gemm_ws_bytes_, cbis_gemm_workspace_size(&q));
     }
   if (gemm_ws_bytes_) hip_check(hipMalloc(&d_gemm_ws_, gemm_ws_bytes_), "hipMalloc gemm workspace");
+  // Greedy lm_head partials (the logits buffer serves paths that store them).
+  q.N = (int)V; q.K = (int)D; q.ldw = (int)D;
+  q.Y = d_logits_; q.y_dtype = CBIS_F32; q.ldy = (int)V;
+  for (int m = 1; m <= max_total_rows; ++m) {
+    q.M = m;
+    amax_ws_bytes_ = std::max(amax_ws_bytes_, cbis_gemm_argmax_workspace_size(&q));
+  }
+  if (amax_ws_bytes_) hip_check(hipMalloc(&d_amax_ws_, amax_ws_bytes_), "hipMalloc argmax workspace");
 }
 
 TransformerRunner::~TransformerRunner() {
   for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
   if (stream_) (void)hipStreamDestroy(stream_);
   (void)hipFree(d_x_); (void)hipFree(d_xn_); (void)hipFree(d_q_); (void)hipFree(d_attn_);
-  (void)hipFree(d_h_); (void)hipFree(d_logits_); (void)hipFree(d_next_); (void)hipFree(d_ws_);
+  (void)hipFree(d_h_); (void)hipFree(d_logits_); (void)hipFree(d_next_); (void)hipFree(d_margin_);
+  (void)hipFree(d_ws_);
+  if (d_amax_ws_) (void)hipFree(d_amax_ws_);
   if (d_gemm_ws_) (void)hipFree(d_gemm_ws_);
   (void)hipFree(d_meta_);
   if (h_meta_) (void)hipHostFree(h_meta_);
@@ -226,7 +238,7 @@ std::vector<int> TransformerRunner::signature() const {
   return {M_, n_decode_, n_tiles_, n_seqs_, bt_width_, max_kv_, split_tokens_};
 }
 
-void TransformerRunner::enqueue_forward() {
+void TransformerRunner::enqueue_forward(bool greedy) {
   const int M = M_, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
   const int act = cfg_.act_dtype(), wd = cfg_.weight_dtype;
   hipStream_t s = stream_;
@@ -319,14 +331,14 @@ void TransformerRunner::enqueue_forward() {
   g.x_dtype = act; g.X = d_xn_; g.ldx = D;
   g.w_dtype = wd; g.W = w_.lm_head; g.ldw = D; g.w_scale = w_.lm_scale;
   g.y_dtype = CBIS_F32; g.Y = d_logits_; g.ldy = V;
-  cbis_check(cbis_gemm(&g, s), "lm_head gemm");
+  if (greedy)
+    cbis_check(cbis_gemm_argmax(&g, d_next_, d_margin_, d_amax_ws_, amax_ws_bytes_, s), "lm_head gemm + argmax");
+  else
+    cbis_check(cbis_gemm(&g, s), "lm_head gemm");
 }
 
 void TransformerRunner::run_step(bool greedy) {
-  auto body = [&]() {
-    enqueue_forward();
-    if (greedy) cbis_check(cbis_argmax_rows(M_, cfg_.vocab, d_logits_, cfg_.vocab, d_next_, stream_), "argmax");
-  };
+  auto body = [&]() { enqueue_forward(greedy); };
   if (!use_graphs_) {
     body();
     return;
@@ -382,7 +394,10 @@ std::vector<int> TransformerRunner::forward_step_greedy(const std::vector<int>& 
   prepare(token_ids.data(), positions.data(), seq_ids.data(), M);
   run_step(true);
   std::vector<int> next(M);
+  margins_.resize(M);
   hip_check(hipMemcpyAsync(next.data(), d_next_, (size_t)M * 4, hipMemcpyDeviceToHost, stream_), "D2H tokens");
+  hip_check(hipMemcpyAsync(margins_.data(), d_margin_, (size_t)M * 4, hipMemcpyDeviceToHost, stream_),
+            "D2H margins");
   hip_check(hipStreamSynchronize(stream_), "forward_step_greedy sync");
   return next;
 }

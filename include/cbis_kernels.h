@@ -150,6 +150,22 @@ int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream);
 int cbis_gemm_layernorm(const cbis_gemm_desc* d, const float* ln_gamma, const float* ln_beta, float eps,
                         int ln_dtype, void* ln_out, int64_t ld_ln, cbis_stream_t stream);
 
+/* lm_head fused with the greedy rule (no counterpart kernel in the reference,
+ * which copies the [M, vocab] logits to the host and scans each row,
+ * src/transformer.cpp:93-97 with src/bench_batching.cpp:66-73):
+ * next_token[r] = the first index of the maximum of row r of
+ * Y = X . W^T * w_scale + bias (strict >, as argmax_row), and, when margin is
+ * not NULL, margin[r] = that maximum minus the largest value at any other
+ * index (0 for a tied maximum).  The kernels that reduce in their epilogue
+ * (M <= 64, and bf16 weights on the wave-specialised tilings) never store Y;
+ * the others store the logits in d->Y (when it is an fp32 [M, N] buffer) or
+ * the workspace and reduce them.  The epilogue must be scale and bias only
+ * (no GELU, residual or K/V scatter).  workspace: 16-byte aligned, at least
+ * cbis_gemm_argmax_workspace_size(d) bytes. */
+size_t cbis_gemm_argmax_workspace_size(const cbis_gemm_desc* d);
+int cbis_gemm_argmax(const cbis_gemm_desc* d, int* next_token, float* margin, void* workspace,
+                     size_t workspace_bytes, cbis_stream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* Paged attention.                                                          */
 /* ----------------------------------------------------------------------- */

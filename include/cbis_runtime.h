@@ -91,11 +91,15 @@ void cbis_runner_destroy(cbis_runner* r);
  * ran ensure_capacity for every row.  logits_out: host [n, vocab] fp32. */
 int cbis_runner_forward_step(cbis_runner* r, int n, const int* token_ids, const int* positions,
                              const int* seq_ids, float* logits_out);
-/* Same step with the greedy argmax of every row taken on the device;
- * next_tokens: host [n]. */
+/* Same step with the greedy argmax of every row taken on the device, fused
+ * with lm_head (cbis_gemm_argmax: the logits are not stored on the paths
+ * that reduce in the GEMM epilogue); next_tokens: host [n]. */
 int cbis_runner_forward_step_greedy(cbis_runner* r, int n, const int* token_ids, const int* positions,
                                     const int* seq_ids, int* next_tokens);
-/* Device pointer of the last step's [n, vocab] fp32 logits. */
+/* Top-2 margins (max logit minus the runner-up) of the last greedy step's
+ * rows (no reference counterpart): writes min(capacity, n); returns n. */
+int cbis_runner_last_margins(const cbis_runner* r, float* out, int capacity);
+/* Device pointer of the last forward_step's [n, vocab] fp32 logits. */
 const float* cbis_runner_logits_device(cbis_runner* r);
 /* hipStream_t the runner launches on. */
 void* cbis_runner_stream(cbis_runner* r);

@@ -956,3 +956,84 @@ def test_scatter_kv_to_cache_reference_signature(cbis, oracle, dev, n_heads):
     assert np.array_equal(vp.cpu().numpy().view(np.uint32), ev.view(np.uint32))
     assert K.cbis_scatter_kv_to_cache(ptr(Kr), ptr(Vr), ptr(kp), ptr(vp), ptr(WP), ptr(WO), M, D + 1, 16, n_heads, 32,
                                       stream()) == 1
+
+
+# --------------------------------------------------------------------------
+# lm_head fused with the greedy argmax and top-2 margin (cbis_gemm_argmax)
+# --------------------------------------------------------------------------
+
+def _top2_np(logits):
+    """First index of each row's maximum and max minus the largest value at
+    any other index, in fp32 (the margin definition of cbis_gemm_argmax)."""
+    lg = np.asarray(logits, np.float32)
+    idx = lg.argmax(axis=1)
+    rest = lg.copy()
+    rest[np.arange(len(lg)), idx] = -np.inf
+    m1 = lg[np.arange(len(lg)), idx]
+    return idx, (m1 - rest.max(axis=1)).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,N,K,wdt", [
+    (7, 32000, 2048, "bf16"),     # skinny kernel, 2000 partials per row
+    (16, 32000, 2048, "fp8"),     # skinny, fp8 codes with channel scales (config 5's lm_head)
+    (8, 512, 256, "f32"),         # skinny fp32 (config 1's decode steps)
+    (1216, 32000, 2048, "bf16"),  # wave-specialised 160 x 256 (config 4's lm_head)
+    (300, 32000, 512, "bf16"),    # wave-specialised, ragged last row tile
+    (100, 1000, 256, "bf16"),     # small grid: logits stored in Y, then reduced
+    (100, 512, 256, "f32"),       # fp32 at M > 64 (config 1's prefill): stored, then reduced
+    (200, 1000, 512, "fp8"),      # fp8 at M > 64: stored, then reduced
+])
+def test_gemm_argmax_matches_logits(cbis, oracle, dev, M, N, K, wdt):
+    """Tokens and margins of the fused greedy lm_head equal, bit for bit,
+    orc_argmax_rows and the top-2 margin of the logits cbis_gemm writes for
+    the same descriptor; columns 37 and N - 5 are made equal and the largest
+    in rows 0..3 (a tie across column tiles: the lower index wins, margin 0)."""
+    import torch
+    K_ = cbis.kernels()
+    w = oracle.normal(71, 2, N * K, 0.02).reshape(N, K)
+    x = oracle.normal(71, 1, M * K).reshape(M, K)
+    w[N - 5] = w[37]
+    x[:4] = np.abs(x[:4])
+    w[37] = np.abs(w[37]) + 0.05
+    w[N - 5] = w[37]
+    b = oracle.normal(71, 3, N, 0.02)
+    b[N - 5] = b[37]
+    if wdt == "f32":
+        X, W = to_dev(x, dev), to_dev(w, dev)
+        xdt, wd, S = cbis.F32, cbis.F32, None
+    elif wdt == "bf16":
+        (X, _), (W, _) = bf16_dev(x, dev), bf16_dev(w, dev)
+        xdt, wd, S = cbis.BF16, cbis.BF16, None
+    else:
+        codes, sc = oracle.quantize_e4m3_rows(w)
+        sc[N - 5] = sc[37]
+        codes[N - 5] = codes[37]
+        (X, _), W, S = bf16_dev(x, dev), to_dev(codes, dev), to_dev(sc, dev)
+        xdt, wd = cbis.BF16, cbis.FP8E4M3
+    B = to_dev(b, dev)
+    Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    d = cbis.GemmDesc()
+    d.M, d.N, d.K = M, N, K
+    d.x_dtype, d.X, d.ldx = xdt, ptr(X), K
+    d.w_dtype, d.W, d.ldw = wd, ptr(W), K
+    d.w_scale, d.bias = ptr(S), ptr(B)
+    d.y_dtype, d.Y, d.ldy = cbis.F32, ptr(Y), N
+    cbis.check(K_.cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
+    sync()
+    logits = Y.cpu().numpy()
+    # greedy call: Y poisoned first, so a path that reduces in its epilogue
+    # must not depend on it (and one that stores the logits rewrites it)
+    Y.fill_(float("nan"))
+    need = K_.cbis_gemm_argmax_workspace_size(ctypes.byref(d))
+    ws = torch.empty(max(4, need // 4), dtype=torch.float32, device=dev)
+    nxt = torch.full((M,), -1, dtype=torch.int32, device=dev)
+    mar = torch.full((M,), -1.0, dtype=torch.float32, device=dev)
+    cbis.check(K_.cbis_gemm_argmax(ctypes.byref(d), ptr(nxt), ptr(mar), ptr(ws), need, stream()), "cbis_gemm_argmax")
+    sync()
+    idx, margin = _top2_np(logits)
+    assert np.array_equal(nxt.cpu().numpy(), oracle.argmax_rows(logits))
+    assert np.array_equal(nxt.cpu().numpy(), idx)
+    assert np.array_equal(mar.cpu().numpy().view(np.uint32), margin.view(np.uint32))
+    assert (idx[:4] == 37).all() and (margin[:4] == 0).all()
+    if need >= 16:
+        assert K_.cbis_gemm_argmax(ctypes.byref(d), ptr(nxt), ptr(mar), ptr(ws), need - 16, stream()) == 3

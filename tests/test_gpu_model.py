@@ -384,9 +384,13 @@ def test_c4_step_at_config_workload(cbis, oracle):
     assert plan["decode_rows"] == 192 and plan["prefill_tiles"] == 16 and plan["split_tokens"] == 1 << 30
     ref = oracle.forward_step_with_cache(om, ocache, tok, pos, osid)
     _check_logits(got, ref, "config 4 step (2 layers)")
-    # The greedy form of the same step: device argmax of the same logits.
-    cache2_tokens = runner.forward_step_greedy(tok, pos, sid)
-    assert cache2_tokens == [int(t) for t in got.argmax(axis=1)]
+    # The greedy form of the same step (lm_head fused with the row argmax, no
+    # logits stored): the argmax and top-2 margin of the same logits, bit for bit.
+    greedy = runner.forward_step_greedy(tok, pos, sid)
+    assert greedy == [int(t) for t in oracle.argmax_rows(got)]
+    m = runner.last_margins()
+    srt = np.sort(got, axis=1)
+    assert np.array_equal(m, (srt[:, -1] - srt[:, -2]).astype(np.float32))
 
 
 def test_c5_decode_at_config_workload(cbis, oracle):
@@ -413,6 +417,11 @@ def test_c5_decode_at_config_workload(cbis, oracle):
         assert runner.last_plan()["split_tokens"] == 8192
         ref = oracle.forward_step_with_cache(om, ocache, toks, pos, oseqs)
         want = _check_logits(got, ref, f"config 5 step {step} (1 layer)")
+        # the greedy step as bench.py runs it (fused fp8 lm_head + argmax):
+        # the argmax and top-2 margin of the same logits, bit for bit
+        assert runner.forward_step_greedy(toks, pos, seqs) == [int(t) for t in oracle.argmax_rows(got)]
+        srt = np.sort(got, axis=1)
+        assert np.array_equal(runner.last_margins(), (srt[:, -1] - srt[:, -2]).astype(np.float32))
         toks = [int(t) for t in want]
 
 
