@@ -185,38 +185,81 @@ def decode_attention_timing(cbis, st, iters):
 
 
 def gemm_timing(cbis, st, iters):
-    """Times the step's bf16 GEMM shapes at M = 1216 (layer 0 weights)."""
+    """Times the step's five bf16 GEMMs at M = 1216 on layer 0's weights with
+    the epilogues the step runs them with: qkv with bias, fp32 q and the K/V
+    page scatter (into layer 0's pools at the step's write slots); the
+    out-projection with bias and the fp32 residual; fc1 with bias, GELU and a
+    bf16 output; fc2 with bias and residual, split-K, its reduce fused with the
+    next LayerNorm (cbis_gemm_layernorm); lm_head fused with the greedy argmax
+    (cbis_gemm_argmax).  The split-K workspace is the one cbis_gemm asks for."""
     import torch
-    w = st["w"]
+    w, cache = st["w"], st["cache"]
     dev = torch.device("cuda:0")
-    M = 1216
-    shapes = [("qkv", 6144, 2048, "l0.wqkv"), ("out", 2048, 2048, "l0.wo"), ("fc1", 8192, 2048, "l0.w1"),
-              ("fc2", 2048, 8192, "l0.w2"), ("lm_head", 32000, 2048, "lm_head")]
-    X = torch.empty((M, 8192), dtype=torch.bfloat16, device=dev)
-    cbis.check(cbis.kernels().cbis_fill_normal_fast(X.data_ptr(), cbis.BF16, X.numel(), 9, 1.0, None))
-    Y = torch.empty((M, 32000), dtype=torch.float32, device=dev)
+    M, D, F, V = 1216, 2048, 8192, 32000
+    K_ = cbis.kernels()
+    X = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+    cbis.check(K_.cbis_fill_normal_fast(X.data_ptr(), cbis.BF16, X.numel(), 9, 1.0, None))
+    Q = torch.empty((M, D), dtype=torch.float32, device=dev)
+    R = torch.empty((M, D), dtype=torch.float32, device=dev)
+    cbis.check(K_.cbis_fill_normal_fast(R.data_ptr(), cbis.F32, R.numel(), 10, 1.0, None))
+    H = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+    LN = torch.empty((M, D), dtype=torch.bfloat16, device=dev)
+    slots = np.array([cache.resolve_slot(s, p) for s, p in zip(st["sid"], st["pos"])], np.int32)
+    WP = torch.from_numpy(np.ascontiguousarray(slots[:, 0])).to(dev)
+    WO = torch.from_numpy(np.ascontiguousarray(slots[:, 1])).to(dev)
+    nxt = torch.empty(M, dtype=torch.int32, device=dev)
+    mar = torch.empty(M, dtype=torch.float32, device=dev)
     ev = Events(st["runner"].stream())
     stream = st["runner"].stream()
-    res = {}
-    tot_flops = tot_ms = 0.0
-    for name, N, K, wname in shapes:
+    keep = []
+
+    def desc(N, K, wname, bias, Y, y_dtype, residual=None, gelu=False):
         d = cbis.GemmDesc()
         d.M, d.N, d.K = M, N, K
         d.x_dtype, d.X, d.ldx = cbis.BF16, X.data_ptr(), K
         d.w_dtype, d.W, d.ldw = cbis.BF16, w.tensor(wname), K
-        d.y_dtype, d.Y, d.ldy = cbis.F32, Y.data_ptr(), N
-        need = cbis.kernels().cbis_gemm_workspace_size(ctypes.byref(d))
+        d.bias = w.tensor(bias) if bias else None
+        d.epilogue = cbis.EPI_GELU if gelu else cbis.EPI_NONE
+        d.residual, d.ldr = (residual.data_ptr() if residual is not None else None), N
+        d.y_dtype, d.Y, d.ldy = y_dtype, (Y.data_ptr() if Y is not None else None), N
+        need = K_.cbis_gemm_workspace_size(ctypes.byref(d))
         ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+        keep.append(ws)
         d.workspace, d.workspace_bytes = ws.data_ptr(), need
-        fn = lambda d=d: cbis.check(cbis.kernels().cbis_gemm(ctypes.byref(d), stream))
+        return d
+
+    dq = desc(3 * D, D, "l0.wqkv", "l0.bqkv", Q, cbis.F32)
+    dq.ldy = D
+    dq.kv_col0, dq.kv_width, dq.kv_dtype, dq.page_size = D, D, cbis.BF16, 16
+    dq.k_pool, dq.v_pool, dq.write_page, dq.write_offset = cache.k_base(0), cache.v_base(0), WP.data_ptr(), WO.data_ptr()
+    do = desc(D, D, "l0.wo", "l0.bo", R, cbis.F32, residual=R)
+    d1 = desc(F, D, "l0.w1", "l0.b1", H, cbis.BF16, gelu=True)
+    d2 = desc(D, F, "l0.w2", "l0.b2", R, cbis.F32, residual=R)
+    dl = desc(V, D, "lm_head", None, None, cbis.F32)
+    need = K_.cbis_gemm_argmax_workspace_size(ctypes.byref(dl))
+    aws = torch.empty(max(4, need // 4), dtype=torch.float32, device=dev)
+    ln_w, ln_b = w.tensor("l1.ln1_w"), w.tensor("l1.ln1_b")
+    calls = [
+        ("qkv", dq, lambda: cbis.check(K_.cbis_gemm(ctypes.byref(dq), stream))),
+        ("out", do, lambda: cbis.check(K_.cbis_gemm(ctypes.byref(do), stream))),
+        ("fc1", d1, lambda: cbis.check(K_.cbis_gemm(ctypes.byref(d1), stream))),
+        ("fc2+ln", d2, lambda: cbis.check(K_.cbis_gemm_layernorm(ctypes.byref(d2), ln_w, ln_b, 1e-5, cbis.BF16,
+                                                                  LN.data_ptr(), D, stream))),
+        ("lm_head+argmax", dl, lambda: cbis.check(K_.cbis_gemm_argmax(ctypes.byref(dl), nxt.data_ptr(),
+                                                                      mar.data_ptr(), aws.data_ptr(), need,
+                                                                      stream))),
+    ]
+    res = {}
+    tot_flops = tot_ms = 0.0
+    for name, d, fn in calls:
         ev.time(fn, 2)
         ms = ev.time(fn, iters)
-        fl = 2.0 * M * N * K
+        fl = 2.0 * M * d.N * d.K
         # per layer the four projections run once; lm_head once per step
-        mult = 1 if name == "lm_head" else st["cfg"].n_layers
+        mult = 1 if name.startswith("lm_head") else st["cfg"].n_layers
         tot_flops += fl * mult
         tot_ms += ms * mult
-        res[name] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 1), "split_k_workspace": need}
+        res[name] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 1), "split_k_workspace": d.workspace_bytes}
     return res, tot_flops, tot_ms
 
 

@@ -84,6 +84,24 @@ __device__ inline void top2_merge(float& m1, float& m2, int& i1, float b1, float
     m2 = fmaxf(m2, b1);
   }
 }
+// One DPP exchange of a top-2 partial with the partner lane of CTRL.
+template <int CTRL>
+__device__ inline void top2_dpp(float& m1, float& m2, int& i1) {
+  const float b1 = dpp_f32<CTRL>(m1), b2 = dpp_f32<CTRL>(m2);
+  const int bi = __builtin_amdgcn_update_dpp(0, i1, CTRL, 0xF, 0xF, true);
+  top2_merge(m1, m2, i1, b1, b2, bi);
+}
+// Every lane of each 16-lane row ends with the row's top-2: partners lane ^ 1,
+// lane ^ 2 (quad_perm), the other quad of its 8 (row_half_mirror), the other
+// 8 of its 16 (row_mirror) -- each step merges two disjoint lane sets, which
+// top2_merge needs (a partial merged with itself would turn its maximum into
+// its own second value).  All VALU: no LDS round trip.
+__device__ inline void top2_row16(float& m1, float& m2, int& i1) {
+  top2_dpp<0xB1>(m1, m2, i1);
+  top2_dpp<0x4E>(m1, m2, i1);
+  top2_dpp<0x141>(m1, m2, i1);
+  top2_dpp<0x140>(m1, m2, i1);
+}
 // Merges across the lanes l ^ 1, l ^ 2, ... l ^ (W / 2): every lane of a
 // W-lane group ends with the group's top-2.
 template <int W>
@@ -860,42 +878,55 @@ __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* til
   }
 }
 
-// Greedy-mode epilogue over a parked BM x BN fp32 tile: wave w takes rows
-// w, w + 8, ...; lane l the columns l, l + 64, ...; each value gets the
-// channel scale and bias exactly as Cols4::finish applies them (so it equals
-// the logit the store path would write), then the row's top-2 partial of the
-// tile is written for column tile n0 / BN.
+// Greedy-mode epilogue over a parked BM x BN fp32 tile: each 16-lane row of
+// a wave takes one tile row (a wave 4 rows at a time), lane j of it the
+// columns 4 j + 64 k .. + 3 (16-byte LDS reads, the 16 lanes covering 256
+// consecutive bytes: no bank conflicts); each value gets the channel scale
+// and bias exactly as Cols4::finish applies them (so it equals the logit the
+// store path would write); the row's top-2 over the tile's columns is
+// written for column tile n0 / BN.
 template <int BM, int BN, int NT = 512>
 __device__ inline void epilogue_top2(const GemmArgs& g, const float* tile, int pitch, int m0, int n0, int tid) {
-  constexpr int CPL = BN / 64;  // columns per lane
-  static_assert(CPL * 64 == BN, "epilogue_top2 tile width");
-  const int wave = tid >> 6, lane = tid & 63;
-  float sc[CPL], bi[CPL];
-  bool ok[CPL];
+  constexpr int KC = BN / 64;  // float4 chunks per lane
+  static_assert(KC * 64 == BN, "epilogue_top2 tile width");
+  const int wave = tid >> 6, lane = tid & 63, grp = lane >> 4, j = lane & 15;
+  float sc[KC][4], bi[KC][4];
+  bool ok[KC][4];
 #pragma unroll
-  for (int k = 0; k < CPL; ++k) {
-    const int c = n0 + lane + 64 * k;
-    ok[k] = c < g.N;
-    sc[k] = (g.w_scale && ok[k]) ? g.w_scale[c] : 1.f;
-    bi[k] = (g.bias && ok[k]) ? g.bias[c] : 0.f;
-  }
-  for (int r = wave; r < BM && m0 + r < g.M; r += NT / 64) {
+  for (int k = 0; k < KC; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = n0 + 64 * k + 4 * j + e;
+      ok[k][e] = c < g.N;
+      sc[k][e] = (g.w_scale && ok[k][e]) ? g.w_scale[c] : 1.f;
+      bi[k][e] = (g.bias && ok[k][e]) ? g.bias[c] : 0.f;
+    }
+  for (int r0 = 4 * wave; r0 < BM; r0 += 4 * (NT / 64)) {
+    const int r = r0 + grp;
     float m1 = -INFINITY, m2 = -INFINITY;
     int i1 = 0x7FFFFFFF;
+    if (r < BM) {
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) {
-      if (!ok[k]) continue;
-      float v = tile[r * pitch + lane + 64 * k];
-      if (g.w_scale) v *= sc[k];
-      if (g.bias) v += bi[k];
-      top2_push(m1, m2, i1, v, n0 + lane + 64 * k);
+      for (int k = 0; k < KC; ++k) {
+        const float4 t = *(const float4*)(tile + r * pitch + 64 * k + 4 * j);
+        const float tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (!ok[k][e]) continue;
+          float v = tv[e];
+          if (g.w_scale) v *= sc[k][e];
+          if (g.bias) v += bi[k][e];
+          top2_push(m1, m2, i1, v, n0 + 64 * k + 4 * j + e);
+        }
+      }
     }
-    top2_lanes<64>(m1, m2, i1);
-    if (lane == 0) g.amax[(int64_t)(m0 + r) * g.amax_ld + n0 / BN] = make_float4(m1, m2, __int_as_float(i1), 0.f);
+    top2_row16(m1, m2, i1);
+    if (j == 0 && r < BM && m0 + r < g.M)
+      g.amax[(int64_t)(m0 + r) * g.amax_ld + n0 / BN] = make_float4(m1, m2, __int_as_float(i1), 0.f);
   }
 }
 
-template <int BM, int BN, int STAGES, int REGS, int WM>
+template <int BM, int BN, int STAGES, int REGS, int WM, bool TOP2>
 __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
   typedef WsTile<BM, BN, STAGES, WM> T;
   constexpr int LPW = T::LPW, STAGE_BYTES = T::STAGE_BYTES, FM = T::FM, FN = T::FN;
@@ -1071,7 +1102,10 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
           }
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (g.amax) epilogue_top2<T::PR, BN>(g, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
+    // Greedy mode is a separate instantiation: the two epilogues in one kernel
+    // raised its scalar-register spills (24 -> 157 at 160 x 256) and slowed
+    // the K loop of every call.
+    if constexpr (TOP2) epilogue_top2<T::PR, BN>(g, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
     else epilogue_rows<T::PR, BN>(g, kz, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
     if (h + 1 < T::PH) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
@@ -1080,7 +1114,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
 template <int BM, int BN, int STAGES, int REGS = 0, int WM = 2>
 int launch_ws(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
-  gemm_bf16_ws_kernel<BM, BN, STAGES, REGS, WM><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
+  if (g.amax) gemm_bf16_ws_kernel<BM, BN, STAGES, REGS, WM, true><<<dim3((unsigned)tiles, 1, 1), 512, 0, s>>>(g);
+  else gemm_bf16_ws_kernel<BM, BN, STAGES, REGS, WM, false><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
   return check_launch("cbis_gemm(bf16 ws)");
 }
 
@@ -1263,7 +1298,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
         if (g.bias) x += bi;
         float m1 = ok ? x : -INFINITY, m2 = -INFINITY;
         int i1 = ok ? col : 0x7FFFFFFF;
-        top2_lanes<16>(m1, m2, i1);
+        top2_row16(m1, m2, i1);
         const int row = i * 16 + 4 * q + e;
         if (c16 == 0 && row < g.M)
           g.amax[(int64_t)row * g.amax_ld + blockIdx.x] = make_float4(m1, m2, __int_as_float(i1), 0.f);
