@@ -315,6 +315,8 @@ static_assert(32 * kQG == CBIS_PREFILL_TILE_ROWS, "prefill tile rows");
 // K/V blocks per wave's register ring: one block in flight while one is
 // computed (a deeper ring costs a wave per SIMD and measured slower).
 constexpr int kPrefillRing = 2;
+// Exponent headroom of the lazy softmax rescale (log2 units): p <= 2^8.
+constexpr float kLazyRescale = 8.f;
 
 // The two 32-lane halves of v exchanged: each lane gets f(v, v of lane ^ 32)
 // through v_permlane32_swap (no LDS round trip).
@@ -329,8 +331,10 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 // Workgroups from prefill_blocks on run the decode rows' split merge
 // (decode_merge over merge_rows rows) instead: the merge then shares the
 // prefill launch, which is independent of it, in place of a launch of its own.
+// At most 128 VGPRs (room for 4 waves per SIMD: 17.96 against 18.4 us on
+// config 4's chunks with the compiler's own 156).
 template <int HPW>
-__global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel(const PrefillArgs a,
+__global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_kernel(const PrefillArgs a,
                                                                                const DecodeArgs merge, int merge_rows,
                                                                                unsigned prefill_blocks) {
   if (blockIdx.x >= prefill_blocks) {
@@ -338,15 +342,24 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel
     return;
   }
   const int lane = threadIdx.x & 63;
-  const int wave_id = threadIdx.x >> 6;
+  const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: block tests and page ids per wave
   const int wave = wave_id % kPrefillWaves;  // key-block lane of this head
   const int hsub = wave_id / kPrefillWaves;
   const int n_hg = a.n_heads / HPW;
   const int tile = blockIdx.x / n_hg;
   const int head = (blockIdx.x % n_hg) * HPW + hsub;
-  const int4 td = *(const int4*)(a.tiles + 4 * (int64_t)tile);
-  const int row0 = td.x, nvalid = td.y, pos0 = td.w;
-  const int* bt = a.bt + (int64_t)td.z * a.bt_stride;
+  // The tile descriptor is the same for the whole workgroup: read it into
+  // scalar registers, so the tests on it (the causal-mask test per block)
+  // compile to scalar branches rather than exec masking.
+  // The tile descriptor is the same for the whole workgroup and the page ids
+  // of a 32-key block the same for the whole wave: both are read through the
+  // constant address space, i.e. with scalar loads (shorter round trips than
+  // per-lane loads of one address, and no share of the K/V loads' counter),
+  // and the tests on them compile to scalar branches.
+  typedef const __attribute__((address_space(4))) int cint_t;
+  cint_t* td = (cint_t*)(a.tiles + 4 * (int64_t)tile);
+  const int row0 = td[0], nvalid = td[1], pos0 = td[3];
+  cint_t* bt = (cint_t*)(a.bt + (int64_t)td[2] * a.bt_stride);
   const int D = a.n_heads * kHD;
   const int col = lane & 31;  // query index within a group (B / C column)
   const int half = lane >> 5;
@@ -409,7 +422,13 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel
   // own key (id_of) one block before that block's K/V loads (load_block):
   // the id load then has a whole block of compute to land in, and waiting
   // for it never waits for the K/V loads in flight.
-  auto id_of = [&](int j0) { return bt[min(j0 + col, kv_end - 1) / kPS]; };
+  // Page id of this lane's key j0 + col, clamped to kv_end - 1: keys j0 ..
+  // j0 + 15 lie on page min(j0, kv_end - 1) / 16, keys j0 + 16 .. j0 + 31 on
+  // page min(j0 + 16, kv_end - 1) / 16 (j0 is a multiple of 32).
+  auto id_of = [&](int j0) {
+    const int pa = bt[min(j0, kv_end - 1) / kPS], pb = bt[min(j0 + 16, kv_end - 1) / kPS];
+    return col < 16 ? pa : pb;
+  };
   auto load_block = [&](int j0, int id, KV& r) {
     const int kc = min(j0 + col, kv_end - 1);
     const int phys = min(max(id, 0), a.num_pages - 1);
@@ -464,13 +483,24 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel
         smax = fmaxf(h.x, h.y);
       }
       const float mloc = smax * a.qscale;
-      // A wave's first blocks may hold no key <= qpos for some queries (it
-      // does not start at key 0, and group 1 starts 32 positions later):
-      // while m and mloc are both -inf, the exponents are taken against 0 so
-      // p = 0 and the (empty) state stays 0.
-      const float mn = fmaxf(m[g], mloc);
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      const float corr = fast_exp2(m[g] - mref);
+      // Lazy rescaling: (m, l, o) stay referred to m, the exponent
+      // reference, which is raised -- and l, o rescaled by 2^(m_old - m_new)
+      // -- only when some query column's block maximum exceeds it by more
+      // than kLazyRescale (log2 units).  Otherwise p = 2^(s - m) <= 2^8, well
+      // inside fp32 and bf16, and the per-block o *= corr is skipped (it was a
+      // third of the block's VALU work).  In exact arithmetic the result does
+      // not depend on the reference; the wave merge below combines each
+      // wave's (m, l, o) by its own reference.  A column whose keys are all
+      // masked so far keeps m = -inf and p = 0 (exponents taken against 0).
+      if (__builtin_amdgcn_ballot_w64(mloc > m[g] + kLazyRescale) != 0) {
+        const float mn = fmaxf(m[g], mloc);
+        const float corr = mn == -INFINITY ? 1.f : fast_exp2(m[g] - mn);
+        l[g] *= corr;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[g][i] *= corr;
+        m[g] = mn;
+      }
+      const float mref = m[g] == -INFINITY ? 0.f : m[g];
       float lsum = 0.f;
       float pf[16];
 #pragma unroll
@@ -489,10 +519,7 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel
         const float2 h = halves(lsum);
         lsum = h.x + h.y;
       }
-      l[g] = l[g] * corr + lsum;
-      m[g] = mn;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[g][i] *= corr;
+      l[g] += lsum;
     }
     // V^T as the A operand: lane = dim (col), k-slot e of MFMA b holds key
     // 16*b + 8*(e/4) + 4*half + (e%4), matching P's register order.  The V
@@ -573,15 +600,20 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64) void paged_prefill_kernel
       for (int i = 0; i < 16; ++i) o[g][i] += ow[i] * c;
     }
     // o[g][i]: dim 8*(i/4) + 4*half + (i%4) of query 32 g + col.
+    // Dims 8 b + 4 half .. + 3 are o[g][4 b .. 4 b + 3]: one 8-byte (bf16) or
+    // 16-byte (fp32) store each (ldo % 4 == 0 and a 16-byte aligned out).
     const int qi = 32 * g + col;
     if (qi < nvalid) {
       const float inv = 1.f / l[g];
-      const int64_t ob = (int64_t)(row0 + qi) * a.ldo + head * kHD;
+      const int64_t ob = (int64_t)(row0 + qi) * a.ldo + head * kHD + 4 * half;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 8 * (i >> 2) + 4 * half + (i & 3);
-        if (a.out_bf16) ((uint16_t*)a.out)[ob + d] = f32_to_bf16(o[g][i] * inv);
-        else ((float*)a.out)[ob + d] = o[g][i] * inv;
+      for (int b = 0; b < 4; ++b) {
+        const float v0 = o[g][4 * b] * inv, v1 = o[g][4 * b + 1] * inv, v2 = o[g][4 * b + 2] * inv,
+                    v3 = o[g][4 * b + 3] * inv;
+        if (a.out_bf16)
+          *(uint2*)((uint16_t*)a.out + ob + 8 * b) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+        else
+          *(float4*)((float*)a.out + ob + 8 * b) = make_float4(v0, v1, v2, v3);
       }
     }
   }
