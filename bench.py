@@ -263,10 +263,12 @@ def gemm_timing(cbis, st, iters):
     return res, tot_flops, tot_ms
 
 
-def cpu_step_sample(oracle, spec, cache, tok, pos, sid):
-    """Times the C oracle (fp64, OpenMP) on one layer of a forward step over
-    the GPU cache's layer-0 K/V (copied to the host), and separately the
-    0-layer remainder (embedding + ln_f + lm_head).  Returns (t_layer, t_head)."""
+def cpu_step_sampler(oracle, spec, cache, tok, pos, sid):
+    """Sets up the C oracle (fp64, OpenMP) on one layer of a forward step over
+    the GPU cache's layer-0 K/V (copied to the host) and returns
+    run(rows=None) -> (t_layer, t_head): the time of that layer over the
+    given rows (all by default) and separately of the 0-layer remainder
+    (embedding + ln_f + lm_head) over them."""
     w = oracle.synthetic_weights(spec, seed=0, pos_rows=max(pos) + 1)
     om = oracle.OracleModel(w, max_pages=1)
     P = cache.max_pages()
@@ -290,27 +292,61 @@ def cpu_step_sample(oracle, spec, cache, tok, pos, sid):
     bt = np.zeros((len(uniq), width), np.int32)
     for q, j in uniq.items():
         bt[j, : len(tables[q])] = tables[q]
-    t0 = time.time()
-    om.forward_step(tok, pos, wpage, woff, bt, row_bt)
-    t_layer_plus_head = time.time() - t0
-    om._mdl.n_layers = 0
-    t1 = time.time()
-    om.forward_step(tok, pos, wpage, woff, bt, row_bt)
-    t_head = time.time() - t1
-    return t_layer_plus_head - t_head, t_head
+    tok_a, pos_a = np.asarray(tok, np.int32), np.asarray(pos, np.int32)
+
+    def run(rows=None):
+        r = np.arange(M) if rows is None else np.asarray(rows)
+        args = (tok_a[r], pos_a[r], wpage[r], woff[r], bt, row_bt[r])
+        om._mdl.n_layers = 1
+        t0 = time.time()
+        om.forward_step(*args)
+        t_layer_plus_head = time.time() - t0
+        om._mdl.n_layers = 0
+        t1 = time.time()
+        om.forward_step(*args)
+        t_head = time.time() - t1
+        om._mdl.n_layers = 1
+        return t_layer_plus_head - t_head, t_head
+
+    return run
 
 
-def cpu_baseline_c4(oracle, st, cbis):
-    """The C oracle on one layer of the same step + lm_head, scaled to 16
-    layers: a bounded sample (~10-30 s of CPU work)."""
+def cpu_step_sample(oracle, spec, cache, tok, pos, sid):
+    """One all-core run of cpu_step_sampler over every row."""
+    return cpu_step_sampler(oracle, spec, cache, tok, pos, sid)()
+
+
+def cpu_baseline_c4(oracle, st, cbis, runs=3):
+    """The C oracle on config 4's step, scaled to 16 layers from one layer
+    (bounded samples of ~10-30 s of CPU work), median of `runs` runs each:
+    all cores on every row (the reported value), and 1 core on every 16th
+    row (12 decode rows; the 64 prefill rows at positions that are multiples
+    of 16), scaled by rows."""
     spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
                             max_seq=32768, weight_dtype="bf16", kv_dtype="bf16")
-    t_layer, t_head = cpu_step_sample(oracle, spec, st["cache"], st["tok"], st["pos"], st["sid"])
-    t_step = t_layer * 16 + t_head
-    return {"value": round(192.0 / t_step, 3), "unit": "decode tokens/s", "cores": oracle.lib().orc_num_threads(),
-            "kind": "port",
-            "sample": f"oracle fp64 forward of config 4's 1216-row step, 1 of 16 layers ({t_layer:.1f}s)"
-                      f" + lm_head ({t_head:.1f}s), scaled to 16 layers; step {t_step:.1f}s"}
+    run = cpu_step_sampler(oracle, spec, st["cache"], st["tok"], st["pos"], st["sid"])
+    lib = oracle.lib()
+    cores = lib.orc_num_threads()
+
+    def median_step(rows, scale):
+        ts = [run(rows) for _ in range(runs)]
+        tl = float(np.median([t[0] for t in ts])) * scale
+        th = float(np.median([t[1] for t in ts])) * scale
+        return tl, th, tl * 16 + th
+
+    tl, th, t_step = median_step(None, 1.0)
+    sub = [i for i, p in enumerate(st["pos"]) if (i < 192 and i % 16 == 0) or (i >= 192 and p % 16 == 0)]
+    old = lib.orc_set_num_threads(1)
+    try:
+        tl1, th1, t_step1 = median_step(sub, len(st["tok"]) / len(sub))
+    finally:
+        lib.orc_set_num_threads(old)
+    return {"value": round(192.0 / t_step, 3), "unit": "decode tokens/s", "cores": cores, "kind": "port",
+            "value_1core": round(192.0 / t_step1, 4),
+            "sample": f"oracle fp64 forward of config 4's 1216-row step, 1 of 16 layers (median of {runs}: "
+                      f"{tl:.2f} s) + lm_head ({th:.2f} s), scaled to 16 layers: step {t_step:.1f} s on {cores} "
+                      f"threads; on 1 thread the {len(sub)} rows of every 16th position (median of {runs}), "
+                      f"scaled by rows: layer {tl1:.1f} s + lm_head {th1:.1f} s -> step {t_step1:.0f} s"}
 
 
 def recorded_traffic(name):

@@ -1313,32 +1313,62 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
   }
 }
 
-// Greedy-mode reduce: one wave per row folds the row's n_parts top-2
-// partials (RAW: the row's fp32 values themselves) in any order -- the merge
-// keeps the lowest index among equal maxima -- and writes the index (0 for a
-// row with no maximum, as the strict-> scan leaves it) and the top-2 margin.
-template <bool RAW>
+// Greedy-mode reduce: the TPR threads of a row (one wave, or a 256-thread
+// workgroup for long rows) fold the row's n_parts top-2 partials (RAW: the
+// row's fp32 values themselves) in any order -- the merge keeps the lowest
+// index among equal maxima -- and write the index (0 for a row with no
+// maximum, as the strict-> scan leaves it) and the top-2 margin.
+template <bool RAW, int TPR>
 __global__ __launch_bounds__(256) void top2_reduce_kernel(const void* src, int n_parts, int64_t ld, int M,
                                                           int* __restrict__ next, float* __restrict__ margin) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= M) return;
+  constexpr int RPB = 256 / TPR;  // rows per workgroup
+  const int t = threadIdx.x % TPR;
+  const int row = blockIdx.x * RPB + threadIdx.x / TPR;
   float m1 = -INFINITY, m2 = -INFINITY;
   int i1 = 0x7FFFFFFF;
-  if constexpr (RAW) {
-    const float* r = (const float*)src + (int64_t)row * ld;
-    for (int c = lane; c < n_parts; c += 64) top2_push(m1, m2, i1, r[c], c);
-  } else {
-    const float4* r = (const float4*)src + (int64_t)row * ld;
-    for (int c = lane; c < n_parts; c += 64) {
-      const float4 p = r[c];
-      top2_merge(m1, m2, i1, p.x, p.y, __float_as_int(p.z));
+  if (row < M) {
+    if constexpr (RAW) {
+      const float* r = (const float*)src + (int64_t)row * ld;
+      for (int c = t; c < n_parts; c += TPR) top2_push(m1, m2, i1, r[c], c);
+    } else {
+      const float4* r = (const float4*)src + (int64_t)row * ld;
+      for (int c = t; c < n_parts; c += TPR) {
+        const float4 p = r[c];
+        top2_merge(m1, m2, i1, p.x, p.y, __float_as_int(p.z));
+      }
     }
   }
   top2_lanes<64>(m1, m2, i1);
-  if (lane == 0) {
+  if constexpr (TPR > 64) {
+    __shared__ float s1[TPR / 64], s2[TPR / 64];
+    __shared__ int si[TPR / 64];
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { s1[w] = m1; s2[w] = m2; si[w] = i1; }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int k = 1; k < TPR / 64; ++k) top2_merge(m1, m2, i1, s1[k], s2[k], si[k]);
+  } else if (t != 0) {
+    return;
+  }
+  if (row < M) {
     next[row] = i1 == 0x7FFFFFFF ? 0 : i1;
     if (margin) margin[row] = m1 - m2;
   }
+}
+
+// Launches the greedy reduce: a wave per row up to 512 partials, else a
+// 256-thread workgroup per row (config 5's fp8 lm_head: 16 rows x 2000
+// partials, 12.9 -> a few us).
+int top2_reduce(bool raw, const void* src, int n_parts, int64_t ld, int M, int* next, float* margin, hipStream_t s) {
+  if (n_parts <= 512) {
+    const unsigned blocks = (unsigned)cdiv(M, 4);
+    if (raw) top2_reduce_kernel<true, 64><<<blocks, 256, 0, s>>>(src, n_parts, ld, M, next, margin);
+    else top2_reduce_kernel<false, 64><<<blocks, 256, 0, s>>>(src, n_parts, ld, M, next, margin);
+  } else {
+    if (raw) top2_reduce_kernel<true, 256><<<(unsigned)M, 256, 0, s>>>(src, n_parts, ld, M, next, margin);
+    else top2_reduce_kernel<false, 256><<<(unsigned)M, 256, 0, s>>>(src, n_parts, ld, M, next, margin);
+  }
+  return check_launch("cbis_gemm_argmax(reduce)");
 }
 
 template <typename XT, typename WT>
@@ -1681,14 +1711,12 @@ int cbis_gemm_argmax(const cbis_gemm_desc* d, int* next_token, float* margin, vo
   CBIS_REQUIRE(workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15u) == 0, CBIS_ERR_WORKSPACE,
                "%s: workspace %zu bytes (16-byte aligned), need %zu", who, workspace_bytes, need);
   hipStream_t s = (hipStream_t)stream;
-  const unsigned blocks = (unsigned)cdiv(d->M, 4);
   const int cols = argmax_tile_cols(d);
   if (cols > 0) {
     GemmArgs g;
     const int rc = gemm_run(d, s, g, (float4*)workspace);
     if (rc) return rc;
-    top2_reduce_kernel<false><<<blocks, 256, 0, s>>>(workspace, g.amax_ld, g.amax_ld, d->M, next_token, margin);
-    return check_launch(who);
+    return top2_reduce(false, workspace, g.amax_ld, g.amax_ld, d->M, next_token, margin, s);
   }
   // Paths without a greedy epilogue: the logits into d->Y (when it is an fp32
   // [M, N] buffer) or the workspace, then the same reduce over them.
@@ -1704,8 +1732,7 @@ int cbis_gemm_argmax(const cbis_gemm_desc* d, int* next_token, float* margin, vo
   e.workspace_bytes = workspace_bytes - lg;
   const int rc = cbis_gemm(&e, stream);
   if (rc) return rc;
-  top2_reduce_kernel<true><<<blocks, 256, 0, s>>>(e.Y, d->N, e.ldy, d->M, next_token, margin);
-  return check_launch(who);
+  return top2_reduce(true, e.Y, d->N, e.ldy, d->M, next_token, margin, s);
 }
 
 size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {

@@ -200,8 +200,7 @@ class TransformerRunner {
   void* d_attn_ = nullptr;
   void* d_h_ = nullptr;
   float* d_logits_ = nullptr;
-  int* d_next_ = nullptr;
-  float* d_margin_ = nullptr;
+  int* d_next_ = nullptr;  // [M] tokens then [M] margins (fp32) of a greedy step
   void* d_amax_ws_ = nullptr;  // cbis_gemm_argmax partials
   size_t amax_ws_bytes_ = 0;
   std::vector<float> margins_;

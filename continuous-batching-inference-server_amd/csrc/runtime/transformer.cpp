@@ -49,8 +49,9 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   hip_check(hipMalloc(&d_attn_, R * D * ae), "hipMalloc attn");
   hip_check(hipMalloc(&d_h_, R * F * ae), "hipMalloc h");
   hip_check(hipMalloc((void**)&d_logits_, R * V * 4), "hipMalloc logits");
-  hip_check(hipMalloc((void**)&d_next_, R * 4), "hipMalloc next");
-  hip_check(hipMalloc((void**)&d_margin_, R * 4), "hipMalloc margin");
+  // Greedy results: a step's M tokens, then its M margins right after them
+  // (one D2H copy brings both back).
+  hip_check(hipMalloc((void**)&d_next_, R * 8), "hipMalloc next");
   // Split-KV partials: the automatic split keeps rows * splits <= 2048 + rows.
   ws_bytes_ = (2048 + R) * (size_t)cfg_.n_heads * (cfg_.head_dim + 4) * 4;
   hip_check(hipMalloc(&d_ws_, ws_bytes_), "hipMalloc attention workspace");
@@ -81,7 +82,7 @@ TransformerRunner::~TransformerRunner() {
   for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
   if (stream_) (void)hipStreamDestroy(stream_);
   (void)hipFree(d_x_); (void)hipFree(d_xn_); (void)hipFree(d_q_); (void)hipFree(d_attn_);
-  (void)hipFree(d_h_); (void)hipFree(d_logits_); (void)hipFree(d_next_); (void)hipFree(d_margin_);
+  (void)hipFree(d_h_); (void)hipFree(d_logits_); (void)hipFree(d_next_);
   (void)hipFree(d_ws_);
   if (d_amax_ws_) (void)hipFree(d_amax_ws_);
   if (d_gemm_ws_) (void)hipFree(d_gemm_ws_);
@@ -332,7 +333,8 @@ void TransformerRunner::enqueue_forward(bool greedy) {
   g.w_dtype = wd; g.W = w_.lm_head; g.ldw = D; g.w_scale = w_.lm_scale;
   g.y_dtype = CBIS_F32; g.Y = d_logits_; g.ldy = V;
   if (greedy)
-    cbis_check(cbis_gemm_argmax(&g, d_next_, d_margin_, d_amax_ws_, amax_ws_bytes_, s), "lm_head gemm + argmax");
+    cbis_check(cbis_gemm_argmax(&g, d_next_, (float*)(d_next_ + M), d_amax_ws_, amax_ws_bytes_, s),
+               "lm_head gemm + argmax");
   else
     cbis_check(cbis_gemm(&g, s), "lm_head gemm");
 }
@@ -393,13 +395,14 @@ std::vector<int> TransformerRunner::forward_step_greedy(const std::vector<int>& 
     throw std::invalid_argument("forward_step_greedy: token_ids/positions/seq_ids sizes differ");
   prepare(token_ids.data(), positions.data(), seq_ids.data(), M);
   run_step(true);
-  std::vector<int> next(M);
-  margins_.resize(M);
-  hip_check(hipMemcpyAsync(next.data(), d_next_, (size_t)M * 4, hipMemcpyDeviceToHost, stream_), "D2H tokens");
-  hip_check(hipMemcpyAsync(margins_.data(), d_margin_, (size_t)M * 4, hipMemcpyDeviceToHost, stream_),
-            "D2H margins");
+  std::vector<int> both(2 * (size_t)M);
+  hip_check(hipMemcpyAsync(both.data(), d_next_, (size_t)M * 8, hipMemcpyDeviceToHost, stream_),
+            "D2H tokens and margins");
   hip_check(hipStreamSynchronize(stream_), "forward_step_greedy sync");
-  return next;
+  margins_.resize(M);
+  std::memcpy(margins_.data(), both.data() + M, (size_t)M * 4);
+  both.resize(M);
+  return both;
 }
 
 }  // namespace cbis

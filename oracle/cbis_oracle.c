@@ -371,3 +371,16 @@ int orc_num_threads(void) {
   return 1;
 #endif
 }
+
+/* Threads for the following calls (bench.py times a 1-core and an all-core
+ * sample); returns the previous count. */
+int orc_set_num_threads(int n) {
+#ifdef _OPENMP
+  const int old = omp_get_max_threads();
+  if (n > 0) omp_set_num_threads(n);
+  return old;
+#else
+  (void)n;
+  return 1;
+#endif
+}

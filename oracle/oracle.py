@@ -91,6 +91,8 @@ def _declare(L):
     L.orc_argmax_rows.argtypes = [_I, _I, _P, _I, _P]
     L.orc_forward_step.argtypes = [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P]
     L.orc_num_threads.restype = _I
+    L.orc_set_num_threads.restype = _I
+    L.orc_set_num_threads.argtypes = [_I]
 
 
 def _ptr(a):
