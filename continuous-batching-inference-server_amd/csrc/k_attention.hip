@@ -296,7 +296,7 @@ struct PrefillArgs {
   int out_bf16;
   int n_heads;
   int max_kv;
-  float qscale;  // log2(e) / sqrt(head_dim), applied to S in fp32
+  float qscale;  // log2(e) / sqrt(head_dim), folded into Q before its bf16 rounding
 };
 
 // Workgroup: one tile of up to 64 query rows x HPW adjacent heads,
@@ -307,13 +307,16 @@ struct PrefillArgs {
 // block read from the pages serves 64 queries.  A key's head_dim slice is
 // 64 bytes, so adjacent heads of one workgroup read the same 128-byte lines
 // at about the same time.  Measured on config 4's two 512-row chunks (one
-// layer): 25.1 us against 27.3 for 32-row tiles with four waves per head,
-// 38 with eight.
+// layer, isolated): 16.3 us.  Slower: four waves per head (23.1 with one head
+// per workgroup, 24.9 with two), a tile pair per workgroup whose waves take
+// equal contiguous shares of both tiles' blocks (20.1), four waves per head
+// on the long tiles only (20.8 - 24.6: the workgroups' pairing on the CUs is
+// lost), deeper K/V rings (17.4 with 3 blocks, 18.8 with 4).
 constexpr int kPrefillWaves = 2;  // waves per head
 constexpr int kQG = 2;            // 32-query groups per tile
 static_assert(32 * kQG == CBIS_PREFILL_TILE_ROWS, "prefill tile rows");
 // K/V blocks per wave's register ring: one block in flight while one is
-// computed (a deeper ring costs a wave per SIMD and measured slower).
+// computed.
 constexpr int kPrefillRing = 2;
 // Exponent headroom of the lazy softmax rescale (log2 units): p <= 2^8.
 constexpr float kLazyRescale = 8.f;
@@ -331,8 +334,6 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 // Workgroups from prefill_blocks on run the decode rows' split merge
 // (decode_merge over merge_rows rows) instead: the merge then shares the
 // prefill launch, which is independent of it, in place of a launch of its own.
-// At most 128 VGPRs (room for 4 waves per SIMD: 17.96 against 18.4 us on
-// config 4's chunks with the compiler's own 156).
 template <int HPW>
 __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_kernel(const PrefillArgs a,
                                                                                const DecodeArgs merge, int merge_rows,
@@ -392,8 +393,8 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      qb0[g][e] = (short)f32_to_bf16(f[e]);
-      qb1[g][e] = (short)f32_to_bf16(f[8 + e]);
+      qb0[g][e] = (short)f32_to_bf16(f[e] * a.qscale);
+      qb1[g][e] = (short)f32_to_bf16(f[8 + e] * a.qscale);
     }
   }
   const int kv_end = min(pos0 + nvalid, a.max_kv);  // keys [0, kv_end) needed by the tile
@@ -402,14 +403,23 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
   // transposing reads).
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[HPW * kPrefillWaves][32][kHD];
   auto& vt_w = vt_all[wave_id];
-  f32x16_t o[kQG];
-  float m[kQG], l[kQG];
+  // Per query column: o (the P.V accumulator), lacc (every entry the
+  // column's sum of the bf16-rounded p: an MFMA of an all-ones A with P^T,
+  // beside the P.V MFMAs, in place of 16 adds and a lane exchange per block)
+  // and the softmax reference m (-inf until the column meets an unmasked
+  // key).  negm (every entry -m, or 0 while m = -inf) is the C operand of
+  // the score MFMA, so the scores come out relative to m and p = 2^s needs
+  // no subtraction per score.
+  f32x16_t o[kQG], lacc[kQG], negm[kQG];
+  float m[kQG];
+  bf16x8_t ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (short)0x3F80;
 #pragma unroll
   for (int g = 0; g < kQG; ++g) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[g][i] = 0.f;
+    for (int i = 0; i < 16; ++i) o[g][i] = lacc[g][i] = negm[g][i] = 0.f;
     m[g] = -INFINITY;
-    l[g] = 0.f;
   }
 
   // K rows for keys j0 + col in the A-operand layout (lane = key, dims
@@ -457,57 +467,70 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
       dst[1] = r.v1;
     }
     bf16x8_t pb0[kQG], pb1[kQG];
+    // Both groups' scores first (no branch between their MFMAs), then one
+    // uniform mask test and one uniform rescale test for the block.
+    // s[g][i]: key j0 + 8*(i/4) + 4*half + (i%4), query 32 g + col, in log2
+    // units relative to m: q.k * log2(e)/sqrt(hd) - m (the scale is folded
+    // into Q).  Only blocks reaching past the tile's first query position or
+    // past kv_end need the causal mask.
+    f32x16_t s[kQG];
 #pragma unroll
     for (int g = 0; g < kQG; ++g) {
-      f32x16_t s;
+      s[g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k0, qb0[g], negm[g], 0, 0, 0);
+      s[g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k1, qb1[g], s[g], 0, 0, 0);
+    }
+    if (j0 + 31 > pos0 || j0 + 31 >= kv_end) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = 0.f;
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k0, qb0[g], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.k1, qb1[g], s, 0, 0, 0);
-      // s[i]: key j0 + 8*(i/4) + 4*half + (i%4), query 32 g + col; raw q.k
-      // (the scale log2(e)/sqrt(hd) > 0 is applied in the exponent).  Only
-      // blocks reaching past the group's first query position or past kv_end
-      // need the causal mask (uniform test).
-      if (j0 + 31 > pos0 + 32 * g || j0 + 31 >= kv_end) {
+      for (int g = 0; g < kQG; ++g)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int kj = j0 + 8 * (i >> 2) + 4 * half + (i & 3);
-          if (kj > qpos[g] || kj >= kv_end) s[i] = -INFINITY;
+          if (kj > qpos[g] || kj >= kv_end) s[g][i] = -INFINITY;
         }
-      }
-      float smax = s[0];
+    }
+    float smax[kQG], thr[kQG];
+    bool up[kQG];
 #pragma unroll
-      for (int i = 1; i < 16; ++i) smax = fmaxf(smax, s[i]);
-      {
-        const float2 h = halves(smax);
-        smax = fmaxf(h.x, h.y);
-      }
-      const float mloc = smax * a.qscale;
-      // Lazy rescaling: (m, l, o) stay referred to m, the exponent
-      // reference, which is raised -- and l, o rescaled by 2^(m_old - m_new)
-      // -- only when some query column's block maximum exceeds it by more
-      // than kLazyRescale (log2 units).  Otherwise p = 2^(s - m) <= 2^8, well
-      // inside fp32 and bf16, and the per-block o *= corr is skipped (it was a
-      // third of the block's VALU work).  In exact arithmetic the result does
-      // not depend on the reference; the wave merge below combines each
-      // wave's (m, l, o) by its own reference.  A column whose keys are all
-      // masked so far keeps m = -inf and p = 0 (exponents taken against 0).
-      if (__builtin_amdgcn_ballot_w64(mloc > m[g] + kLazyRescale) != 0) {
-        const float mn = fmaxf(m[g], mloc);
-        const float corr = mn == -INFINITY ? 1.f : fast_exp2(m[g] - mn);
-        l[g] *= corr;
+    for (int g = 0; g < kQG; ++g) {
+      float v = s[g][0];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[g][i] *= corr;
+      for (int i = 1; i < 16; ++i) v = fmaxf(v, s[g][i]);
+      const float2 h = halves(v);
+      smax[g] = fmaxf(h.x, h.y);
+      thr[g] = m[g] == -INFINITY ? -INFINITY : kLazyRescale;
+      up[g] = smax[g] > thr[g];
+    }
+    // Lazy rescaling: m is raised -- o and lacc rescaled by 2^(m_old - m_new),
+    // the block's scores shifted, negm reloaded -- only when some column's
+    // block maximum exceeds it by more than kLazyRescale (log2 units), or on
+    // a column's first unmasked key.  Otherwise p = 2^s <= 2^8, well inside
+    // fp32 and bf16.  In exact arithmetic the result does not depend on the
+    // reference; the wave merge below combines each wave's (m, l, o) by its
+    // own reference.  A column whose keys are all masked so far keeps
+    // m = -inf and p = 0.
+    if (__builtin_amdgcn_ballot_w64(up[0] || up[1]) != 0) {
+#pragma unroll
+      for (int g = 0; g < kQG; ++g) {
+        const float cur = m[g] == -INFINITY ? 0.f : m[g];
+        const float mn = up[g] ? fmaxf(m[g], smax[g] + cur) : m[g];
+        const float corr = (up[g] && m[g] != -INFINITY) ? fast_exp2(m[g] - mn) : 1.f;
+        const float d = up[g] ? mn - cur : 0.f;
+        const float nm = mn == -INFINITY ? 0.f : -mn;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          s[g][i] -= d;
+          o[g][i] *= corr;
+          lacc[g][i] *= corr;
+          negm[g][i] = nm;
+        }
         m[g] = mn;
       }
-      const float mref = m[g] == -INFINITY ? 0.f : m[g];
-      float lsum = 0.f;
+    }
+#pragma unroll
+    for (int g = 0; g < kQG; ++g) {
       float pf[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        pf[i] = fast_exp2(fmaf(s[i], a.qscale, -mref));
-        lsum += pf[i];
-      }
+      for (int i = 0; i < 16; ++i) pf[i] = fast_exp2(s[g][i]);
       uint4 u0, u1;
       u0.x = pack_bf16x2(pf[0], pf[1]);   u0.y = pack_bf16x2(pf[2], pf[3]);
       u0.z = pack_bf16x2(pf[4], pf[5]);   u0.w = pack_bf16x2(pf[6], pf[7]);
@@ -515,11 +538,6 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
       u1.z = pack_bf16x2(pf[12], pf[13]); u1.w = pack_bf16x2(pf[14], pf[15]);
       pb0[g] = __builtin_bit_cast(bf16x8_t, u0);
       pb1[g] = __builtin_bit_cast(bf16x8_t, u1);
-      {
-        const float2 h = halves(lsum);
-        lsum = h.x + h.y;
-      }
-      l[g] += lsum;
     }
     // V^T as the A operand: lane = dim (col), k-slot e of MFMA b holds key
     // 16*b + 8*(e/4) + 4*half + (e%4), matching P's register order.  The V
@@ -538,6 +556,8 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
     for (int g = 0; g < kQG; ++g) {
       o[g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va0, pb0[g], o[g], 0, 0, 0);
       o[g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va1, pb1[g], o[g], 0, 0, 0);
+      lacc[g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb0[g], lacc[g], 0, 0, 0);
+      lacc[g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb1[g], lacc[g], 0, 0, 0);
     }
     // The next block's V writes come after these reads in program order.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -575,26 +595,27 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
 #pragma unroll
   for (int g = 0; g < kQG; ++g) {
     pm_all[hsub][wave][g][lane] = m[g];
-    pl_all[hsub][wave][g][lane] = l[g];
+    pl_all[hsub][wave][g][lane] = lacc[g][0];
     if (wave > 0) po_all[hsub][wave - 1][g][lane] = o[g];
   }
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int g = 0; g < kQG; ++g) {
+    float l = lacc[g][0];
     float M = m[g];
 #pragma unroll
     for (int w = 1; w < kPrefillWaves; ++w) M = fmaxf(M, pm_all[hsub][w][g][lane]);
     {
       const float c0 = fast_exp2(m[g] - M);
-      l[g] *= c0;
+      l *= c0;
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[g][i] *= c0;
     }
 #pragma unroll
     for (int w = 1; w < kPrefillWaves; ++w) {
       const float c = fast_exp2(pm_all[hsub][w][g][lane] - M);
-      l[g] += pl_all[hsub][w][g][lane] * c;
+      l += pl_all[hsub][w][g][lane] * c;
       const f32x16_t ow = po_all[hsub][w - 1][g][lane];
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[g][i] += ow[i] * c;
@@ -604,7 +625,7 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
     // 16-byte (fp32) store each (ldo % 4 == 0 and a 16-byte aligned out).
     const int qi = 32 * g + col;
     if (qi < nvalid) {
-      const float inv = 1.f / l[g];
+      const float inv = 1.f / l;
       const int64_t ob = (int64_t)(row0 + qi) * a.ldo + head * kHD + 4 * half;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
