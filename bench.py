@@ -649,7 +649,8 @@ def run_c2(args, cbis, oracle):
     """Config 2: the isolated flattened-batch linear layers of the reference
     model (d_model 256): QKV 256->768 (+bias), out-proj 256->256 (+bias),
     MLP up 256->1024 (+bias, GELU), MLP down 1024->256 (+bias, residual), at
-    M in {64, 512, 4096}, fp32 and bf16 (fp32 accumulate).  Device time per
+    M in {64, 512, 4096}, fp32 and bf16 (fp32 accumulate), each call given
+    the split-K workspace cbis_gemm_workspace_size asks for.  Device time per
     call from a replayed graph of `steps` calls.  value = total flops of the
     24 GEMMs / their summed time; each shape is reported with
     its TFLOP/s, bytes moved and roofline fraction (fp32: MFMA-bound against
@@ -680,6 +681,9 @@ def run_c2(args, cbis, oracle):
                 if has_r:
                     d.residual, d.ldr = Y.data_ptr(), N
                 d.y_dtype, d.Y, d.ldy = cbis.F32, Y.data_ptr(), N
+                need = K_.cbis_gemm_workspace_size(ctypes.byref(d))
+                ws = torch.empty(max(1, need // 4), dtype=torch.float32, device=dev)
+                d.workspace, d.workspace_bytes = ws.data_ptr(), need
                 fn = lambda d=d: cbis.check(K_.cbis_gemm(ctypes.byref(d), torch.cuda.current_stream().cuda_stream))
                 ms = ev.time_graph(fn, max(5, args.steps))
                 fl = 2.0 * M * N * K

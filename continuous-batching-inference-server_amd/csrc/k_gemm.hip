@@ -1487,13 +1487,45 @@ int launch(const GemmArgs& g, hipStream_t s) {
   return check_launch("cbis_gemm");
 }
 
+// fp32 x fp32 tiling.  A 32x32x2 fp32 MFMA occupies its SIMD for 64 cycles,
+// so one wave per SIMD cannot hide its LDS reads and barriers: large grids
+// take 64 x 128 tiles on 8 waves (two per SIMD; config 2 at M = 4096, K =
+// 256: QKV 40.9 -> 24.8 us, MLP up 41.4 -> 25.7 against 128 x 128 on 4
+// waves), and grids with fewer than 4 workgroups of 4 waves per CU split K
+// into up to 4 parts when the caller gives the workspace (config 2, M = 512:
+// MLP down 35.5 -> 14.2 us, the K = 256 shapes 13 -> 9.4-11.7 us).
+struct F32Plan {
+  bool wide;  // 64 x 128 on 8 waves; else 64 x 64 (32 x 64 for M <= 32) on 4 waves
+  int ksplit = 1;
+  int k_per = 0;
+};
+
+F32Plan plan_f32(int M, int N, int K) {
+  F32Plan p;
+  p.wide = cdiv(M, 128) * cdiv(N, 128) >= 192;
+  p.k_per = K;
+  if (p.wide) return p;
+  const int64_t tiles = M <= 32 ? cdiv(M, 32) * cdiv(N, 64) : cdiv(M, 64) * cdiv(N, 64);
+  const int kt = K / 32;
+  // A grid that already gives every CU a workgroup splits only deep K (each
+  // part >= 8 K tiles): config 2's out-projection at M = 4096 (256 tiles,
+  // K = 256) measured 13.5 us whole and 17.3 in two parts.
+  const int min_kt = tiles >= kCUs ? 8 : 4;
+  const int ks = (int)std::min<int64_t>({4, (4 * kCUs) / std::max<int64_t>(1, tiles), kt / min_kt});
+  if (ks <= 1) return p;
+  const int per = (kt + ks - 1) / ks;
+  p.ksplit = (kt + per - 1) / per;
+  p.k_per = per * 32;
+  return p;
+}
+
 // Picks a tile shape from the problem size: the largest tile that still
 // gives the 256 CUs at least about one workgroup each.
 template <typename XT, typename WT>
 int dispatch(const GemmArgs& g, hipStream_t s) {
   const int64_t t128 = cdiv(g.M, 128) * cdiv(g.N, 128);
   if constexpr (sizeof(XT) == 4) {
-    if (t128 >= 192) return launch<128, 128, 2, 2, XT, WT>(g, s);
+    if (plan_f32(g.M, g.N, g.K).wide) return launch<64, 128, 2, 4, XT, WT>(g, s);
     if (g.M <= 32) return launch<32, 64, 1, 2, XT, WT>(g, s);
     return launch<64, 64, 2, 2, XT, WT>(g, s);
   } else {
@@ -1588,7 +1620,16 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax =
     if (d->w_dtype == CBIS_BF16) return launch_skinny<uint16_t, uint16_t>(g, s);
     return launch_skinny<uint16_t, uint8_t>(g, s);
   }
-  if (f32) return dispatch<float, float>(g, s);
+  if (f32) {
+    const F32Plan p = plan_f32(d->M, d->N, d->K);
+    const size_t need = (size_t)p.ksplit * d->M * d->N * sizeof(float);
+    if (!amax && p.ksplit > 1 && d->workspace && d->workspace_bytes >= need) {
+      g.ksplit = p.ksplit;
+      g.k_per = p.k_per;
+      g.partial = (float*)d->workspace;
+    }
+    return dispatch<float, float>(g, s);
+  }
   if (d->w_dtype == CBIS_BF16) {
     // The direct-to-LDS path needs 16-byte aligned rows of both operands.
     if (dma_eligible(d)) {
@@ -1613,9 +1654,13 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax =
       }
       // Grids with fewer 128 x 128 tiles than CUs run 64 x 64 tiles (4 waves
       // of 32 x 32): four times the workgroups (config 4's out-projection,
-      // 160 tiles: 28.3 -> 23.4 us).
-      if (g.ksplit == 1 && cdiv(d->M, kDmaBM) * cdiv(d->N, kDmaBN) < kCUs)
+      // 160 tiles: 28.3 -> 23.4 us).  A third ring slot pays when the grid
+      // fills the CUs and K has 8 or more tiles (config 2's MLP down at
+      // M = 4096, K = 1024: 12.2 -> 10.7 us; at M = 512 it costs 1 us).
+      if (g.ksplit == 1 && cdiv(d->M, kDmaBM) * cdiv(d->N, kDmaBN) < kCUs) {
+        if (d->K >= 512 && cdiv(d->M, 64) * cdiv(d->N, 64) >= kCUs) return launch_dma<64, 64, 2, 2, 3>(g, s);
         return launch_dma<64, 64, 2, 2, 2>(g, s);
+      }
       return launch_dma<kDmaBM, kDmaBN, 2, 4, 2>(g, s);
     }
     return dispatch<uint16_t, uint16_t>(g, s);
@@ -1736,7 +1781,15 @@ int cbis_gemm_argmax(const cbis_gemm_desc* d, int* next_token, float* margin, vo
 }
 
 size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {
-  if (!d || d->M <= 0 || d->N <= 0 || d->K <= 0 || !dma_eligible(d) || d->K % 64) return 0;
+  if (!d || d->M <= 0 || d->N <= 0 || d->K <= 0) return 0;
+  if (d->x_dtype == CBIS_F32 && d->w_dtype == CBIS_F32) {
+    // gemm_run's fp32 paths: the skinny kernel (no split) or plan_f32.
+    const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * 4) % 16 == 0;
+    if ((d->M <= kSkinnyMaxM && w_al && d->K % 32 == 0) || d->K % 32) return 0;
+    const F32Plan p = plan_f32(d->M, d->N, d->K);
+    return p.ksplit > 1 ? (size_t)p.ksplit * d->M * d->N * sizeof(float) : 0;
+  }
+  if (!dma_eligible(d) || d->K % 64) return 0;
   const SplitPlan p = plan_dma_split(d->M, d->N, d->K);
   return p.ksplit > 1 ? (size_t)p.ksplit * d->M * d->N * sizeof(float) : 0;
 }

@@ -103,9 +103,13 @@ def _sample_rows(M, k, seed):
     return r
 
 
+@pytest.mark.parametrize("ws", [False, True], ids=["no_ws", "split_ws"])
 @pytest.mark.parametrize("M", [64, 512, 4096])
 @pytest.mark.parametrize("shape", C2_SHAPES, ids=lambda s: s[0])
-def test_gemm_fp32_c2(cbis, oracle, dev, M, shape):
+def test_gemm_fp32_c2(cbis, oracle, dev, M, shape, ws):
+    """fp32 C2 shapes; with the workspace cbis_gemm_workspace_size asks for,
+    the grids too small to fill the CUs split K (M = 512 all four shapes,
+    M = 4096 MLP down) and the partials are reduced with the epilogue."""
     import torch
     name, N, K, has_b, gelu, has_r = shape
     x = oracle.normal(11, 1, M * K).reshape(M, K)
@@ -115,7 +119,10 @@ def test_gemm_fp32_c2(cbis, oracle, dev, M, shape):
     X, W = to_dev(x, dev), to_dev(w, dev)
     B = to_dev(b, dev) if has_b else None
     Y = to_dev(r, dev) if has_r else torch.empty((M, N), dtype=torch.float32, device=dev)
-    _gemm(cbis, M, N, K, X, cbis.F32, W, cbis.F32, Y, cbis.F32, bias=B, gelu=gelu, residual=Y if has_r else None)
+    used = _gemm(cbis, M, N, K, X, cbis.F32, W, cbis.F32, Y, cbis.F32, bias=B, gelu=gelu,
+                 residual=Y if has_r else None, workspace=ws)
+    if ws:
+        assert (used > 0) == (M == 512 or (M == 4096 and name == "down")), used
     rows = _sample_rows(M, 512, M)
     ref = oracle.gemm(x[rows], w, bias=b, gelu=gelu, residual=None if r is None else r[rows])
     err = np.abs(Y.cpu().numpy()[rows] - ref).max()
@@ -1018,8 +1025,14 @@ def test_gemm_argmax_matches_logits(cbis, oracle, dev, M, N, K, wdt):
     d.w_dtype, d.W, d.ldw = wd, ptr(W), K
     d.w_scale, d.bias = ptr(S), ptr(B)
     d.y_dtype, d.Y, d.ldy = cbis.F32, ptr(Y), N
+    # the logits as cbis_gemm writes them with its split-K workspace, which
+    # the greedy call's fallback (paths that store logits) is given as well
+    gneed = K_.cbis_gemm_workspace_size(ctypes.byref(d))
+    gws = torch.empty(max(1, gneed // 4), dtype=torch.float32, device=dev)
+    d.workspace, d.workspace_bytes = ptr(gws), gneed
     cbis.check(K_.cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
     sync()
+    d.workspace, d.workspace_bytes = None, 0
     logits = Y.cpu().numpy()
     # greedy call: Y poisoned first, so a path that reduces in its epilogue
     # must not depend on it (and one that stores the logits rewrites it)
