@@ -533,7 +533,8 @@ def run_c3(args, cbis, oracle):
             "config": {"workload": "c3_paged_decode_attention", "rows": n, "heads": "8x32", "kv_len": "U[128,2048]",
                        "pool_pages": P, "page_size": 16},
             "roofline": {"bound": "hbm", "kernel": "paged_decode_kernel<f32> + split merge", "achieved": round(gbs, 1),
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": recorded_traffic("paged_decode_c3_hbm_traffic.md"),
                          "algorithmic_bytes": alg, "ms": round(ms, 4)},
             "cpu_baseline": cpu}
 
