@@ -89,6 +89,7 @@ KERNEL_SYMBOLS = {
     "cbis_fused_paged_causal_attention": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "cbis_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
     "cbis_gemm_layernorm": (_I, [ctypes.POINTER(GemmDesc), _P, _P, _F, _I, _P, _I64, _P]),
+    "cbis_layernorm_gemm": (_I, [ctypes.POINTER(GemmDesc), _P, _I64, _P, _P, _F, _P]),
     "cbis_kv_pages_gather": (_I, [_P, _P, _I, _I, ctypes.c_int64, _P, _I, _P]),
     "cbis_kv_pages_scatter": (_I, [_P, _P, _I, _I, ctypes.c_int64, _P, _I, _P]),
     "cbis_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),

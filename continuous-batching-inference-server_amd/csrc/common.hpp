@@ -174,9 +174,13 @@ __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // the variance's over those inside the row -- exchanged through terms
 // (__shared__ [4 VPW][64]), then reduced across the wave with wave_sum.  Every
 // wave computes the same mean and variance and stores its own chunks.
+// Products and sums stay separately rounded (no FMA contraction), so every
+// kernel that restates these statistics (the skinny GEMM's LayerNorm
+// prologue) reproduces them bit for bit.
 template <int VPW, typename YT>
 __device__ inline void ln_block_row(const float4* v, const float4* gg, const float4* bb, int wave, int lane, int N,
                                     int nch, float eps, float (*terms)[64], YT* y) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int j = 0; j < VPW; ++j) terms[j * 4 + wave][lane] = (v[j].x + v[j].y) + (v[j].z + v[j].w);
   __syncthreads();

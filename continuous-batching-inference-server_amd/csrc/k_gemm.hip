@@ -59,7 +59,23 @@ struct GemmArgs {
   // index of the max (bits), 0} to amax[row * amax_ld + column tile].
   float4* amax;
   int amax_ld;
+  // LayerNorm prologue (skinny kernel, cbis_layernorm_gemm): X is not read;
+  // the kernel forms X = LayerNorm(ln_x) row by row, as layernorm_kernel
+  // would (same statistics, same rounding), with ln_nch <= kLnMaxChunks.
+  const float* ln_x;
+  int64_t ln_ldx;
+  const float* ln_g;
+  const float* ln_b;
+  float ln_eps;
+  int ln_nch;
 };
+// cbis_layernorm_gemm forms the normalised rows in the skinny kernel for K up
+// to kLnPrologueMaxK: every workgroup re-reads its rows' fp32 x and their
+// statistics, which costs less than a LayerNorm launch only for short rows
+// (config 1, K = 256: 48.6-49.1k -> 50.3-50.4k decode tok/s; config 5,
+// K = 2048: 11.00 -> 11.27 ms per step, so there it runs the two kernels).
+constexpr int kLnPrologueMaxK = 512;
+constexpr int kLnMaxChunks = kLnPrologueMaxK / 256;  // float4 chunks per lane of a row
 
 // Top-2 of a row: the maximum m1 at the lowest index i1 among equal maxima
 // (the strict-> scan of src/bench_batching.cpp:66-73), and the largest value
@@ -1165,7 +1181,7 @@ struct SkinnyW<uint8_t> {  // fp8 e4m3: 8 elements = 8 bytes
 
 constexpr int kSkinnyWaves = 8;
 
-template <typename XT, typename WT, int MB>
+template <typename XT, typename WT, int MB, bool LN>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const GemmArgs g) {
   constexpr bool F32 = sizeof(XT) == 4;
   constexpr int KB = F32 ? 16 : 32;  // k per MFMA step
@@ -1185,6 +1201,76 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
 #pragma unroll
   for (int i = 0; i < MB; ++i) xrow[i] = min(i * 16 + c16, g.M - 1);
 
+  // LayerNorm prologue: each wave takes rows wave, wave + 8, ... of the
+  // workgroup's 16 MB rows and forms their mean and 1/std exactly as
+  // ln_block_row does (per-lane sums over the row's float4 chunks 0 .. nch-1
+  // in order, then wave_sum; no FMA contraction in either), so the
+  // normalised X equals layernorm_kernel's output bit for bit.  Rows past M
+  // repeat row M - 1.
+  __shared__ float ln_mu[16 * MB], ln_rs[16 * MB];
+  float lnm[MB], lnr[MB];
+  if constexpr (LN) {
+#pragma clang fp contract(off)
+    for (int r = wave; r < 16 * MB; r += kSkinnyWaves) {
+      const float* xr = g.ln_x + (int64_t)min(r, g.M - 1) * g.ln_ldx;
+      float4 v[kLnMaxChunks];
+#pragma unroll
+      for (int i = 0; i < kLnMaxChunks; ++i) {
+        const int c = 4 * (64 * i + lane);
+        v[i] = (i < g.ln_nch && c < g.K) ? *(const float4*)(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < kLnMaxChunks; ++i)
+        if (i < g.ln_nch) sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+      const float mean = wave_sum(sum) / (float)g.K;
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < kLnMaxChunks; ++i) {
+        const float a0 = v[i].x - mean, a1 = v[i].y - mean, a2 = v[i].z - mean, a3 = v[i].w - mean;
+        if (i < g.ln_nch && (i * 64 + lane) * 4 < g.K) sq += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+      }
+      const float inv = rsqrtf(wave_sum(sq) / (float)g.K + g.ln_eps);
+      if (lane == 0) {
+        ln_mu[r] = mean;
+        ln_rs[r] = inv;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      lnm[i] = ln_mu[xrow[i]];
+      lnr[i] = ln_rs[xrow[i]];
+    }
+  }
+  // N consecutive normalised X values of row block i from column k
+  // (layernorm_kernel's expression per element).
+  auto ln_vals = [&](int i, int k, float* out, auto NV) {
+#pragma clang fp contract(off)
+    constexpr int N = decltype(NV)::value;
+    const float* xr = g.ln_x + (int64_t)xrow[i] * g.ln_ldx + k;
+#pragma unroll
+    for (int h = 0; h < N / 4; ++h) {
+      const float4 xv = *(const float4*)(xr + 4 * h);
+      const float4 gv = *(const float4*)(g.ln_g + k + 4 * h);
+      const float4 bv = *(const float4*)(g.ln_b + k + 4 * h);
+      out[4 * h + 0] = (xv.x - lnm[i]) * lnr[i] * gv.x + bv.x;
+      out[4 * h + 1] = (xv.y - lnm[i]) * lnr[i] * gv.y + bv.y;
+      out[4 * h + 2] = (xv.z - lnm[i]) * lnr[i] * gv.z + bv.z;
+      out[4 * h + 3] = (xv.w - lnm[i]) * lnr[i] * gv.w + bv.w;
+    }
+  };
+  auto ln_bf16x8 = [&](int i, int k) {
+    float f[8];
+    ln_vals(i, k, f, std::integral_constant<int, 8>());
+    uint4 u;
+    u.x = pack_bf16x2(f[0], f[1]);
+    u.y = pack_bf16x2(f[2], f[3]);
+    u.z = pack_bf16x2(f[4], f[5]);
+    u.w = pack_bf16x2(f[6], f[7]);
+    return __builtin_bit_cast(bf16x8_t, u);
+  };
+
   if constexpr (F32) {
     const float* wp = (const float*)g.W + (int64_t)n * g.ldw + 4 * q;
     const float* xp[MB];
@@ -1198,7 +1284,15 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
       for (int u = 0; u < NU; ++u) {
         w[u] = *(const f32x4_t*)(wp + (kb + u) * KB);
 #pragma unroll
-        for (int i = 0; i < MB; ++i) x[u][i] = *(const f32x4_t*)(xp[i] + (kb + u) * KB);
+        for (int i = 0; i < MB; ++i) {
+          if constexpr (LN) {
+            float f[4];
+            ln_vals(i, (kb + u) * KB + 4 * q, f, std::integral_constant<int, 4>());
+            x[u][i] = f32x4_t{f[0], f[1], f[2], f[3]};
+          } else {
+            x[u][i] = *(const f32x4_t*)(xp[i] + (kb + u) * KB);
+          }
+        }
       }
 #pragma unroll
       for (int u = 0; u < NU; ++u)
@@ -1230,8 +1324,13 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
         wr[u] = *(const uint4*)(wp + (kb + u) * 64);
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
-          x[u][i][0] = *(const bf16x8_t*)(xp[i] + (kb + u) * 64);
-          x[u][i][1] = *(const bf16x8_t*)(xp[i] + (kb + u) * 64 + 8);
+          if constexpr (LN) {
+            x[u][i][0] = ln_bf16x8(i, (kb + u) * 64 + 16 * q);
+            x[u][i][1] = ln_bf16x8(i, (kb + u) * 64 + 16 * q + 8);
+          } else {
+            x[u][i][0] = *(const bf16x8_t*)(xp[i] + (kb + u) * 64);
+            x[u][i][1] = *(const bf16x8_t*)(xp[i] + (kb + u) * 64 + 8);
+          }
         }
       }
 #pragma unroll
@@ -1260,7 +1359,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
       for (int u = 0; u < NU; ++u) {
         w[u] = SkinnyW<WT>::load(wp + (kb + u) * KB);
 #pragma unroll
-        for (int i = 0; i < MB; ++i) x[u][i] = *(const bf16x8_t*)(xp[i] + (kb + u) * KB);
+        for (int i = 0; i < MB; ++i) {
+          if constexpr (LN) x[u][i] = ln_bf16x8(i, (kb + u) * KB + 8 * q);
+          else x[u][i] = *(const bf16x8_t*)(xp[i] + (kb + u) * KB);
+        }
       }
 #pragma unroll
       for (int u = 0; u < NU; ++u)
@@ -1371,12 +1473,18 @@ int top2_reduce(bool raw, const void* src, int n_parts, int64_t ld, int M, int* 
   return check_launch("cbis_gemm_argmax(reduce)");
 }
 
+template <typename XT, typename WT, bool LN>
+void launch_skinny_mb(const GemmArgs& g, hipStream_t s) {
+  const unsigned grid = (unsigned)cdiv(g.N, 16);
+  if (g.M <= 16) gemm_skinny_kernel<XT, WT, 1, LN><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
+  else if (g.M <= 32) gemm_skinny_kernel<XT, WT, 2, LN><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
+  else gemm_skinny_kernel<XT, WT, 4, LN><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
+}
+
 template <typename XT, typename WT>
 int launch_skinny(const GemmArgs& g, hipStream_t s) {
-  const unsigned grid = (unsigned)cdiv(g.N, 16);
-  if (g.M <= 16) gemm_skinny_kernel<XT, WT, 1><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
-  else if (g.M <= 32) gemm_skinny_kernel<XT, WT, 2><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
-  else gemm_skinny_kernel<XT, WT, 4><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
+  if (g.ln_x) launch_skinny_mb<XT, WT, true>(g, s);
+  else launch_skinny_mb<XT, WT, false>(g, s);
   return check_launch("cbis_gemm(skinny)");
 }
 
@@ -1562,7 +1670,24 @@ int argmax_tile_cols(const cbis_gemm_desc* d) {
 // are in the workspace partials and still need their reduce).  With amax the
 // kernel runs in greedy mode (no Y; never split): the caller checked that
 // argmax_tile_cols(d) > 0 and sized amax [M][cdiv(N, that)].
-int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax = nullptr) {
+// LayerNorm prologue arguments of cbis_layernorm_gemm.
+struct LnPrologue {
+  const float* x;
+  int64_t ldx;
+  const float* gamma;
+  const float* beta;
+  float eps;
+};
+
+// Whether d's GEMM runs on the skinny (decode-sized) kernel.
+bool skinny_path(const cbis_gemm_desc* d) {
+  const int we = d->w_dtype == CBIS_F32 ? 4 : (d->w_dtype == CBIS_BF16 ? 2 : 1);
+  const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * we) % 16 == 0;
+  return d->M <= kSkinnyMaxM && w_al && d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0;
+}
+
+int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax = nullptr,
+             const LnPrologue* ln = nullptr) {
   g.ksplit = 1;
   CBIS_REQUIRE(d, CBIS_ERR_INVALID, "cbis_gemm: null descriptor");
   CBIS_REQUIRE(d->M >= 0 && d->N > 0 && d->K > 0, CBIS_ERR_INVALID, "cbis_gemm: bad M/N/K %d/%d/%d", d->M, d->N, d->K);
@@ -1611,6 +1736,13 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax =
   g.partial = nullptr;
   g.amax = amax;
   g.amax_ld = amax ? (int)cdiv(d->N, argmax_tile_cols(d)) : 0;
+  g.ln_x = ln ? ln->x : nullptr;
+  g.ln_ldx = ln ? ln->ldx : 0;
+  g.ln_g = ln ? ln->gamma : nullptr;
+  g.ln_b = ln ? ln->beta : nullptr;
+  g.ln_eps = ln ? ln->eps : 0.f;
+  g.ln_nch = ln ? ln_chunks(d->K) : 0;
+  CBIS_REQUIRE(!ln || skinny_path(d), CBIS_ERR_UNSUPPORTED, "cbis_layernorm_gemm: LayerNorm prologue off the skinny path");
 
   // Decode-sized M: weight streaming (K a multiple of 32 for bf16 and fp32,
   // of 64 for fp8; W rows 16-byte aligned).
@@ -1733,6 +1865,28 @@ int cbis_gemm_layernorm(const cbis_gemm_desc* d, const float* ln_gamma, const fl
 #undef CBIS_SKLN_KS
 #undef CBIS_SKLN
   return check_launch("cbis_gemm_layernorm(split-k reduce + layernorm)");
+}
+
+int cbis_layernorm_gemm(const cbis_gemm_desc* d, const float* x, int64_t ldx, const float* ln_gamma,
+                        const float* ln_beta, float eps, cbis_stream_t stream) {
+  const char* who = "cbis_layernorm_gemm";
+  CBIS_REQUIRE(d, CBIS_ERR_INVALID, "%s: null descriptor", who);
+  CBIS_REQUIRE(x && ln_gamma && ln_beta && d->X, CBIS_ERR_INVALID, "%s: null x / LayerNorm / X pointer", who);
+  CBIS_REQUIRE(d->x_dtype == CBIS_F32 || d->x_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: x dtype", who);
+  CBIS_REQUIRE(ldx >= d->K, CBIS_ERR_INVALID, "%s: ldx %lld < K %d", who, (long long)ldx, d->K);
+  if (d->M == 0) return CBIS_OK;
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const bool fuse = skinny_path(d) && d->K % 4 == 0 && d->K <= kLnPrologueMaxK && a16(x) && ldx % 4 == 0 &&
+                    a16(ln_gamma) && a16(ln_beta);
+  if (!fuse) {
+    const int rc = cbis_layernorm(d->M, d->K, x, ldx, ln_gamma, ln_beta, eps, d->x_dtype, (void*)d->X, d->ldx, stream);
+    if (rc) return rc;
+    return cbis_gemm(d, stream);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  GemmArgs g;
+  const LnPrologue ln = {x, ldx, ln_gamma, ln_beta, eps};
+  return gemm_run(d, s, g, nullptr, &ln);
 }
 
 size_t cbis_gemm_argmax_workspace_size(const cbis_gemm_desc* d) {

@@ -274,8 +274,14 @@ void TransformerRunner::enqueue_forward(bool greedy) {
 
   // LayerNorms that follow a residual GEMM (ln2 after the out-projection,
   // the next layer's ln1 or ln_f after fc2) run with it (cbis_gemm_layernorm:
-  // fused with fc2's split-K reduce).
-  cbis_check(cbis_layernorm(M, D, d_x_, D, w_.layers[0].ln1_w, w_.layers[0].ln1_b, 1e-5f, act, d_xn_, D, s), "ln1");
+  // fused with fc2's split-K reduce).  Decode-sized steps instead hand ln1
+  // and ln2 to the QKV and fc1 GEMMs that read them (cbis_layernorm_gemm:
+  // same values; for short rows formed inside the GEMM, two launches fewer
+  // per layer).
+  const bool ln_pro = M <= 64;
+  if (!ln_pro)
+    cbis_check(cbis_layernorm(M, D, d_x_, D, w_.layers[0].ln1_w, w_.layers[0].ln1_b, 1e-5f, act, d_xn_, D, s),
+               "ln1");
   for (int l = 0; l < cfg_.n_layers; ++l) {
     const LayerWeights& L = w_.layers[l];
     // QKV projection; K and V columns go straight to their page slots.
@@ -289,7 +295,8 @@ void TransformerRunner::enqueue_forward(bool greedy) {
     g.kv_col0 = D; g.kv_width = D; g.kv_dtype = cfg_.kv_dtype; g.page_size = cfg_.page_size;
     g.k_pool = cache_.k_base(l); g.v_pool = cache_.v_base(l);
     g.write_page = d_wpage_; g.write_offset = d_woff_;
-    cbis_check(cbis_gemm(&g, s), "qkv gemm");
+    if (ln_pro) cbis_check(cbis_layernorm_gemm(&g, d_x_, D, L.ln1_w, L.ln1_b, 1e-5f, s), "ln1 + qkv gemm");
+    else cbis_check(cbis_gemm(&g, s), "qkv gemm");
     a.k_pool = cache_.k_base(l);
     a.v_pool = cache_.v_base(l);
     // Single rows on the split-KV decode kernel, runs of rows on the MFMA
@@ -305,7 +312,8 @@ void TransformerRunner::enqueue_forward(bool greedy) {
     g.w_dtype = wd; g.W = L.wo; g.ldw = D; g.w_scale = L.so;
     g.bias = L.bo; g.residual = d_x_; g.ldr = D;
     g.y_dtype = CBIS_F32; g.Y = d_x_; g.ldy = D;
-    cbis_check(cbis_gemm_layernorm(&g, L.ln2_w, L.ln2_b, 1e-5f, act, d_xn_, D, s), "out-proj gemm + ln2");
+    if (ln_pro) cbis_check(cbis_gemm(&g, s), "out-proj gemm");
+    else cbis_check(cbis_gemm_layernorm(&g, L.ln2_w, L.ln2_b, 1e-5f, act, d_xn_, D, s), "out-proj gemm + ln2");
     g = cbis_gemm_desc{};
     g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
     g.M = M; g.N = F; g.K = D;
@@ -313,7 +321,8 @@ void TransformerRunner::enqueue_forward(bool greedy) {
     g.w_dtype = wd; g.W = L.w1; g.ldw = D; g.w_scale = L.s1;
     g.bias = L.b1; g.epilogue = CBIS_EPI_GELU;
     g.y_dtype = act; g.Y = d_h_; g.ldy = F;
-    cbis_check(cbis_gemm(&g, s), "fc1 gemm");
+    if (ln_pro) cbis_check(cbis_layernorm_gemm(&g, d_x_, D, L.ln2_w, L.ln2_b, 1e-5f, s), "ln2 + fc1 gemm");
+    else cbis_check(cbis_gemm(&g, s), "fc1 gemm");
     g = cbis_gemm_desc{};
     g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
     g.M = M; g.N = D; g.K = F;
@@ -324,7 +333,9 @@ void TransformerRunner::enqueue_forward(bool greedy) {
     const bool last = l + 1 == cfg_.n_layers;
     const float* nw = last ? w_.ln_f_w : w_.layers[l + 1].ln1_w;
     const float* nb = last ? w_.ln_f_b : w_.layers[l + 1].ln1_b;
-    cbis_check(cbis_gemm_layernorm(&g, nw, nb, 1e-5f, act, d_xn_, D, s), last ? "fc2 gemm + ln_f" : "fc2 gemm + ln1");
+    if (ln_pro && !last) cbis_check(cbis_gemm(&g, s), "fc2 gemm");
+    else
+      cbis_check(cbis_gemm_layernorm(&g, nw, nb, 1e-5f, act, d_xn_, D, s), last ? "fc2 gemm + ln_f" : "fc2 gemm + ln1");
   }
   g = cbis_gemm_desc{};
   g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;

@@ -252,6 +252,17 @@ int cbis_embed(int T, int d_model, const int* token_ids, const int* positions, i
 int cbis_layernorm(int T, int d_model, const float* X, int64_t ldx, const float* gamma, const float* beta,
                    float eps, int y_dtype, void* Y, int64_t ldy, cbis_stream_t stream);
 
+/* Y = LayerNorm(x) . W^T with d's epilogue: cbis_layernorm of x [M, K] (fp32,
+ * row stride ldx; gamma, beta [K]) into d->X as d->x_dtype, then cbis_gemm(d),
+ * the layernorm_forward + linear_forward of src/transformer.cpp:69-72 (and
+ * :84-85) in one call.  Decode-sized calls with short rows (the skinny path:
+ * M <= 64; K <= 512; x, gamma, beta 16-byte aligned, ldx % 4 == 0) form the
+ * normalised rows inside the GEMM instead (one launch, X not written); both
+ * ways give the same Y bit for bit.  d->X must be a [M, K] buffer of
+ * d->x_dtype (row stride d->ldx). */
+int cbis_layernorm_gemm(const cbis_gemm_desc* d, const float* x, int64_t ldx, const float* ln_gamma,
+                        const float* ln_beta, float eps, cbis_stream_t stream);
+
 /* out[r] = first index of the maximum of logits[r, 0:N] (strict >), the
  * greedy rule of src/bench_batching.cpp:66-73. */
 int cbis_argmax_rows(int T, int N, const float* logits, int64_t ld, int* out, cbis_stream_t stream);

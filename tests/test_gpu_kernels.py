@@ -270,6 +270,57 @@ def test_gemm_layernorm_matches_gemm_then_layernorm(cbis, oracle, dev, M, N, K, 
     assert np.array_equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("wdt", ["f32", "bf16", "fp8"])
+@pytest.mark.parametrize("M,K", [(1, 256), (8, 256), (33, 512), (64, 512), (16, 2048), (100, 256), (8, 4096)])
+def test_layernorm_gemm_matches_layernorm_then_gemm(cbis, oracle, dev, M, K, wdt):
+    """cbis_layernorm_gemm (Y = LayerNorm(x) . W^T + b, GELU) against
+    cbis_layernorm into X followed by cbis_gemm: bit-identical Y.  Decode-sized
+    calls with short rows (M <= 64, K <= 512) form the normalised rows inside
+    the skinny GEMM (X is then left untouched); M = 100 and K = 2048 / 4096
+    take the two-kernel path."""
+    import torch
+    N = 200
+    x = oracle.normal(23, 1, M * K).reshape(M, K) * 2.0 + 0.5
+    gam = to_dev(1.0 + oracle.normal(23, 5, K, 0.1), dev)
+    bet = to_dev(oracle.normal(23, 6, K, 0.1), dev)
+    b = to_dev(oracle.normal(23, 3, N, 0.02), dev)
+    w = oracle.normal(23, 2, N * K, 0.02).reshape(N, K)
+    xd = to_dev(x, dev)
+    if wdt == "f32":
+        W, S, xdt, wd = to_dev(w, dev), None, cbis.F32, cbis.F32
+    elif wdt == "bf16":
+        (W, _), S, xdt, wd = bf16_dev(w, dev), None, cbis.BF16, cbis.BF16
+    else:
+        codes, sc = oracle.quantize_e4m3_rows(w)
+        W, S, xdt, wd = to_dev(codes, dev), to_dev(sc, dev), cbis.BF16, cbis.FP8E4M3
+    tdt = torch.float32 if xdt == cbis.F32 else torch.bfloat16
+    outs = []
+    for fused in (True, False):
+        Xbuf = torch.full((M, K), 7.0, dtype=tdt, device=dev)
+        Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        d = cbis.GemmDesc()
+        d.M, d.N, d.K = M, N, K
+        d.x_dtype, d.X, d.ldx = xdt, ptr(Xbuf), K
+        d.w_dtype, d.W, d.ldw = wd, ptr(W), K
+        d.w_scale, d.bias = ptr(S), ptr(b)
+        d.epilogue = cbis.EPI_GELU
+        d.y_dtype, d.Y, d.ldy = cbis.F32, ptr(Y), N
+        if fused:
+            cbis.check(cbis.kernels().cbis_layernorm_gemm(ctypes.byref(d), ptr(xd), K, ptr(gam), ptr(bet), 1e-5,
+                                                           stream()), "cbis_layernorm_gemm")
+        else:
+            cbis.check(cbis.kernels().cbis_layernorm(M, K, ptr(xd), K, ptr(gam), ptr(bet), 1e-5, xdt, ptr(Xbuf), K,
+                                                     stream()), "cbis_layernorm")
+            cbis.check(cbis.kernels().cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
+        sync()
+        outs.append(Y.cpu().numpy().view(np.uint32))
+        if fused:
+            # the prologue path leaves X untouched; the two-kernel path writes LayerNorm(x) there
+            untouched = bool((Xbuf.float() == 7.0).all())
+            assert untouched == (M <= 64 and K <= 512), (M, K)
+    assert np.array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("M", [16, 200])
 def test_gemm_fp8_weights(cbis, oracle, dev, M):
     import torch
