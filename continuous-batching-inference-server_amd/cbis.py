@@ -95,6 +95,7 @@ KERNEL_SYMBOLS = {
     "cbis_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "cbis_gemm_argmax_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "cbis_gemm_argmax": (_I, [ctypes.POINTER(GemmDesc), _P, _P, _P, _SZ, _P]),
+    "cbis_layernorm_gemm_argmax": (_I, [ctypes.POINTER(GemmDesc), _P, _I64, _P, _P, _F, _P, _P, _P, _SZ, _P]),
     "cbis_paged_attention_workspace_size": (_SZ, [ctypes.POINTER(AttnDesc)]),
     "cbis_paged_attention": (_I, [ctypes.POINTER(AttnDesc), _P]),
     "cbis_paged_attention_static": (_I, [ctypes.POINTER(AttnDesc), _P]),

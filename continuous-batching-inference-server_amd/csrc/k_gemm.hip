@@ -1686,6 +1686,13 @@ bool skinny_path(const cbis_gemm_desc* d) {
   return d->M <= kSkinnyMaxM && w_al && d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0;
 }
 
+// Whether cbis_layernorm_gemm(_argmax) forms d's LayerNorm inside the GEMM.
+bool ln_prologue_ok(const cbis_gemm_desc* d, const float* x, int64_t ldx, const float* gamma, const float* beta) {
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  return skinny_path(d) && d->K % 4 == 0 && d->K <= kLnPrologueMaxK && a16(x) && ldx % 4 == 0 && a16(gamma) &&
+         a16(beta);
+}
+
 int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax = nullptr,
              const LnPrologue* ln = nullptr) {
   g.ksplit = 1;
@@ -1800,6 +1807,42 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax =
   return dispatch<uint16_t, uint8_t>(g, s);
 }
 
+int gemm_argmax(const cbis_gemm_desc* d, int* next_token, float* margin, void* workspace, size_t workspace_bytes,
+                hipStream_t s, const LnPrologue* ln, const char* who) {
+  CBIS_REQUIRE(d, CBIS_ERR_INVALID, "%s: null descriptor", who);
+  CBIS_REQUIRE(d->epilogue == CBIS_EPI_NONE && !d->residual && !d->k_pool, CBIS_ERR_INVALID,
+               "%s: the greedy epilogue takes the scale and bias only (no GELU, residual or K/V scatter)", who);
+  CBIS_REQUIRE(next_token, CBIS_ERR_INVALID, "%s: null next_token", who);
+  if (d->M == 0) return CBIS_OK;
+  const size_t need = cbis_gemm_argmax_workspace_size(d);
+  CBIS_REQUIRE(workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15u) == 0, CBIS_ERR_WORKSPACE,
+               "%s: workspace %zu bytes (16-byte aligned), need %zu", who, workspace_bytes, need);
+  const int cols = argmax_tile_cols(d);
+  if (cols > 0) {
+    GemmArgs g;
+    const int rc = gemm_run(d, s, g, (float4*)workspace, ln);
+    if (rc) return rc;
+    return top2_reduce(false, workspace, g.amax_ld, g.amax_ld, d->M, next_token, margin, s);
+  }
+  // Paths without a greedy epilogue: the logits into d->Y (when it is an fp32
+  // [M, N] buffer) or the workspace, then the same reduce over them.
+  cbis_gemm_desc e = *d;
+  const bool y_given = d->Y && d->y_dtype == CBIS_F32 && d->ldy >= d->N;
+  const size_t lg = y_given ? 0 : (size_t)d->M * d->N * sizeof(float);
+  if (!y_given) {
+    e.y_dtype = CBIS_F32;
+    e.Y = workspace;
+    e.ldy = d->N;
+  }
+  e.workspace = (char*)workspace + lg;
+  e.workspace_bytes = workspace_bytes - lg;
+  CBIS_REQUIRE(!ln, CBIS_ERR_UNSUPPORTED, "%s: LayerNorm prologue on a path that stores logits", who);
+  const int rc = cbis_gemm(&e, (cbis_stream_t)s);
+  if (rc) return rc;
+  return top2_reduce(true, e.Y, d->N, e.ldy, d->M, next_token, margin, s);
+}
+
+
 int splitk_reduce(const GemmArgs& g, hipStream_t s) {
   splitk_reduce_kernel<<<splitk_reduce_blocks(g), 256, 0, s>>>(g);
   return check_launch("cbis_gemm(split-k reduce)");
@@ -1875,10 +1918,7 @@ int cbis_layernorm_gemm(const cbis_gemm_desc* d, const float* x, int64_t ldx, co
   CBIS_REQUIRE(d->x_dtype == CBIS_F32 || d->x_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: x dtype", who);
   CBIS_REQUIRE(ldx >= d->K, CBIS_ERR_INVALID, "%s: ldx %lld < K %d", who, (long long)ldx, d->K);
   if (d->M == 0) return CBIS_OK;
-  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-  const bool fuse = skinny_path(d) && d->K % 4 == 0 && d->K <= kLnPrologueMaxK && a16(x) && ldx % 4 == 0 &&
-                    a16(ln_gamma) && a16(ln_beta);
-  if (!fuse) {
+  if (!ln_prologue_ok(d, x, ldx, ln_gamma, ln_beta)) {
     const int rc = cbis_layernorm(d->M, d->K, x, ldx, ln_gamma, ln_beta, eps, d->x_dtype, (void*)d->X, d->ldx, stream);
     if (rc) return rc;
     return cbis_gemm(d, stream);
@@ -1900,38 +1940,26 @@ size_t cbis_gemm_argmax_workspace_size(const cbis_gemm_desc* d) {
 
 int cbis_gemm_argmax(const cbis_gemm_desc* d, int* next_token, float* margin, void* workspace,
                      size_t workspace_bytes, cbis_stream_t stream) {
-  const char* who = "cbis_gemm_argmax";
+  return gemm_argmax(d, next_token, margin, workspace, workspace_bytes, (hipStream_t)stream, nullptr,
+                     "cbis_gemm_argmax");
+}
+
+int cbis_layernorm_gemm_argmax(const cbis_gemm_desc* d, const float* x, int64_t ldx, const float* ln_gamma,
+                               const float* ln_beta, float eps, int* next_token, float* margin, void* workspace,
+                               size_t workspace_bytes, cbis_stream_t stream) {
+  const char* who = "cbis_layernorm_gemm_argmax";
   CBIS_REQUIRE(d, CBIS_ERR_INVALID, "%s: null descriptor", who);
-  CBIS_REQUIRE(d->epilogue == CBIS_EPI_NONE && !d->residual && !d->k_pool, CBIS_ERR_INVALID,
-               "%s: the greedy epilogue takes the scale and bias only (no GELU, residual or K/V scatter)", who);
-  CBIS_REQUIRE(next_token, CBIS_ERR_INVALID, "%s: null next_token", who);
+  CBIS_REQUIRE(x && ln_gamma && ln_beta && d->X, CBIS_ERR_INVALID, "%s: null x / LayerNorm / X pointer", who);
+  CBIS_REQUIRE(d->x_dtype == CBIS_F32 || d->x_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: x dtype", who);
+  CBIS_REQUIRE(ldx >= d->K, CBIS_ERR_INVALID, "%s: ldx %lld < K %d", who, (long long)ldx, d->K);
   if (d->M == 0) return CBIS_OK;
-  const size_t need = cbis_gemm_argmax_workspace_size(d);
-  CBIS_REQUIRE(workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15u) == 0, CBIS_ERR_WORKSPACE,
-               "%s: workspace %zu bytes (16-byte aligned), need %zu", who, workspace_bytes, need);
-  hipStream_t s = (hipStream_t)stream;
-  const int cols = argmax_tile_cols(d);
-  if (cols > 0) {
-    GemmArgs g;
-    const int rc = gemm_run(d, s, g, (float4*)workspace);
+  if (!ln_prologue_ok(d, x, ldx, ln_gamma, ln_beta)) {
+    const int rc = cbis_layernorm(d->M, d->K, x, ldx, ln_gamma, ln_beta, eps, d->x_dtype, (void*)d->X, d->ldx, stream);
     if (rc) return rc;
-    return top2_reduce(false, workspace, g.amax_ld, g.amax_ld, d->M, next_token, margin, s);
+    return cbis_gemm_argmax(d, next_token, margin, workspace, workspace_bytes, stream);
   }
-  // Paths without a greedy epilogue: the logits into d->Y (when it is an fp32
-  // [M, N] buffer) or the workspace, then the same reduce over them.
-  cbis_gemm_desc e = *d;
-  const bool y_given = d->Y && d->y_dtype == CBIS_F32 && d->ldy >= d->N;
-  const size_t lg = y_given ? 0 : (size_t)d->M * d->N * sizeof(float);
-  if (!y_given) {
-    e.y_dtype = CBIS_F32;
-    e.Y = workspace;
-    e.ldy = d->N;
-  }
-  e.workspace = (char*)workspace + lg;
-  e.workspace_bytes = workspace_bytes - lg;
-  const int rc = cbis_gemm(&e, stream);
-  if (rc) return rc;
-  return top2_reduce(true, e.Y, d->N, e.ldy, d->M, next_token, margin, s);
+  const LnPrologue ln = {x, ldx, ln_gamma, ln_beta, eps};
+  return gemm_argmax(d, next_token, margin, workspace, workspace_bytes, (hipStream_t)stream, &ln, who);
 }
 
 size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {

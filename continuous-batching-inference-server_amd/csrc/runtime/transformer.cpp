@@ -333,7 +333,7 @@ void TransformerRunner::enqueue_forward(bool greedy) {
     const bool last = l + 1 == cfg_.n_layers;
     const float* nw = last ? w_.ln_f_w : w_.layers[l + 1].ln1_w;
     const float* nb = last ? w_.ln_f_b : w_.layers[l + 1].ln1_b;
-    if (ln_pro && !last) cbis_check(cbis_gemm(&g, s), "fc2 gemm");
+    if (ln_pro) cbis_check(cbis_gemm(&g, s), "fc2 gemm");
     else
       cbis_check(cbis_gemm_layernorm(&g, nw, nb, 1e-5f, act, d_xn_, D, s), last ? "fc2 gemm + ln_f" : "fc2 gemm + ln1");
   }
@@ -343,9 +343,15 @@ void TransformerRunner::enqueue_forward(bool greedy) {
   g.x_dtype = act; g.X = d_xn_; g.ldx = D;
   g.w_dtype = wd; g.W = w_.lm_head; g.ldw = D; g.w_scale = w_.lm_scale;
   g.y_dtype = CBIS_F32; g.Y = d_logits_; g.ldy = V;
-  if (greedy)
-    cbis_check(cbis_gemm_argmax(&g, d_next_, (float*)(d_next_ + M), d_amax_ws_, amax_ws_bytes_, s),
-               "lm_head gemm + argmax");
+  float* margins = (float*)(d_next_ + M);
+  if (ln_pro && greedy)
+    cbis_check(cbis_layernorm_gemm_argmax(&g, d_x_, D, w_.ln_f_w, w_.ln_f_b, 1e-5f, d_next_, margins, d_amax_ws_,
+                                          amax_ws_bytes_, s),
+               "ln_f + lm_head gemm + argmax");
+  else if (ln_pro)
+    cbis_check(cbis_layernorm_gemm(&g, d_x_, D, w_.ln_f_w, w_.ln_f_b, 1e-5f, s), "ln_f + lm_head gemm");
+  else if (greedy)
+    cbis_check(cbis_gemm_argmax(&g, d_next_, margins, d_amax_ws_, amax_ws_bytes_, s), "lm_head gemm + argmax");
   else
     cbis_check(cbis_gemm(&g, s), "lm_head gemm");
 }

@@ -166,6 +166,15 @@ size_t cbis_gemm_argmax_workspace_size(const cbis_gemm_desc* d);
 int cbis_gemm_argmax(const cbis_gemm_desc* d, int* next_token, float* margin, void* workspace,
                      size_t workspace_bytes, cbis_stream_t stream);
 
+/* cbis_gemm_argmax of LayerNorm(x): the final layernorm_forward + lm_head +
+ * argmax of src/transformer.cpp:92-93 and src/bench_batching.cpp:66-73 in one
+ * call, with cbis_layernorm_gemm's rule for where the LayerNorm runs (inside
+ * the skinny GEMM for M <= 64 and K <= 512, else cbis_layernorm into d->X
+ * first); tokens and margins as cbis_gemm_argmax's, bit for bit. */
+int cbis_layernorm_gemm_argmax(const cbis_gemm_desc* d, const float* x, int64_t ldx, const float* ln_gamma,
+                               const float* ln_beta, float eps, int* next_token, float* margin, void* workspace,
+                               size_t workspace_bytes, cbis_stream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* Paged attention.                                                          */
 /* ----------------------------------------------------------------------- */

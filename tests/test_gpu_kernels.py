@@ -321,6 +321,56 @@ def test_layernorm_gemm_matches_layernorm_then_gemm(cbis, oracle, dev, M, K, wdt
     assert np.array_equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("wdt", ["f32", "bf16", "fp8"])
+@pytest.mark.parametrize("M,K", [(8, 256), (64, 512), (16, 2048), (100, 256)])
+def test_layernorm_gemm_argmax_matches_layernorm_then_argmax(cbis, oracle, dev, M, K, wdt):
+    """cbis_layernorm_gemm_argmax against cbis_layernorm into X followed by
+    cbis_gemm_argmax: identical tokens and bit-identical margins, whether the
+    LayerNorm runs inside the skinny GEMM (M <= 64, K <= 512) or before it."""
+    import torch
+    K_ = cbis.kernels()
+    N = 1000
+    x = oracle.normal(29, 1, M * K).reshape(M, K) * 1.5 - 0.25
+    gam = to_dev(1.0 + oracle.normal(29, 5, K, 0.1), dev)
+    bet = to_dev(oracle.normal(29, 6, K, 0.1), dev)
+    w = oracle.normal(29, 2, N * K, 0.02).reshape(N, K)
+    b = to_dev(oracle.normal(29, 3, N, 0.02), dev)
+    xd = to_dev(x, dev)
+    if wdt == "f32":
+        W, S, xdt, wd = to_dev(w, dev), None, cbis.F32, cbis.F32
+    elif wdt == "bf16":
+        (W, _), S, xdt, wd = bf16_dev(w, dev), None, cbis.BF16, cbis.BF16
+    else:
+        codes, sc = oracle.quantize_e4m3_rows(w)
+        W, S, xdt, wd = to_dev(codes, dev), to_dev(sc, dev), cbis.BF16, cbis.FP8E4M3
+    tdt = torch.float32 if xdt == cbis.F32 else torch.bfloat16
+    res = []
+    for fused in (True, False):
+        Xbuf = torch.zeros((M, K), dtype=tdt, device=dev)
+        d = cbis.GemmDesc()
+        d.M, d.N, d.K = M, N, K
+        d.x_dtype, d.X, d.ldx = xdt, ptr(Xbuf), K
+        d.w_dtype, d.W, d.ldw = wd, ptr(W), K
+        d.w_scale, d.bias = ptr(S), ptr(b)
+        need = K_.cbis_gemm_argmax_workspace_size(ctypes.byref(d))
+        ws = torch.empty(max(4, need // 4), dtype=torch.float32, device=dev)
+        nxt = torch.full((M,), -1, dtype=torch.int32, device=dev)
+        mar = torch.full((M,), -1.0, dtype=torch.float32, device=dev)
+        if fused:
+            cbis.check(K_.cbis_layernorm_gemm_argmax(ctypes.byref(d), ptr(xd), K, ptr(gam), ptr(bet), 1e-5, ptr(nxt),
+                                                     ptr(mar), ptr(ws), need, stream()), "cbis_layernorm_gemm_argmax")
+        else:
+            cbis.check(K_.cbis_layernorm(M, K, ptr(xd), K, ptr(gam), ptr(bet), 1e-5, xdt, ptr(Xbuf), K, stream()),
+                       "cbis_layernorm")
+            cbis.check(K_.cbis_gemm_argmax(ctypes.byref(d), ptr(nxt), ptr(mar), ptr(ws), need, stream()),
+                       "cbis_gemm_argmax")
+        sync()
+        res.append((nxt.cpu().numpy(), mar.cpu().numpy().view(np.uint32)))
+    assert np.array_equal(res[0][0], res[1][0])
+    assert np.array_equal(res[0][1], res[1][1])
+    assert (res[0][0] >= 0).all() and (res[0][0] < N).all()
+
+
 @pytest.mark.parametrize("M", [16, 200])
 def test_gemm_fp8_weights(cbis, oracle, dev, M):
     import torch
