@@ -170,86 +170,6 @@ __device__ inline void epilogue_store(const GemmArgs& g, int row, int col, float
   else ((float*)g.Y)[o] = v;
 }
 
-// Epilogue of one 32 x 32 MFMA block: this lane holds column `col` of rows
-// rb + 8 * (e / 4) + (e % 4), e = 0..15, handled four rows at a time.  The
-// four rows' inputs (residual, K/V slot ids) are loaded before their stores:
-// Y may alias the residual (x += ...), so loads interleaved with stores
-// would be issued one round trip at a time.  The channel scale and bias are
-// loaded once.  With ksplit > 1 the raw sums go to the partials.
-__device__ inline void epilogue_block(const GemmArgs& g, int kz, int rb, int col, const f32x16_t& acc) {
-  if (col >= g.N) return;
-  const float sc = g.w_scale ? g.w_scale[col] : 1.f;
-  const float bi = g.bias ? g.bias[col] : 0.f;
-  const bool kv = g.k_pool && col >= g.kv_col0;
-  const int c = col - g.kv_col0;
-  const bool is_v = kv && c >= g.kv_width;
-  const int ce = is_v ? c - g.kv_width : c;
-  void* pool = is_v ? g.v_pool : g.k_pool;
-  // Column pairs (2i, 2i+1) stay together (both < N, same K/V half, 4-byte
-  // aligned destinations) when these are all even.
-  const bool pair_ok = ((g.N | g.ldy) & 1) == 0 && (!g.k_pool || ((g.kv_col0 | g.kv_width) & 1) == 0) &&
-                       (((uintptr_t)g.Y | (uintptr_t)g.k_pool | (uintptr_t)g.v_pool) & 3) == 0;
-#pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    const int r0 = rb + 8 * qd;
-    bool ok[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) ok[e] = r0 + e < g.M;
-    if (g.ksplit > 1) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (ok[e]) g.partial[((int64_t)kz * g.M + r0 + e) * g.N + col] = acc[4 * qd + e];
-      continue;
-    }
-    float v[4], r[4];
-    int64_t off[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      r[e] = (g.residual && ok[e]) ? g.residual[(int64_t)(r0 + e) * g.ldr + col] : 0.f;
-      off[e] = (kv && ok[e]) ? ((int64_t)g.wpage[r0 + e] * g.page_size + g.woff[r0 + e]) * g.kv_width + ce : 0;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = acc[4 * qd + e];
-      if (g.w_scale) v[e] *= sc;
-      if (g.bias) v[e] += bi;
-      if (g.gelu) v[e] = gelu_erf(v[e]);
-      if (g.residual) v[e] += r[e];
-    }
-    const bool bf16_out = kv ? g.kv_bf16 : g.y_bf16;
-    if (bf16_out && pair_ok) {
-      // Lanes 2i and 2i+1 hold adjacent columns: trade values so the even
-      // lane stores rows r0, r0+1 and the odd lane rows r0+2, r0+3 of both
-      // columns as 4-byte bf16 pairs (half the store instructions).
-      const int odd = col & 1;
-      float nb[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) nb[e] = __shfl_xor(v[e], 1, 64);
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int e = 2 * odd + k;
-        if (!ok[e]) continue;
-        const uint32_t w = odd ? pack_bf16x2(nb[e], v[e]) : pack_bf16x2(v[e], nb[e]);
-        if (kv) *(uint32_t*)((uint16_t*)pool + off[e] - odd) = w;
-        else *(uint32_t*)((uint16_t*)g.Y + (int64_t)(r0 + e) * g.ldy + col - odd) = w;
-      }
-      continue;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (!ok[e]) continue;
-      if (kv) {
-        if (g.kv_bf16) ((uint16_t*)pool)[off[e]] = f32_to_bf16(v[e]);
-        else ((float*)pool)[off[e]] = v[e];
-      } else {
-        const int64_t o = (int64_t)(r0 + e) * g.ldy + col;
-        if (g.y_bf16) ((uint16_t*)g.Y)[o] = f32_to_bf16(v[e]);
-        else ((float*)g.Y)[o] = v[e];
-      }
-    }
-  }
-}
-
 template <typename WT>
 struct WLoad;  // global W chunk (covering 16 bytes of LDS) -> uint4 of the compute type
 template <>
@@ -297,6 +217,13 @@ __device__ inline int xcd_contiguous(int bid, int nwg) {
 // 128-255 of the 64 banks, each set in 8 distinct slots: no bank conflicts.
 __device__ inline int swz_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 __device__ inline int swz(int row, int chunk) { return row * 128 + (swz_slot(row, chunk) << 4); }
+
+template <int BM, int BN, int WM, int WN, int FM, int FN>
+__device__ inline void epilogue_parked(const GemmArgs& g, int kz, uint8_t* smem, const f32x16_t (&acc)[FM][FN],
+                                       int m0, int n0);
+// LDS bytes epilogue_parked needs for a BM x BN tile.
+template <int BM, int BN>
+constexpr int parked_bytes() { return BM * (BN + 8) * 4; }
 
 template <int BM, int BN, int WM, int WN, typename XT, typename WT>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
@@ -422,20 +349,19 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
     __syncthreads();
   }
 
-  // Epilogue straight from the accumulators: acc[i][j][e] is row
-  // 8*(e/4) + 4*half + (e%4), column l32 of block (i, j).
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-      epilogue_block(g, kz, m0 + wm * TM + i * 32 + 4 * half, n0 + wn * TN + j * 32 + l32, acc[i][j]);
+  epilogue_parked<BM, BN, WM, WN>(g, kz, smem, acc, m0, n0);
 }
 
 // Epilogue of the 4 consecutive output columns col..col+3 (fewer at the
 // right edge) handled by one thread: the per-column constants once, then per
 // row the inputs (residual, K/V slot) and the finished store.  One 16-byte
 // (fp32) or 8-byte (bf16) store when the 4 columns share a destination and
-// its alignment allows, else element by element like epilogue_store.
+// its alignment allows, else element by element like epilogue_store.  The
+// wide output stores carry the nontemporal hint: every output line is written
+// once, by one workgroup, and is read (if at all) by a later kernel (on
+// config 2's bf16 M = 4096 shapes 16-byte stores alone gained 11-21%, with
+// the hint 30-37%).  Split-K partials, read back right away by the reduce,
+// are stored plainly.
 struct Cols4 {
   int col, nc;
   float sc[4], bi[4];
@@ -522,8 +448,13 @@ struct Cols4 {
     const bool bf = to_kv ? g.kv_bf16 : g.y_bf16;
     void* dst = to_kv ? (void*)((char*)pool + (slot * g.kv_width + ce) * (bf ? 2 : 4))
                       : (void*)((char*)g.Y + ((int64_t)row * g.ldy + col) * (bf ? 2 : 4));
-    if (bf) *(uint2*)dst = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-    else *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+    if (bf) {
+      const u32x2_t w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      __builtin_nontemporal_store(w, (u32x2_t*)dst);
+    } else {
+      const f32x4_t w = {v[0], v[1], v[2], v[3]};
+      __builtin_nontemporal_store(w, (f32x4_t*)dst);
+    }
   }
 
   // Raw sums to split kz's partials.
@@ -676,7 +607,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmAr
   static_assert(LPW * NWAVES == GROUPS && BM % 8 == 0 && BN % 8 == 0, "tile / wave mismatch");
   static_assert(LPW * (STAGES - 1) < 64, "vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
+  constexpr int RING = STAGES * STAGE_BYTES;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[RING > parked_bytes<BM, BN>() ? RING : parked_bytes<BM, BN>()];
 
   const int mt = (g.M + BM - 1) / BM;
   const int nwg = gridDim.x;
@@ -792,11 +724,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmAr
     }
   }
 
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-      epilogue_block(g, kz, m0 + wm * TM + i * 32 + 4 * half, n0 + wn * TN + j * 32 + l32, acc[i][j]);
+  epilogue_parked<BM, BN, WM, WN>(g, kz, smem, acc, m0, n0);
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES>
@@ -892,6 +820,36 @@ __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* til
       else c.finish(g, row, v[q], r[q], slot[q]);
     }
   }
+}
+
+// Epilogue of the single-role kernels (gemm_kernel, gemm_bf16_dma_kernel):
+// every wave parks its accumulators in LDS as one row-major fp32 tile
+// (pitch BN + 8: the two row halves of a 32 x 32 block, 4 rows apart, land
+// in opposite halves of the 64 banks) and the whole workgroup runs
+// epilogue_rows over it.  Stored straight from the MFMA layout, a wave's
+// store instruction covers 2 rows x 128 bytes (4 bytes a lane); from the
+// parked tile it covers 4-8 rows x 256-512 bytes (16 bytes a lane), a
+// quarter of the instructions for the same bytes.  smem needs
+// BM * (BN + 8) * 4 bytes; the caller's K loop must be done with it.
+template <int BM, int BN, int WM, int WN, int FM, int FN>
+__device__ inline void epilogue_parked(const GemmArgs& g, int kz, uint8_t* smem, const f32x16_t (&acc)[FM][FN],
+                                       int m0, int n0) {
+  constexpr int TM = BM / WM, TN = BN / WN, PITCH = BN + 8;
+  static_assert(FM * 32 == TM && FN * 32 == TN, "accumulator blocks");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int half = lane >> 5, l32 = lane & 31;
+  float* tile = (float*)smem;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        tile[(wm * TM + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3)) * PITCH + wn * TN + j * 32 + l32] = acc[i][j][e];
+  __syncthreads();
+  epilogue_rows<BM, BN, WM * WN * 64>(g, kz, tile, PITCH, m0, n0, tid);
 }
 
 // Greedy-mode epilogue over a parked BM x BN fp32 tile: each 16-lane row of
@@ -1584,7 +1542,7 @@ bool dma_eligible(const cbis_gemm_desc* d) {
 template <int BM, int BN, int WM, int WN, typename XT, typename WT>
 int launch(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
-  const size_t lds = 2 * (size_t)(BM + BN) * 128;
+  const size_t lds = std::max(2 * (size_t)(BM + BN) * 128, (size_t)parked_bytes<BM, BN>());
   auto k = gemm_kernel<BM, BN, WM, WN, XT, WT>;
   static bool attr_set = false;  // raise the dynamic-LDS cap once per instantiation
   if (!attr_set && lds > 65536) {
