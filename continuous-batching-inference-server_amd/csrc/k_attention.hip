@@ -399,10 +399,13 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
   }
   const int kv_end = min(pos0 + nvalid, a.max_kv);  // keys [0, kv_end) needed by the tile
 
-  // Per-wave V tile [key][dim], 64-byte rows (8-byte aligned for the
-  // transposing reads).
-  __shared__ __attribute__((aligned(16))) uint16_t vt_all[HPW * kPrefillWaves][32][kHD];
-  auto& vt_w = vt_all[wave_id];
+  // Per-wave V tile [key][dim]: 64-byte rows of four 16-byte chunks, chunk c
+  // of key row r in position c ^ ((r >> 2) & 3).  Unswizzled, the 16 lanes
+  // of a ds_write_b128 (keys 0..15, one chunk) hit 4 bank groups 4 times
+  // each; swizzled, 16 distinct groups.
+  __shared__ __attribute__((aligned(16))) uint8_t vt_all[HPW * kPrefillWaves][32 * kHD * 2];
+  uint8_t* const vt_w = vt_all[wave_id];
+  auto vpos = [](int key, int chunk) { return key * (kHD * 2) + ((chunk ^ ((key >> 2) & 3)) << 4); };
   // Per query column: o (the P.V accumulator), lacc (every entry the
   // column's sum of the bf16-rounded p: an MFMA of an all-ones A with P^T,
   // beside the P.V MFMAs, in place of 16 adds and a lane exchange per block)
@@ -435,14 +438,21 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
   // Page id of this lane's key j0 + col, clamped to kv_end - 1: keys j0 ..
   // j0 + 15 lie on page min(j0, kv_end - 1) / 16, keys j0 + 16 .. j0 + 31 on
   // page min(j0 + 16, kv_end - 1) / 16 (j0 is a multiple of 32).
+  // The ids are clamped to the pool here, in scalar registers.
   auto id_of = [&](int j0) {
-    const int pa = bt[min(j0, kv_end - 1) / kPS], pb = bt[min(j0 + 16, kv_end - 1) / kPS];
+    const unsigned last = (unsigned)(kv_end - 1);
+    const int pa = min(max(bt[min((unsigned)j0, last) / kPS], 0), a.num_pages - 1);
+    const int pb = min(max(bt[min((unsigned)j0 + 16u, last) / kPS], 0), a.num_pages - 1);
     return col < 16 ? pa : pb;
   };
-  auto load_block = [&](int j0, int id, KV& r) {
-    const int kc = min(j0 + col, kv_end - 1);
-    const int phys = min(max(id, 0), a.num_pages - 1);
-    const int64_t slot = (int64_t)phys * (kPS * D) + (kc % kPS) * D + head * kHD;
+  // Element offset of this lane's key within its page, plus its head:
+  // (col % 16) * D + head * kHD for every block that ends before kv_end.
+  const int lane_off = (col & (kPS - 1)) * D + head * kHD;
+  const int64_t page_elems = (int64_t)kPS * D;
+  auto load_block = [&](int j0, int phys, KV& r) {
+    int off = lane_off;
+    if (j0 + 31 >= kv_end) off = (min(j0 + col, kv_end - 1) & (kPS - 1)) * D + head * kHD;
+    const int64_t slot = phys * page_elems + off;
     r.k0 = *(const bf16x8_t*)(a.kpool + slot + half * 8);
     r.k1 = *(const bf16x8_t*)(a.kpool + slot + 16 + half * 8);
     const uint4* vs = (const uint4*)(a.vpool + slot + half * 16);
@@ -456,16 +466,19 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
   // receives V[4 h + e][d] (+ 8, 16, 24): the A-operand layout of V^T below.
   const int kr = 4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2);
   const int dc = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  auto vt_read = [&](int key) {
+  // Byte offsets of the 8-byte rows read for keys kr + 8 m (m = 0..3) and of
+  // this lane's two V chunks (key col, dims 16 half .. + 15).
+  int vrd[4];
+#pragma unroll
+  for (int mm = 0; mm < 4; ++mm) vrd[mm] = vpos(kr + 8 * mm, dc >> 3) + (dc & 7) * 2;
+  const int vwr0 = vpos(col, 2 * half), vwr1 = vpos(col, 2 * half + 1);
+  auto vt_read = [&](int mm) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_short4_t*)(__attribute__((address_space(3))) void*)&vt_w[key][dc]);
+        (lds_short4_t*)(__attribute__((address_space(3))) void*)(vt_w + vrd[mm]));
   };
   auto compute_block = [&](int j0, const KV& r) {
-    {
-      uint4* dst = (uint4*)&vt_w[col][half * 16];  // this lane's key, 16 dims
-      dst[0] = r.v0;
-      dst[1] = r.v1;
-    }
+    *(uint4*)(vt_w + vwr0) = r.v0;  // this lane's key, dims 16 half .. + 7
+    *(uint4*)(vt_w + vwr1) = r.v1;  // and + 8 .. + 15
     bf16x8_t pb0[kQG], pb1[kQG];
     // Both groups' scores first (no branch between their MFMAs), then one
     // uniform mask test and one uniform rescale test for the block.
@@ -545,7 +558,7 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
     // its lanes read each other's entries.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
-    const short4_t a0 = vt_read(kr), a1 = vt_read(8 + kr), b0 = vt_read(16 + kr), b1 = vt_read(24 + kr);
+    const short4_t a0 = vt_read(0), a1 = vt_read(1), b0 = vt_read(2), b1 = vt_read(3);
     bf16x8_t va0, va1;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
