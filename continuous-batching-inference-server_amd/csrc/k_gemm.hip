@@ -170,6 +170,30 @@ __device__ inline void epilogue_store(const GemmArgs& g, int row, int col, float
   else ((float*)g.Y)[o] = v;
 }
 
+// epilogue_store with its inputs loaded beforehand: the channel scale sc, bias
+// bi, residual r and the row's K/V slot (wpage * page_size + woff), as
+// epilogue_store would read them.
+__device__ inline void epilogue_store_pre(const GemmArgs& g, int row, int col, float v, float sc, float bi, float r,
+                                          int64_t kv_slot) {
+  if (g.w_scale) v *= sc;
+  if (g.bias) v += bi;
+  if (g.gelu) v = gelu_erf(v);
+  if (g.residual) v += r;
+  if (g.k_pool && col >= g.kv_col0) {
+    const int c = col - g.kv_col0;
+    const bool is_v = c >= g.kv_width;
+    const int e = is_v ? c - g.kv_width : c;
+    const int64_t off = kv_slot * g.kv_width + e;
+    void* pool = is_v ? g.v_pool : g.k_pool;
+    if (g.kv_bf16) ((uint16_t*)pool)[off] = f32_to_bf16(v);
+    else ((float*)pool)[off] = v;
+    return;
+  }
+  const int64_t o = (int64_t)row * g.ldy + col;
+  if (g.y_bf16) ((uint16_t*)g.Y)[o] = f32_to_bf16(v);
+  else ((float*)g.Y)[o] = v;
+}
+
 template <typename WT>
 struct WLoad;  // global W chunk (covering 16 bytes of LDS) -> uint4 of the compute type
 template <>
@@ -1159,6 +1183,30 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
 #pragma unroll
   for (int i = 0; i < MB; ++i) xrow[i] = min(i * 16 + c16, g.M - 1);
 
+  // Wave 0 finishes the tile.  With up to 32 rows (MB <= 2) it loads the
+  // epilogue's inputs (channel scale, bias, residual, K/V slots of its rows)
+  // now, so their round trip overlaps the K loop instead of following it;
+  // rows / columns past M / N read row M - 1 / column N - 1 (in bounds, never
+  // stored).  At MB = 4 the registers they hold cost more (spills).
+  constexpr bool PRE = MB <= 2;
+  const int pcol = min(n0 + c16, g.N - 1);
+  float pre_sc = 1.f, pre_bi = 0.f;
+  float pre_r[MB][4];
+  int64_t pre_slot[MB][4];
+  if (PRE && wave == 0 && !g.amax) {
+    if (g.w_scale) pre_sc = g.w_scale[pcol];
+    if (g.bias) pre_bi = g.bias[pcol];
+    const bool kv = g.k_pool && pcol >= g.kv_col0;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = min(i * 16 + 4 * q + e, g.M - 1);
+        pre_r[i][e] = g.residual ? g.residual[(int64_t)row * g.ldr + pcol] : 0.f;
+        pre_slot[i][e] = kv ? (int64_t)g.wpage[row] * g.page_size + g.woff[row] : 0;
+      }
+  }
+
   // LayerNorm prologue: each wave takes rows wave, wave + 8, ... of the
   // workgroup's 16 MB rows and forms their mean and 1/std exactly as
   // ln_block_row does (per-lane sums over the row's float4 chunks 0 .. nch-1
@@ -1368,7 +1416,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = i * 16 + 4 * q + e;
-      if (row < g.M && col < g.N) epilogue_store(g, row, col, v[e]);
+      if (row < g.M && col < g.N) {
+        if constexpr (PRE) epilogue_store_pre(g, row, col, v[e], pre_sc, pre_bi, pre_r[i][e], pre_slot[i][e]);
+        else epilogue_store(g, row, col, v[e]);
+      }
     }
   }
 }
