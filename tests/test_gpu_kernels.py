@@ -191,6 +191,60 @@ def test_gemm_gelu_epilogue_accuracy(cbis, dev, M, xdt):
     assert np.all(np.abs(got - ref[:, None]) <= 1e-6 * (1 + np.abs(ref[:, None])))
 
 
+@pytest.mark.parametrize("wdt", ["f32", "bf16", "fp8"])
+@pytest.mark.parametrize("ydt", ["f32", "bf16"])
+@pytest.mark.parametrize("N,pad", [(250, 3), (252, 0), (258, 4)])
+def test_gemm_parked_epilogue_ragged(cbis, oracle, dev, wdt, ydt, N, pad):
+    """The LDS-parked epilogue of the single-role kernels (gemm_kernel for
+    fp32 / fp8 W, gemm_bf16_dma_kernel for bf16) on ragged shapes, whole K:
+    M = 600 ends inside a row tile, N = 250 / 258 inside a 4-column group
+    (element-wise stores), N = 252 inside a column tile with 16-byte groups;
+    Y rows padded by `pad` elements (an odd pitch forces element-wise
+    stores), bias + GELU, and a residual (aliasing Y when Y is fp32),
+    against the fp64 oracle; columns of the padding stay untouched."""
+    import torch
+    M, K = 600, 256
+    ldy = N + pad
+    x = oracle.normal(23, 1, M * K).reshape(M, K)
+    w = oracle.normal(23, 2, N * K, 0.02).reshape(N, K)
+    b = oracle.normal(23, 3, N, 0.02)
+    r = oracle.normal(23, 4, M * N).reshape(M, N)
+    S = None
+    if wdt == "f32":
+        X, W, xdt, wd, xr, wr = to_dev(x, dev), to_dev(w, dev), cbis.F32, cbis.F32, x, w
+    elif wdt == "bf16":
+        (X, xr), (W, wr) = bf16_dev(x, dev), bf16_dev(w, dev)
+        xdt, wd = cbis.BF16, cbis.BF16
+    else:
+        codes, sc = oracle.quantize_e4m3_rows(w)
+        (X, xr), W, S = bf16_dev(x, dev), to_dev(codes, dev), to_dev(sc, dev)
+        wr = oracle.e4m3_table()[codes] * sc[:, None]
+        xdt, wd = cbis.BF16, cbis.FP8E4M3
+    sentinel = 7.0
+    if ydt == "f32":
+        Y = torch.full((M, ldy), sentinel, dtype=torch.float32, device=dev)
+        Y[:, :N] = to_dev(r, dev)
+        R, ldr = Y, ldy
+    else:
+        Y = torch.full((M, ldy), sentinel, dtype=torch.bfloat16, device=dev)
+        R, ldr = to_dev(r, dev), N
+    d = cbis.GemmDesc()
+    d.M, d.N, d.K = M, N, K
+    d.x_dtype, d.X, d.ldx = xdt, ptr(X), K
+    d.w_dtype, d.W, d.ldw = wd, ptr(W), K
+    d.w_scale, d.bias = ptr(S), ptr(to_dev(b, dev))
+    d.epilogue = cbis.EPI_GELU
+    d.residual, d.ldr = ptr(R), ldr
+    d.y_dtype, d.Y, d.ldy = cbis.F32 if ydt == "f32" else cbis.BF16, ptr(Y), ldy
+    cbis.check(cbis.kernels().cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
+    sync()
+    got = Y.float().cpu().numpy()
+    ref = oracle.gemm(xr, wr.astype(np.float32), bias=b, gelu=True, residual=r)
+    tol = FP32_TOL if ydt == "f32" else 8e-3 * (1 + np.abs(ref))
+    assert np.all(np.abs(got[:, :N] - ref) <= tol)
+    assert np.all(got[:, N:] == sentinel)
+
+
 @pytest.mark.parametrize("M", [192, 1216])
 @pytest.mark.parametrize("N,K,gelu", [(2048, 4096, False), (2048, 8192, False), (1024, 4096, True), (1030, 4096, False),
                                       (2050, 4096, False), (8192, 2048, True)])
