@@ -384,12 +384,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
 // wide stores to Y carry the nontemporal hint: every output line is written
 // once, by one workgroup, and is read (if at all) by a later kernel (on
 // config 2's bf16 M = 4096 shapes 16-byte stores alone gained 11-21%, with
-// the hint 30-37%; config 4's fc1 50.0 against 51.7 us).  K/V rows scattered
-// into the pools are stored plainly: the step's prefill attention reads them
-// after the decode kernel's non-temporal stream over the pools, and plainly
-// stored they are still in the caches then (config 4's prefill 18.1 against
-// 20.3 us with the hint, same box); so are the split-K partials, which the
-// reduce reads right away.
+// the hint 30-37%; config 4's fc1 50.0 against 51.7 us).  A call that
+// scatters K/V (the QKV projection) stores plainly, Q and K/V alike: the
+// step's prefill attention reads them after the decode kernel's non-temporal
+// stream over the pools, and plainly stored they are still in the caches then
+// (config 4's prefill 17.9 us against 18.2 with Q hinted and 20.3 with Q and
+// K/V hinted, same box); so are the split-K partials, which the reduce reads
+// right away.
 struct Cols4 {
   int col, nc;
   float sc[4], bi[4];
@@ -476,7 +477,7 @@ struct Cols4 {
     const bool bf = to_kv ? g.kv_bf16 : g.y_bf16;
     void* dst = to_kv ? (void*)((char*)pool + (slot * g.kv_width + ce) * (bf ? 2 : 4))
                       : (void*)((char*)g.Y + ((int64_t)row * g.ldy + col) * (bf ? 2 : 4));
-    if (to_kv) {
+    if (g.k_pool) {
       if (bf) *(uint2*)dst = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       else *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
     } else if (bf) {
