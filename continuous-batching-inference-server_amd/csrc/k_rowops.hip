@@ -4,9 +4,11 @@
 // K/V page scatter (kernels/attention.cu:7-19), greedy argmax
 // (src/bench_batching.cpp:66-73) and the synthetic-data fills.
 //
-// LayerNorm runs one wave per row with the row held in registers (two-pass
-// mean / variance over registers, DPP/shuffle reductions), instead of the
-// reference's one 256-thread block per row with a shared-memory tree.
+// LayerNorm keeps the row in registers of one 256-thread workgroup (16-byte
+// chunks, chunk i on wave i mod 4) and forms a two-pass mean / variance from
+// per-lane sums in chunk order, exchanged through LDS and finished with wave
+// reductions (ln_block_row), instead of the reference's one-pass E[x^2] -
+// mean^2 over a shared-memory tree.
 #include <cstdarg>
 
 #include "common.hpp"
