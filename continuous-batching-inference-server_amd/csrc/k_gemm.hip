@@ -68,7 +68,30 @@ struct GemmArgs {
   const float* ln_b;
   float ln_eps;
   int ln_nch;
+  // Every 4-column group of the output is whole and aligned in its
+  // destination (Y, the K/V pools or the partials) and in the residual: the
+  // parked epilogue then takes its vector path on tiles inside N (with_vec).
+  int vec_ok;
 };
+
+// g with vec_ok set from its shapes, strides and pointers.
+GemmArgs with_vec(const GemmArgs& g) {
+  GemmArgs a = g;
+  bool ok = (g.N & 3) == 0;
+  if (g.ksplit > 1) {
+    ok = ok && ((uintptr_t)g.partial & 15u) == 0;
+  } else {
+    if (g.residual) ok = ok && (g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15u) == 0;
+    if (g.k_pool) {
+      const uintptr_t al = g.kv_bf16 ? 7u : 15u;
+      ok = ok && (g.kv_col0 & 3) == 0 && (g.kv_width & 3) == 0 && ((uintptr_t)g.k_pool & al) == 0 &&
+           ((uintptr_t)g.v_pool & al) == 0;
+    }
+    if (!g.k_pool || g.kv_col0 > 0) ok = ok && (g.ldy & 3) == 0 && ((uintptr_t)g.Y & (g.y_bf16 ? 7u : 15u)) == 0;
+  }
+  a.vec_ok = ok ? 1 : 0;
+  return a;
+}
 // cbis_layernorm_gemm forms the normalised rows in the skinny kernel for K up
 // to kLnPrologueMaxK: every workgroup re-reads its rows' fp32 x and their
 // statistics, which costs less than a LayerNorm launch only for short rows
@@ -80,15 +103,15 @@ constexpr int kLnMaxChunks = kLnPrologueMaxK / 256;  // float4 chunks per lane o
 // Top-2 of a row: the maximum m1 at the lowest index i1 among equal maxima
 // (the strict-> scan of src/bench_batching.cpp:66-73), and the largest value
 // m2 at any other index (m2 == m1 when the maximum is tied).  NaN never
-// wins.  Start from m1 = m2 = -inf, i1 = INT_MAX.
+// wins.  Start from m1 = m2 = -inf, i1 = INT_MAX.  top2_push takes one lane's
+// columns in increasing order, so a value equal to the maximum never
+// displaces it (the strict > keeps the lowest index); a lane that sees only
+// -inf keeps i1 = INT_MAX, which the merges rank after every real index.
 __device__ inline void top2_push(float& m1, float& m2, int& i1, float v, int c) {
-  if (v > m1 || (v == m1 && c < i1)) {
-    m2 = m1;
-    m1 = v;
-    i1 = c;
-  } else {
-    m2 = fmaxf(m2, v);
-  }
+  const bool up = v > m1;
+  m2 = fmaxf(m2, up ? m1 : v);
+  i1 = up ? c : i1;
+  m1 = up ? v : m1;
 }
 // Merges another partial (b1, b2, bi) of disjoint columns; order-free.
 __device__ inline void top2_merge(float& m1, float& m2, int& i1, float b1, float b2, int bi) {
@@ -762,7 +785,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmAr
 template <int BM, int BN, int WM, int WN, int STAGES>
 int launch_dma(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
-  gemm_bf16_dma_kernel<BM, BN, WM, WN, STAGES><<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, 0, s>>>(g);
+  gemm_bf16_dma_kernel<BM, BN, WM, WN, STAGES><<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, 0, s>>>(with_vec(g));
   return check_launch("cbis_gemm(bf16)");
 }
 
@@ -818,6 +841,114 @@ struct WsTile {
   static_assert(BM % PH == 0 && PR * PITCH * 4 <= kLdsMax && LDS <= kLdsMax, "LDS");
 };
 
+// Vector path of epilogue_rows, for tiles whose every 4-column group is whole
+// and aligned in its destination (g.vec_ok, tile inside N).  vmcnt counts
+// stores as well as loads and retires them in order, so a memory read issued
+// after a store -- or a register that an in-flight store still names being
+// rewritten on a load's path -- makes the code wait for that store's write
+// acknowledgement; the general path's per-row loads and branches cost such a
+// wait on every row.  Here the thread's global inputs (RES: the residual
+// values, KV: the rows' page and offset ids) are all loaded before the first
+// store, the parked values are read G rows at a time from LDS (which vmcnt
+// does not count), and each row is finished -- the same operations in the
+// same order as Cols4::finish -- and stored with one 16-byte (fp32) or 8-byte
+// (bf16) store.  RES and KV are template flags so that a variant holds only
+// the registers its inputs need.  Config 4's step, same box: qkv 41.3 ->
+// 37.2 us, out-projection 25.7 -> 22.9, fc1 50.2 -> 48.5 (its GELU is most of
+// what remains of its epilogue).
+template <int PASSES, int RPP, bool RES, bool KV>
+__device__ inline void epilogue_rows_vec(const GemmArgs& g, int kz, const float* tile, int pitch, int m0, int n0,
+                                         int cg, int rs) {
+  constexpr int G = PASSES % 4 == 0 ? 4 : (PASSES % 2 == 0 ? 2 : 1);
+  const bool raw = g.ksplit > 1;  // RES and KV imply !raw
+  const int col = n0 + 4 * cg;
+  float sc[4], bi[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sc[e] = (!raw && g.w_scale) ? g.w_scale[col + e] : 1.f;
+    bi[e] = (!raw && g.bias) ? g.bias[col + e] : 0.f;
+  }
+  const bool to_kv = KV && col >= g.kv_col0;
+  const int c = col - g.kv_col0;
+  const bool is_v = to_kv && c >= g.kv_width;
+  const bool bf = !raw && (to_kv ? g.kv_bf16 : g.y_bf16);
+  const int esz = bf ? 2 : 4;
+  // Destination of row index ri (the row, or the K/V slot): base + ri * stride.
+  char* base;
+  int64_t stride;
+  if (raw) {
+    base = (char*)(g.partial + (int64_t)kz * g.M * g.N + col);
+    stride = (int64_t)g.N * 4;
+  } else if (to_kv) {
+    base = (char*)(is_v ? g.v_pool : g.k_pool) + (int64_t)(is_v ? c - g.kv_width : c) * esz;
+    stride = (int64_t)g.kv_width * esz;
+  } else {
+    base = (char*)g.Y + (int64_t)col * esz;
+    stride = g.ldy * esz;
+  }
+  // Rows clamped to M - 1 (rows past M are not stored), so the loads need no
+  // per-lane condition and issue back to back.
+  float4 res[RES ? PASSES : 1];
+  uint32_t wp[KV ? PASSES : 1], wo[KV ? PASSES : 1];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int row = min(m0 + p * RPP + rs, g.M - 1);
+    if constexpr (RES) res[p] = *(const float4*)(g.residual + (int64_t)row * g.ldr + col);
+    if constexpr (KV) {
+      wp[p] = (uint32_t)g.wpage[row];
+      wo[p] = (uint32_t)g.woff[row];
+    }
+  }
+  const bool hs = !raw && g.w_scale, hb = !raw && g.bias, hg = !raw && g.gelu;
+#pragma unroll
+  for (int p0 = 0; p0 < PASSES; p0 += G) {
+    float4 tv[G];
+#pragma unroll
+    for (int q = 0; q < G; ++q) tv[q] = *(const float4*)(tile + ((p0 + q) * RPP + rs) * pitch + 4 * cg);
+#pragma unroll
+    for (int q = 0; q < G; ++q) {
+      const int p = p0 + q;
+      const int row = m0 + p * RPP + rs;
+      float v[4] = {tv[q].x, tv[q].y, tv[q].z, tv[q].w};
+      // Scale and bias by selects (x * 1 or x + 0 would not be exact for
+      // every x), GELU under one branch per row.
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xs = v[e] * sc[e];
+        v[e] = hs ? xs : v[e];
+        const float xb = v[e] + bi[e];
+        v[e] = hb ? xb : v[e];
+      }
+      if (hg) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+      }
+      if constexpr (RES) {
+        v[0] += res[p].x; v[1] += res[p].y; v[2] += res[p].z; v[3] += res[p].w;
+      }
+      // Slot ids are non-negative: widened unsigned, so no sign extension is
+      // computed (and waited for) right after their loads.
+      int64_t ri = row;
+      if constexpr (KV) {
+        if (to_kv) ri = (int64_t)((uint64_t)wp[p] * (uint32_t)g.page_size + wo[p]);
+      }
+      char* dst = base + ri * stride;
+      if (row >= g.M) continue;
+      if (raw || KV) {
+        // Split-K partials and calls that scatter K/V: plain stores.
+        if (bf) *(uint2*)dst = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        else *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+      } else if (bf) {
+        const u32x2_t w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        __builtin_nontemporal_store(w, (u32x2_t*)dst);
+      } else {
+        const f32x4_t w = {v[0], v[1], v[2], v[3]};
+        __builtin_nontemporal_store(w, (f32x4_t*)dst);
+      }
+    }
+  }
+}
+
 // Epilogue over a parked BM x BN fp32 tile by the workgroup's NT threads:
 // thread (rs, cg) takes columns 4cg..4cg+3 of rows rs, rs + RPP, ...; the
 // inputs of 4 rows are loaded before their stores (Y may alias the residual).
@@ -830,6 +961,26 @@ __device__ inline void epilogue_rows(const GemmArgs& g, int kz, const float* til
   constexpr int G = PASSES % 4 == 0 ? 4 : 2;  // rows whose inputs are loaded before their stores
   static_assert(RPP * CG == NT && PASSES % G == 0, "epilogue thread map");
   const int cg = tid % CG, rs = tid / CG;
+  // The vector path (tiles inside N with aligned groups); a residual is
+  // preloaded there only for up to 8 rows per thread (its registers would
+  // otherwise raise every call's allocation), and never with a K/V scatter.
+  if (g.vec_ok && n0 + BN <= g.N) {
+    const bool raw_call = g.ksplit > 1, res = !raw_call && g.residual, kv = !raw_call && g.k_pool;
+    if (!res && !kv) {
+      epilogue_rows_vec<PASSES, RPP, false, false>(g, kz, tile, pitch, m0, n0, cg, rs);
+      return;
+    }
+    if (!res) {
+      epilogue_rows_vec<PASSES, RPP, false, true>(g, kz, tile, pitch, m0, n0, cg, rs);
+      return;
+    }
+    if constexpr (PASSES <= 8) {
+      if (!kv) {
+        epilogue_rows_vec<PASSES, RPP, true, false>(g, kz, tile, pitch, m0, n0, cg, rs);
+        return;
+      }
+    }
+  }
   if (n0 + 4 * cg >= g.N) return;
   const bool raw = g.ksplit > 1;
   const Cols4 c(g, n0 + 4 * cg, raw);
@@ -884,52 +1035,96 @@ __device__ inline void epilogue_parked(const GemmArgs& g, int kz, uint8_t* smem,
   epilogue_rows<BM, BN, WM * WN * 64>(g, kz, tile, PITCH, m0, n0, tid);
 }
 
+// Channel scale and bias of the greedy epilogue's columns for lane j of a
+// 16-lane row group: columns n0 + 64 k + 4 j + e (loaded once per tile, with
+// the column clamped to N - 1: columns past N are never ranked).
+template <int BN>
+struct Top2Cols {
+  static constexpr int KC = BN / 64;  // float4 chunks per lane
+  float sc[KC][4], bi[KC][4];
+  __device__ Top2Cols(const GemmArgs& g, int n0, int j) {
+#pragma unroll
+    for (int k = 0; k < KC; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = min(n0 + 64 * k + 4 * j + e, g.N - 1);
+        sc[k][e] = g.w_scale ? g.w_scale[c] : 1.f;
+        bi[k][e] = g.bias ? g.bias[c] : 0.f;
+      }
+  }
+};
+struct NoCols {
+  __device__ NoCols(const GemmArgs&, int, int) {}
+};
+
 // Greedy-mode epilogue over a parked BM x BN fp32 tile: each 16-lane row of
 // a wave takes one tile row (a wave 4 rows at a time), lane j of it the
 // columns 4 j + 64 k .. + 3 (16-byte LDS reads, the 16 lanes covering 256
 // consecutive bytes: no bank conflicts); each value gets the channel scale
 // and bias exactly as Cols4::finish applies them (so it equals the logit the
 // store path would write); the row's top-2 over the tile's columns is
-// written for column tile n0 / BN.
-template <int BM, int BN, int NT = 512>
-__device__ inline void epilogue_top2(const GemmArgs& g, const float* tile, int pitch, int m0, int n0, int tid) {
-  constexpr int KC = BN / 64;  // float4 chunks per lane
-  static_assert(KC * 64 == BN, "epilogue_top2 tile width");
+// written for column tile n0 / BN.  The work is VALU-bound, so the variants
+// for a tile inside N (CHECK false: no column test) and for calls without
+// scale or bias (AFFINE false) are separate loops, chosen once per tile; the
+// partials of all the wave's rows are stored after the last of them is
+// formed, so no store is waited for inside the epilogue (config 4's lm_head
+// in the step, same box: 188 -> 164.5 us, 969 TFLOP/s).
+template <int BM, int BN, int NT, bool CHECK, bool AFFINE>
+__device__ inline void epilogue_top2_rows(const GemmArgs& g, const Top2Cols<BN>& cc, const float* tile, int pitch,
+                                          int m0, int n0, int tid) {
+  constexpr int KC = Top2Cols<BN>::KC;
+  static_assert(KC * 64 == BN && BM % 4 == 0, "epilogue_top2 tile");
+  constexpr int RPI = 4 * (NT / 64);  // rows per iteration of the workgroup
+  constexpr int IT = (BM + RPI - 1) / RPI;
   const int wave = tid >> 6, lane = tid & 63, grp = lane >> 4, j = lane & 15;
-  float sc[KC][4], bi[KC][4];
-  bool ok[KC][4];
+  const bool hs = g.w_scale != nullptr, hb = g.bias != nullptr;
+  float4 part[IT];
 #pragma unroll
-  for (int k = 0; k < KC; ++k)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int c = n0 + 64 * k + 4 * j + e;
-      ok[k][e] = c < g.N;
-      sc[k][e] = (g.w_scale && ok[k][e]) ? g.w_scale[c] : 1.f;
-      bi[k][e] = (g.bias && ok[k][e]) ? g.bias[c] : 0.f;
-    }
-  for (int r0 = 4 * wave; r0 < BM; r0 += 4 * (NT / 64)) {
-    const int r = r0 + grp;
+  for (int it = 0; it < IT; ++it) {
+    const int rw = 4 * wave + RPI * it;  // the wave's first row: wave-uniform
     float m1 = -INFINITY, m2 = -INFINITY;
     int i1 = 0x7FFFFFFF;
-    if (r < BM) {
+    if (rw < BM) {
+      const int r = rw + grp;
+      float4 t[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) t[k] = *(const float4*)(tile + r * pitch + 64 * k + 4 * j);
 #pragma unroll
       for (int k = 0; k < KC; ++k) {
-        const float4 t = *(const float4*)(tile + r * pitch + 64 * k + 4 * j);
-        const float tv[4] = {t.x, t.y, t.z, t.w};
+        const float tv[4] = {t[k].x, t[k].y, t[k].z, t[k].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if (!ok[k][e]) continue;
+          const int c = n0 + 64 * k + 4 * j + e;
           float v = tv[e];
-          if (g.w_scale) v *= sc[k][e];
-          if (g.bias) v += bi[k][e];
-          top2_push(m1, m2, i1, v, n0 + 64 * k + 4 * j + e);
+          if constexpr (AFFINE) {
+            const float xs = v * cc.sc[k][e];
+            v = hs ? xs : v;
+            const float xb = v + cc.bi[k][e];
+            v = hb ? xb : v;
+          }
+          if constexpr (CHECK) v = c < g.N ? v : -INFINITY;  // -inf: no effect on the top-2
+          top2_push(m1, m2, i1, v, c);
         }
       }
     }
     top2_row16(m1, m2, i1);
-    if (j == 0 && r < BM && m0 + r < g.M)
-      g.amax[(int64_t)(m0 + r) * g.amax_ld + n0 / BN] = make_float4(m1, m2, __int_as_float(i1), 0.f);
+    part[it] = make_float4(m1, m2, __int_as_float(i1), 0.f);
   }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int r = 4 * wave + RPI * it + grp;
+    if (j == 0 && 4 * wave + RPI * it < BM && m0 + r < g.M)
+      g.amax[(int64_t)(m0 + r) * g.amax_ld + n0 / BN] = part[it];
+  }
+}
+
+template <int BM, int BN, int NT = 512>
+__device__ inline void epilogue_top2(const GemmArgs& g, const Top2Cols<BN>& cc, const float* tile, int pitch, int m0,
+                                     int n0, int tid) {
+  const bool check = n0 + BN > g.N, affine = g.w_scale || g.bias;
+  if (check) epilogue_top2_rows<BM, BN, NT, true, true>(g, cc, tile, pitch, m0, n0, tid);
+  else if (affine) epilogue_top2_rows<BM, BN, NT, false, true>(g, cc, tile, pitch, m0, n0, tid);
+  else epilogue_top2_rows<BM, BN, NT, false, false>(g, cc, tile, pitch, m0, n0, tid);
 }
 
 template <int BM, int BN, int STAGES, int REGS, int WM, bool TOP2>
@@ -1094,6 +1289,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
   }
   // Park the accumulators (PH blocks of PR rows) and finish them row-wise.
   float* park = (float*)smem;
+  // Greedy mode: the tile's column constants, loaded once for all row blocks.
+  const typename std::conditional<TOP2, Top2Cols<BN>, NoCols>::type cols(g, n0, tid & 15);
 #pragma unroll
   for (int h = 0; h < T::PH; ++h) {
     if (wave < 4) {
@@ -1111,7 +1308,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
     // Greedy mode is a separate instantiation: the two epilogues in one kernel
     // raised its scalar-register spills (24 -> 157 at 160 x 256) and slowed
     // the K loop of every call.
-    if constexpr (TOP2) epilogue_top2<T::PR, BN>(g, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
+    if constexpr (TOP2) epilogue_top2<T::PR, BN>(g, cols, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
     else epilogue_rows<T::PR, BN>(g, kz, (const float*)smem, T::PITCH, m0 + h * T::PR, n0, tid);
     if (h + 1 < T::PH) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
@@ -1121,7 +1318,7 @@ template <int BM, int BN, int STAGES, int REGS = 0, int WM = 2>
 int launch_ws(const GemmArgs& g, hipStream_t s) {
   const int64_t tiles = cdiv(g.M, BM) * cdiv(g.N, BN);
   if (g.amax) gemm_bf16_ws_kernel<BM, BN, STAGES, REGS, WM, true><<<dim3((unsigned)tiles, 1, 1), 512, 0, s>>>(g);
-  else gemm_bf16_ws_kernel<BM, BN, STAGES, REGS, WM, false><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(g);
+  else gemm_bf16_ws_kernel<BM, BN, STAGES, REGS, WM, false><<<dim3((unsigned)tiles, 1, g.ksplit), 512, 0, s>>>(with_vec(g));
   return check_launch("cbis_gemm(bf16 ws)");
 }
 
@@ -1608,7 +1805,7 @@ int launch(const GemmArgs& g, hipStream_t s) {
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr_set = true;
   }
-  k<<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, lds, s>>>(g);
+  k<<<dim3((unsigned)tiles, 1, g.ksplit), WM * WN * 64, lds, s>>>(with_vec(g));
   return check_launch("cbis_gemm");
 }
 
