@@ -1144,6 +1144,8 @@ def _top2_np(logits):
     (100, 1000, 256, "bf16"),     # small grid: logits stored in Y, then reduced
     (100, 512, 256, "f32"),       # fp32 at M > 64 (config 1's prefill): stored, then reduced
     (200, 1000, 512, "fp8"),      # fp8 at M > 64: stored, then reduced
+    (600, 20007, 512, "bf16"),    # wave-specialised, last column tile partial (the column-test epilogue)
+    (600, 20480, 512, "bf16-nobias"),  # wave-specialised, no scale or bias (the plain epilogue)
 ])
 def test_gemm_argmax_matches_logits(cbis, oracle, dev, M, N, K, wdt):
     """Tokens and margins of the fused greedy lm_head equal, bit for bit,
@@ -1163,7 +1165,7 @@ def test_gemm_argmax_matches_logits(cbis, oracle, dev, M, N, K, wdt):
     if wdt == "f32":
         X, W = to_dev(x, dev), to_dev(w, dev)
         xdt, wd, S = cbis.F32, cbis.F32, None
-    elif wdt == "bf16":
+    elif wdt.startswith("bf16"):
         (X, _), (W, _) = bf16_dev(x, dev), bf16_dev(w, dev)
         xdt, wd, S = cbis.BF16, cbis.BF16, None
     else:
@@ -1172,7 +1174,7 @@ def test_gemm_argmax_matches_logits(cbis, oracle, dev, M, N, K, wdt):
         codes[N - 5] = codes[37]
         (X, _), W, S = bf16_dev(x, dev), to_dev(codes, dev), to_dev(sc, dev)
         xdt, wd = cbis.BF16, cbis.FP8E4M3
-    B = to_dev(b, dev)
+    B = None if wdt == "bf16-nobias" else to_dev(b, dev)
     Y = torch.empty((M, N), dtype=torch.float32, device=dev)
     d = cbis.GemmDesc()
     d.M, d.N, d.K = M, N, K
