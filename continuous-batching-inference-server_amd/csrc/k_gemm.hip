@@ -813,8 +813,10 @@ int launch_dma(const GemmArgs& g, hipStream_t s) {
 // parked in two row blocks, one after the other) and all 8 waves apply the
 // epilogue row by row, 4 consecutive columns per thread: the channel scale
 // and bias are loaded once per thread, residual / partial accesses are 16
-// bytes and bf16 / K/V stores 8 bytes, and every thread loads the inputs of
-// 4 rows before storing them (Y may alias the residual).
+// bytes and bf16 / K/V stores 8 bytes; on aligned tiles inside N every
+// global input of the thread's rows is loaded before its first store
+// (epilogue_rows_vec), elsewhere the inputs of 2-4 rows before their stores
+// (Y may alias the residual either way).
 // ---------------------------------------------------------------------------
 constexpr int kWsProducers = 4;
 
