@@ -172,30 +172,9 @@ __device__ inline float gelu_erf(float v) {
   return 0.5f * v * (1.0f + copysignf(erf_abs, v));
 }
 
-// Applies the epilogue to one accumulator and stores it.
-__device__ inline void epilogue_store(const GemmArgs& g, int row, int col, float v) {
-  if (g.w_scale) v *= g.w_scale[col];
-  if (g.bias) v += g.bias[col];
-  if (g.gelu) v = gelu_erf(v);
-  if (g.residual) v += g.residual[(int64_t)row * g.ldr + col];
-  if (g.k_pool && col >= g.kv_col0) {
-    const int c = col - g.kv_col0;
-    const bool is_v = c >= g.kv_width;
-    const int e = is_v ? c - g.kv_width : c;
-    const int64_t off = ((int64_t)g.wpage[row] * g.page_size + g.woff[row]) * g.kv_width + e;
-    void* pool = is_v ? g.v_pool : g.k_pool;
-    if (g.kv_bf16) ((uint16_t*)pool)[off] = f32_to_bf16(v);
-    else ((float*)pool)[off] = v;
-    return;
-  }
-  const int64_t o = (int64_t)row * g.ldy + col;
-  if (g.y_bf16) ((uint16_t*)g.Y)[o] = f32_to_bf16(v);
-  else ((float*)g.Y)[o] = v;
-}
-
-// epilogue_store with its inputs loaded beforehand: the channel scale sc, bias
-// bi, residual r and the row's K/V slot (wpage * page_size + woff), as
-// epilogue_store would read them.
+// Applies the epilogue to one accumulator and stores it (the skinny kernel),
+// with its inputs loaded beforehand: the channel scale sc, bias bi, residual r
+// and the row's K/V slot (wpage * page_size + woff).
 __device__ inline void epilogue_store_pre(const GemmArgs& g, int row, int col, float v, float sc, float bi, float r,
                                           int64_t kv_slot) {
   if (g.w_scale) v *= sc;
@@ -403,7 +382,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
 // right edge) handled by one thread: the per-column constants once, then per
 // row the inputs (residual, K/V slot) and the finished store.  One 16-byte
 // (fp32) or 8-byte (bf16) store when the 4 columns share a destination and
-// its alignment allows, else element by element like epilogue_store.  The
+// its alignment allows, else element by element.  The
 // wide stores to Y carry the nontemporal hint: every output line is written
 // once, by one workgroup, and is read (if at all) by a later kernel (on
 // config 2's bf16 M = 4096 shapes 16-byte stores alone gained 11-21%, with
@@ -1394,13 +1373,14 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
   // epilogue's inputs (channel scale, bias, residual, K/V slots of its rows)
   // now, so their round trip overlaps the K loop instead of following it;
   // rows / columns past M / N read row M - 1 / column N - 1 (in bounds, never
-  // stored).  At MB = 4 the registers they hold cost more (spills).
+  // stored).  At MB = 4 the registers they would hold through the K loop
+  // cost more (spills), so there they are loaded after it.
   constexpr bool PRE = MB <= 2;
   const int pcol = min(n0 + c16, g.N - 1);
   float pre_sc = 1.f, pre_bi = 0.f;
   float pre_r[MB][4];
   int64_t pre_slot[MB][4];
-  if (PRE && wave == 0 && !g.amax) {
+  auto load_pre = [&]() {
     if (g.w_scale) pre_sc = g.w_scale[pcol];
     if (g.bias) pre_bi = g.bias[pcol];
     const bool kv = g.k_pool && pcol >= g.kv_col0;
@@ -1412,7 +1392,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
         pre_r[i][e] = g.residual ? g.residual[(int64_t)row * g.ldr + pcol] : 0.f;
         pre_slot[i][e] = kv ? (int64_t)g.wpage[row] * g.page_size + g.woff[row] : 0;
       }
-  }
+  };
+  if (PRE && wave == 0 && !g.amax) load_pre();
 
   // LayerNorm prologue: each wave takes rows wave, wave + 8, ... of the
   // workgroup's 16 MB rows and forms their mean and 1/std exactly as
@@ -1594,6 +1575,14 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
   __syncthreads();
   if (wave != 0) return;
   const int col = n0 + c16;
+  // At MB = 4 the epilogue inputs are loaded here, after the K loop but still
+  // before the first store: a load issued after a store would wait for the
+  // store's write acknowledgement too (vmcnt counts both, in order), once per
+  // element (config 2's M = 64 MLP down, whose residual is such a load).
+  if (!PRE && !g.amax) load_pre();
+  const bool ok = col < g.N;
+  const float gsc = (g.amax && g.w_scale && ok) ? g.w_scale[col] : 1.f;
+  const float gbi = (g.amax && g.bias && ok) ? g.bias[col] : 0.f;
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
     f32x4_t v = part[0][i][lane];
@@ -1602,10 +1591,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
     if (g.amax) {
       // Greedy mode: the row's top-2 over this workgroup's 16 columns (lanes
       // 16 q .. 16 q + 15 hold the same rows), value = sum * scale + bias as
-      // epilogue_store computes it.
-      const bool ok = col < g.N;
-      const float sc = (g.w_scale && ok) ? g.w_scale[col] : 1.f;
-      const float bi = (g.bias && ok) ? g.bias[col] : 0.f;
+      // epilogue_store_pre computes it.
+      const float sc = gsc, bi = gbi;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float x = v[e];
@@ -1623,10 +1610,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = i * 16 + 4 * q + e;
-      if (row < g.M && col < g.N) {
-        if constexpr (PRE) epilogue_store_pre(g, row, col, v[e], pre_sc, pre_bi, pre_r[i][e], pre_slot[i][e]);
-        else epilogue_store(g, row, col, v[e]);
-      }
+      if (row < g.M && col < g.N) epilogue_store_pre(g, row, col, v[e], pre_sc, pre_bi, pre_r[i][e], pre_slot[i][e]);
     }
   }
 }
