@@ -53,19 +53,33 @@ __global__ __launch_bounds__(256) void embed_kernel(int T, int D, const int* __r
   const ET* a = te + (int64_t)t * D;
   const ET* b = pe + (int64_t)p * D;
   float* o = out + (int64_t)row * D;
-  for (int c = lane * 4; c < D; c += 256) {
-    float4 r;
-    if constexpr (sizeof(ET) == 4) {
-      const float4 x = *(const float4*)(a + c);
-      const float4 y = *(const float4*)(b + c);
-      r = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
-    } else {
-      const uint2 x = *(const uint2*)(a + c);
-      const uint2 y = *(const uint2*)(b + c);
-      r = make_float4(bf16lo(x.x) + bf16lo(y.x), bf16hi(x.x) + bf16hi(y.x), bf16lo(x.y) + bf16lo(y.y),
-                      bf16hi(x.y) + bf16hi(y.y));
+  // Chunks of 256 columns, 8 at a time: all of a group's loads before its
+  // stores (a load issued after a store would wait for the store's write
+  // acknowledgement too: vmcnt counts both, in order).
+  constexpr int G = 8;
+  for (int c0 = lane * 4; c0 < D; c0 += 256 * G) {
+    float4 r[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int c = c0 + 256 * k;
+      if (c >= D) break;
+      if constexpr (sizeof(ET) == 4) {
+        const float4 x = *(const float4*)(a + c);
+        const float4 y = *(const float4*)(b + c);
+        r[k] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+      } else {
+        const uint2 x = *(const uint2*)(a + c);
+        const uint2 y = *(const uint2*)(b + c);
+        r[k] = make_float4(bf16lo(x.x) + bf16lo(y.x), bf16hi(x.x) + bf16hi(y.x), bf16lo(x.y) + bf16lo(y.y),
+                           bf16hi(x.y) + bf16hi(y.y));
+      }
     }
-    *(float4*)(o + c) = r;
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int c = c0 + 256 * k;
+      if (c >= D) break;
+      *(float4*)(o + c) = r[k];
+    }
   }
 }
 
