@@ -296,6 +296,11 @@ int cbis_embed(int T, int D, const int* tok, const int* pos, int emb_dtype, cons
   CBIS_REQUIRE(vocab > 0 && max_pos > 0, CBIS_ERR_INVALID, "cbis_embed: vocab/max_pos must be > 0");
   if (T == 0) return CBIS_OK;
   CBIS_REQUIRE(tok && pos && te && pe && out, CBIS_ERR_INVALID, "cbis_embed: null pointer");
+  // Each lane moves 4 columns: 16-byte fp32 (8-byte bf16) table loads and
+  // 16-byte stores.
+  const uintptr_t tal = emb_dtype == CBIS_BF16 ? 7u : 15u;
+  CBIS_REQUIRE(((uintptr_t)te & tal) == 0 && ((uintptr_t)pe & tal) == 0 && aligned16(out), CBIS_ERR_INVALID,
+               "cbis_embed: tables and out must be %d-byte / 16-byte aligned", (int)tal + 1);
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)cdiv(T, 4));
   if (emb_dtype == CBIS_F32)

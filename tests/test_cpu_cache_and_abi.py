@@ -176,3 +176,8 @@ def test_abi_validation_without_gpu(cbis):
     a.split_tokens = 64
     assert K.cbis_paged_attention(ctypes.byref(a), None) == 1
     assert K.cbis_layernorm(4, 10000, 4096, 10000, 4096, 4096, 1e-5, 0, 4096, 10000, None) == 2
+    # embedding tables: 16-byte fp32 / 8-byte bf16 lane loads, 16-byte stores
+    assert K.cbis_embed(4, 256, 4096, 4096, cbis.F32, 4104, 4096, 10, 10, 4096, None) == 1
+    assert b"aligned" in K.cbis_last_error()
+    assert K.cbis_embed(4, 256, 4096, 4096, cbis.BF16, 4096, 4100, 10, 10, 4096, None) == 1
+    assert K.cbis_embed(4, 256, 4096, 4096, cbis.BF16, 4096, 4096, 10, 10, 4104, None) == 1
