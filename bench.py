@@ -25,7 +25,9 @@ attention alone), --config c5 (long-context fp8 decode), --config gemm
 restore); --copy-calib (a plain device copy for PMC byte calibration).
 """
 import argparse
+import contextlib
 import ctypes
+import gc
 import json
 import os
 import sys
@@ -94,6 +96,23 @@ class Events:
             e.record(self.stream)
         e.synchronize()
         return s.elapsed_time(e) / iters  # ms
+
+
+@contextlib.contextmanager
+def gc_paused():
+    """Runs a timed loop with Python's cyclic garbage collector paused, as
+    the standard library's timeit does (the collector runs once before).  A
+    full collection of this process's heap takes 40-55 ms on the GPU box's
+    host; one falling inside a 20-step region of config 4 added ~2 ms to the
+    mean step while every step's device time and C++ call time stayed put."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
 
 
 def shuffled_cache(cbis, cache, n_pages, seed):
@@ -418,17 +437,41 @@ def run_c4(args, cbis, oracle):
     # per-step host work (checks, slot resolution, block tables, one H2D copy).
     tok, pos, sid = (np.asarray(st[k], dtype=np.int32) for k in ("tok", "pos", "sid"))
     step = lambda: runner.forward_step_greedy(tok, pos, sid)
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    ms_step = dt * 1000.0 / args.steps
+    # Every step is timed twice: host wall time around the call (the step
+    # returns after its tokens are back on the host) and the device time of
+    # its forward between two events on the runner's stream.  The collector
+    # is paused from before the warmup, whose steps absorb the idle GPU's
+    # slower first step after the collection.
+    wall, dev, host = [], [], []
+    with gc_paused():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            t1 = time.perf_counter()
+            step()
+            wall.append((time.perf_counter() - t1) * 1000.0)
+            dev.append(runner.last_device_ms())
+            host.append(runner.last_host_ms())
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
     value = 192.0 * args.steps / dt
-    _log(f"c4 step {ms_step:.3f} ms -> {value:.1f} decode tok/s ({1216 * args.steps / dt:.0f} rows/s)")
+    stats = {"wall_median": float(np.median(wall)), "wall_mean": float(np.mean(wall)), "wall_min": min(wall),
+             "wall_max": max(wall), "device_median": float(np.median(dev)), "device_min": min(dev),
+             "device_max": max(dev), "region_mean": dt * 1000.0 / args.steps}
+    stats = {k: round(v, 4) for k, v in stats.items()}
+    ms_step = stats["wall_median"]
+    _log("c4 per-step wall ms: " + " ".join(f"{x:.3f}" for x in wall))
+    _log("c4 per-step device ms: " + " ".join(f"{x:.3f}" for x in dev))
+    med = float(np.median(wall))
+    for i, (w_, d_, h_) in enumerate(zip(wall, dev, host)):
+        if w_ > med + 1.0:
+            _log(f"c4 slow step {i}: wall {w_:.3f} ms, device {d_:.3f} ms; host phases: prepare + H2D "
+                 f"{h_[0]:.3f}, launch {h_[1]:.3f}, wait {h_[2]:.3f} ms")
+    _log(f"c4 step median {ms_step:.3f} ms (mean over the region {stats['region_mean']:.3f}, device median "
+         f"{stats['device_median']:.3f}) -> {value:.1f} decode tok/s over the region "
+         f"({1216 * args.steps / dt:.0f} rows/s)")
     att_ms, att_bytes = decode_attention_timing(cbis, st, max(10, args.steps))
     att_gbs = att_bytes / att_ms / 1e6
     _log(f"decode attention (1 layer): {att_ms:.4f} ms, {att_bytes / 1e9:.3f} GB -> {att_gbs:.0f} GB/s")
@@ -447,6 +490,7 @@ def run_c4(args, cbis, oracle):
         "value": round(value, 2),
         "unit": "decode tokens/s",
         "ms_per_step": round(ms_step, 4),
+        "step_ms": stats,
         "dtype": "bf16",
         "data": "synthetic (seeded weights N(0,0.02); K/V cache N(0,1); random token ids)",
         "config": {"workload": "c4_mixed_step", "model": "gpt-mid L16 d2048 h64x32 mlp8192 V32000",
@@ -551,13 +595,14 @@ def run_c1(args, cbis, oracle):
     runner = cbis.TransformerRunner(w, cache, 512)
     prompts = [r.prompt for r in reqs]
     dl = [r.decode_len for r in reqs]
-    for _ in range(max(1, args.warmup)):
-        cbis.run_continuous(runner, cache, prompts, dl)
     dec, tot, toks = [], [], None
-    for _ in range(args.steps):
-        toks, ms = cbis.run_continuous(runner, cache, prompts, dl)
-        dec.append(sum(ms[1:]))
-        tot.append(sum(ms))
+    with gc_paused():
+        for _ in range(max(1, args.warmup)):
+            cbis.run_continuous(runner, cache, prompts, dl)
+        for _ in range(args.steps):
+            toks, ms = cbis.run_continuous(runner, cache, prompts, dl)
+            dec.append(sum(ms[1:]))
+            tot.append(sum(ms))
     n_dec = sum(d - 1 for d in dl)
     n_prompt = sum(len(p) for p in prompts)
     dec_ms, tot_ms = float(np.median(dec)), float(np.median(tot))
@@ -584,13 +629,11 @@ def run_c1(args, cbis, oracle):
             "cpu_baseline": cpu}
 
 
-def run_c5(args, cbis, oracle):
-    """Config 5: the mid-size GPT with fp8-e4m3 linear weights (per-channel
-    fp32 scales) and a bf16 paged K/V cache; 16 sequences whose caches hold
-    32704 synthetic tokens greedy-decode 64 tokens each at positions
-    32704..32767 (the last one is kMaxSeqLen - 1).  A step is 16 rows;
-    value = 16 * 64 / wall time of the 64 steps (median over `steps` runs)."""
-    import torch
+def c5_setup(cbis, oracle):
+    """Config 5's model, cache and sequences as run_c5 times them: fp8
+    weights, a bf16 cache of 16 x 2048 + 64 pages filled N(0, 1) over a
+    shuffled free list, 16 sequences owning positions 0..32767, and their
+    first tokens; decode runs at positions ctx .. ctx + gen - 1."""
     n_seq, ctx, gen = 16, 32768 - 64, 64
     cfg = cbis.ModelConfig.make(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=16, mlp=8192,
                                 max_seq=32768, weight_dtype="fp8", kv_dtype="bf16")
@@ -609,6 +652,19 @@ def run_c5(args, cbis, oracle):
     _log(f"c5 setup {time.time() - t0:.1f}s: weights {w.device_bytes() / 1e9:.2f} GB, "
          f"kv {pages} pages x 16 layers ({cache.max_pages() * 16 * 2048 * 2 * 2 * 16 / 1e9:.1f} GB)")
     first = [int(t) for t in oracle.uniform_int(0, 5003, n_seq, 0, 31999)]
+    return dict(cfg=cfg, w=w, cache=cache, runner=runner, seqs=seqs, first=first, n_seq=n_seq, ctx=ctx, gen=gen)
+
+
+def run_c5(args, cbis, oracle):
+    """Config 5: the mid-size GPT with fp8-e4m3 linear weights (per-channel
+    fp32 scales) and a bf16 paged K/V cache; 16 sequences whose caches hold
+    32704 synthetic tokens greedy-decode 64 tokens each at positions
+    32704..32767 (the last one is kMaxSeqLen - 1).  A step is 16 rows;
+    value = 16 * 64 / wall time of the 64 steps (median over `steps` runs)."""
+    import torch
+    st = c5_setup(cbis, oracle)
+    runner, cache, seqs, first = st["runner"], st["cache"], st["seqs"], st["first"]
+    n_seq, ctx, gen = st["n_seq"], st["ctx"], st["gen"]
 
     def run():
         toks = first
@@ -616,15 +672,16 @@ def run_c5(args, cbis, oracle):
             toks = runner.forward_step_greedy(toks, [ctx + i] * n_seq, seqs)
         return toks
 
-    for _ in range(max(1, args.warmup)):
-        run()
     times = []
-    for _ in range(args.steps):
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        run()
-        torch.cuda.synchronize()
-        times.append(time.perf_counter() - t1)
+    with gc_paused():
+        for _ in range(max(1, args.warmup)):
+            run()
+        for _ in range(args.steps):
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            run()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t1)
     dt = float(np.median(times))
     value = n_seq * gen / dt
     _log(f"c5: {gen} steps in {dt * 1000:.2f} ms -> {value:.1f} tok/s ({dt * 1000 / gen:.3f} ms/step)")
@@ -882,8 +939,8 @@ def main():
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": res["dtype"], "data": res["data"], "config": res["config"],
-            "roofline": res["roofline"], "gemm_roofline": res["gemm_roofline"], "cpu_baseline": res["cpu_baseline"],
-            "machine": res["machine"]}
+            "step_ms": res["step_ms"], "roofline": res["roofline"], "gemm_roofline": res["gemm_roofline"],
+            "cpu_baseline": res["cpu_baseline"], "machine": res["machine"]}
     print(json.dumps(line), flush=True)
 
 

@@ -236,6 +236,12 @@ int cbis_runner_forward_step_greedy(cbis_runner* r, int n, const int* token_ids,
 
 const float* cbis_runner_logits_device(cbis_runner* r) { return r->impl->logits_device(); }
 
+float cbis_runner_last_device_ms(const cbis_runner* r) { return r->impl->last_device_ms(); }
+
+void cbis_runner_last_host_ms(const cbis_runner* r, double out[3]) {
+  for (int i = 0; i < 3; ++i) out[i] = r->impl->last_host_ms()[i];
+}
+
 void* cbis_runner_stream(cbis_runner* r) { return (void*)r->impl->stream(); }
 
 void cbis_runner_set_graphs(cbis_runner* r, int enable) { r->impl->set_graphs(enable != 0); }

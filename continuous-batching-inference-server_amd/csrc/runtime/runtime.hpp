@@ -166,7 +166,15 @@ class TransformerRunner {
   // each row's top-2 margin (max logit minus the runner-up).
   std::vector<int> forward_step_greedy(const std::vector<int>& token_ids, const std::vector<int>& positions,
                                        const std::vector<int>& seq_ids);
+  // Empty after a plain forward_step: margins belong to greedy steps only.
   const std::vector<float>& last_margins() const { return margins_; }
+  // Device time of the last step's forward (embedding through lm_head and
+  // the argmax, between two events on the runner's stream; the metadata H2D
+  // before it and the result D2H after it are not included), in ms.
+  float last_device_ms() const { return last_device_ms_; }
+  // Host wall time of the last step's phases, in ms: {host preparation and
+  // the metadata H2D enqueue, the forward's launch, the wait for its results}.
+  const double* last_host_ms() const { return host_ms_; }
   // Device logits of the last forward_step (not of a greedy step).
   const float* logits_device() const { return d_logits_; }
   hipStream_t stream() const { return stream_; }
@@ -180,12 +188,16 @@ class TransformerRunner {
   void prepare(const int* tok, const int* pos, const int* seq, int M);
   void enqueue_forward(bool greedy);
   void run_step(bool greedy);
+  void timed_step(bool greedy);
 
   const ModelWeights& w_;
   PagedKVCache& cache_;
   ModelConfig cfg_;
   int max_rows_;
   hipStream_t stream_ = nullptr;
+  hipEvent_t ev_start_ = nullptr, ev_stop_ = nullptr;
+  float last_device_ms_ = 0.f;
+  double host_ms_[3] = {0, 0, 0};
   bool use_graphs_ = true;
 
   // metadata staging (pinned host, one H2D per step)
@@ -201,6 +213,7 @@ class TransformerRunner {
   void* d_h_ = nullptr;
   float* d_logits_ = nullptr;
   int* d_next_ = nullptr;  // [M] tokens then [M] margins (fp32) of a greedy step
+  int* h_next_ = nullptr;  // pinned host copy of d_next_
   void* d_amax_ws_ = nullptr;  // cbis_gemm_argmax partials
   size_t amax_ws_bytes_ = 0;
   std::vector<float> margins_;

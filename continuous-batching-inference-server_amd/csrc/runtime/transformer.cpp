@@ -16,6 +16,7 @@
 //  * forward_step_greedy runs lm_head fused with the row argmax and top-2
 //    margin on the device (no logits stored where the GEMM reduces them).
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 #include <unordered_map>
 
@@ -41,6 +42,8 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   // The attention kernels are built for head_dim 32 (any head count).
   if (cfg_.head_dim != 32) throw std::invalid_argument("TransformerRunner: attention needs head_dim 32");
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  hip_check(hipEventCreate(&ev_start_), "hipEventCreate");
+  hip_check(hipEventCreate(&ev_stop_), "hipEventCreate");
   const size_t R = max_total_rows, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
   const size_t ae = dtype_size(cfg_.act_dtype());
   hip_check(hipMalloc((void**)&d_x_, R * D * 4), "hipMalloc x");
@@ -52,6 +55,9 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   // Greedy results: a step's M tokens, then its M margins right after them
   // (one D2H copy brings both back).
   hip_check(hipMalloc((void**)&d_next_, R * 8), "hipMalloc next");
+  // Pinned, so the per-step D2H of the results is a plain DMA (a pageable
+  // destination makes the runtime stage or lock host pages on every copy).
+  hip_check(hipHostMalloc((void**)&h_next_, R * 8, 0), "hipHostMalloc next");
   // Split-KV partials: the automatic split keeps rows * splits <= 2048 + rows.
   ws_bytes_ = (2048 + R) * (size_t)cfg_.n_heads * (cfg_.head_dim + 4) * 4;
   hip_check(hipMalloc(&d_ws_, ws_bytes_), "hipMalloc attention workspace");
@@ -81,6 +87,8 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
 TransformerRunner::~TransformerRunner() {
   for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
   if (stream_) (void)hipStreamDestroy(stream_);
+  if (ev_start_) (void)hipEventDestroy(ev_start_);
+  if (ev_stop_) (void)hipEventDestroy(ev_stop_);
   (void)hipFree(d_x_); (void)hipFree(d_xn_); (void)hipFree(d_q_); (void)hipFree(d_attn_);
   (void)hipFree(d_h_); (void)hipFree(d_logits_); (void)hipFree(d_next_);
   (void)hipFree(d_ws_);
@@ -88,6 +96,7 @@ TransformerRunner::~TransformerRunner() {
   if (d_gemm_ws_) (void)hipFree(d_gemm_ws_);
   (void)hipFree(d_meta_);
   if (h_meta_) (void)hipHostFree(h_meta_);
+  if (h_next_) (void)hipHostFree(h_next_);
 }
 
 void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, int M) {
@@ -389,37 +398,53 @@ void TransformerRunner::run_step(bool greedy) {
   hip_check(hipGraphLaunch(it->second.exec, stream_), "hipGraphLaunch");
 }
 
+void TransformerRunner::timed_step(bool greedy) {
+  hip_check(hipEventRecord(ev_start_, stream_), "hipEventRecord");
+  run_step(greedy);
+  hip_check(hipEventRecord(ev_stop_, stream_), "hipEventRecord");
+}
+
 std::vector<float> TransformerRunner::forward_step(const std::vector<int>& token_ids, const std::vector<int>& positions,
                                                    const std::vector<int>& seq_ids) {
+  margins_.clear();
   const int M = (int)token_ids.size();
   if (M == 0) return {};
   if ((int)positions.size() != M || (int)seq_ids.size() != M)
     throw std::invalid_argument("forward_step: token_ids/positions/seq_ids sizes differ");
   prepare(token_ids.data(), positions.data(), seq_ids.data(), M);
-  run_step(false);
+  timed_step(false);
   std::vector<float> logits((size_t)M * cfg_.vocab);
   hip_check(hipMemcpyAsync(logits.data(), d_logits_, logits.size() * 4, hipMemcpyDeviceToHost, stream_), "D2H logits");
   hip_check(hipStreamSynchronize(stream_), "forward_step sync");
+  hip_check(hipEventElapsedTime(&last_device_ms_, ev_start_, ev_stop_), "hipEventElapsedTime");
   return logits;
 }
 
 std::vector<int> TransformerRunner::forward_step_greedy(const std::vector<int>& token_ids,
                                                         const std::vector<int>& positions,
                                                         const std::vector<int>& seq_ids) {
+  margins_.clear();
   const int M = (int)token_ids.size();
   if (M == 0) return {};
   if ((int)positions.size() != M || (int)seq_ids.size() != M)
     throw std::invalid_argument("forward_step_greedy: token_ids/positions/seq_ids sizes differ");
+  using clk = std::chrono::steady_clock;
+  const auto t0 = clk::now();
   prepare(token_ids.data(), positions.data(), seq_ids.data(), M);
-  run_step(true);
-  std::vector<int> both(2 * (size_t)M);
-  hip_check(hipMemcpyAsync(both.data(), d_next_, (size_t)M * 8, hipMemcpyDeviceToHost, stream_),
+  const auto t1 = clk::now();
+  timed_step(true);
+  hip_check(hipMemcpyAsync(h_next_, d_next_, (size_t)M * 8, hipMemcpyDeviceToHost, stream_),
             "D2H tokens and margins");
+  const auto t2 = clk::now();
   hip_check(hipStreamSynchronize(stream_), "forward_step_greedy sync");
-  margins_.resize(M);
-  std::memcpy(margins_.data(), both.data() + M, (size_t)M * 4);
-  both.resize(M);
-  return both;
+  const auto t3 = clk::now();
+  hip_check(hipEventElapsedTime(&last_device_ms_, ev_start_, ev_stop_), "hipEventElapsedTime");
+  auto ms = [](clk::duration d) { return std::chrono::duration<double, std::milli>(d).count(); };
+  host_ms_[0] = ms(t1 - t0);
+  host_ms_[1] = ms(t2 - t1);
+  host_ms_[2] = ms(t3 - t2);
+  margins_.assign((const float*)(h_next_ + M), (const float*)(h_next_ + M) + M);
+  return std::vector<int>(h_next_, h_next_ + M);
 }
 
 }  // namespace cbis

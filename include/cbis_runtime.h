@@ -97,8 +97,17 @@ int cbis_runner_forward_step(cbis_runner* r, int n, const int* token_ids, const 
 int cbis_runner_forward_step_greedy(cbis_runner* r, int n, const int* token_ids, const int* positions,
                                     const int* seq_ids, int* next_tokens);
 /* Top-2 margins (max logit minus the runner-up) of the last greedy step's
- * rows (no reference counterpart): writes min(capacity, n); returns n. */
+ * rows (no reference counterpart): writes min(capacity, n); returns n, which
+ * is 0 after a plain forward_step. */
 int cbis_runner_last_margins(const cbis_runner* r, float* out, int capacity);
+/* Device time in ms of the last step's forward (no reference counterpart: a
+ * diagnostic): two events on the runner's stream around the forward's
+ * kernels, after the step's metadata H2D and before its result D2H. */
+float cbis_runner_last_device_ms(const cbis_runner* r);
+/* Host wall time in ms of the last greedy step's phases (no reference
+ * counterpart: a diagnostic): out[0] host preparation and the metadata H2D
+ * enqueue, out[1] the forward's launch, out[2] the wait for its results. */
+void cbis_runner_last_host_ms(const cbis_runner* r, double out[3]);
 /* Device pointer of the last forward_step's [n, vocab] fp32 logits. */
 const float* cbis_runner_logits_device(cbis_runner* r);
 /* hipStream_t the runner launches on. */
