@@ -21,7 +21,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(HERE, "lib")
 KERNELS_SO = os.path.join(LIB_DIR, "libcbis_kernels.so")
-RUNTIME_SO = os.path.join(LIB_DIR, "libcbis.so")
+# CBIS_RUNTIME_SO selects another build of the runtime library (the host
+# sanitizer build, `make sanitize`).
+RUNTIME_SO = os.environ.get("CBIS_RUNTIME_SO") or os.path.join(LIB_DIR, "libcbis.so")
 
 F32, BF16, FP8E4M3 = 0, 1, 2
 EPI_NONE, EPI_GELU = 0, 1
@@ -142,6 +144,8 @@ RUNTIME_SYMBOLS = {
     "cbis_runner_stream": (_P, [_P]),
     "cbis_runner_set_graphs": (None, [_P, _I]),
     "cbis_runner_last_plan": (_I, [_P, _IP, _I]),
+    "cbis_runner_last_device_ms": (ctypes.c_float, [_P]),
+    "cbis_runner_last_host_ms": (None, [_P, ctypes.POINTER(ctypes.c_double)]),
     "cbis_runner_last_margins": (_I, [_P, ctypes.POINTER(ctypes.c_float), _I]),
     "cbis_run_continuous": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _IP, ctypes.POINTER(ctypes.c_double), _I]),
     "cbis_eviction_params_default": (None, [ctypes.POINTER(EvictionParams)]),
@@ -398,6 +402,18 @@ class TransformerRunner:
 
     def logits_device(self) -> int:
         return runtime().cbis_runner_logits_device(self._h)
+
+    def last_device_ms(self) -> float:
+        """Device time of the last step's forward (events on the runner's
+        stream around its kernels; the H2D / D2H of the step excluded)."""
+        return float(runtime().cbis_runner_last_device_ms(self._h))
+
+    def last_host_ms(self):
+        """Host wall time of the last greedy step's phases: (preparation +
+        H2D enqueue, launch, wait for the results), ms."""
+        out = (ctypes.c_double * 3)()
+        runtime().cbis_runner_last_host_ms(self._h, out)
+        return tuple(out)
 
     def stream(self) -> int:
         return runtime().cbis_runner_stream(self._h) or 0

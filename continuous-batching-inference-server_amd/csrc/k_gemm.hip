@@ -103,7 +103,11 @@ constexpr int kLnMaxChunks = kLnPrologueMaxK / 256;  // float4 chunks per lane o
 // Top-2 of a row: the maximum m1 at the lowest index i1 among equal maxima
 // (the strict-> scan of src/bench_batching.cpp:66-73), and the largest value
 // m2 at any other index (m2 == m1 when the maximum is tied).  NaN never
-// wins.  Start from m1 = m2 = -inf, i1 = INT_MAX.  top2_push takes one lane's
+// wins, except at column 0: the reference's scan starts from the row's first
+// value and no comparison with a NaN there succeeds, so a NaN at column 0 is
+// the row's answer -- the callers push it as +inf (nan0_as_inf), which wins
+// every comparison and keeps the lowest index among equal maxima.  Start
+// from m1 = m2 = -inf, i1 = INT_MAX.  top2_push takes one lane's
 // columns in increasing order, so a value equal to the maximum never
 // displaces it (the strict > keeps the lowest index); a lane that sees only
 // -inf keeps i1 = INT_MAX, which the merges rank after every real index.
@@ -113,6 +117,7 @@ __device__ inline void top2_push(float& m1, float& m2, int& i1, float v, int c) 
   i1 = up ? c : i1;
   m1 = up ? v : m1;
 }
+__device__ inline float nan0_as_inf(float v, int c) { return (c == 0 && v != v) ? INFINITY : v; }
 // Merges another partial (b1, b2, bi) of disjoint columns; order-free.
 __device__ inline void top2_merge(float& m1, float& m2, int& i1, float b1, float b2, int bi) {
   if (b1 > m1 || (b1 == m1 && bi < i1)) {
@@ -1084,6 +1089,7 @@ __device__ inline void epilogue_top2_rows(const GemmArgs& g, const Top2Cols<BN>&
             v = hb ? xb : v;
           }
           if constexpr (CHECK) v = c < g.N ? v : -INFINITY;  // -inf: no effect on the top-2
+          if (k == 0 && e == 0) v = nan0_as_inf(v, c);       // only lane 0 of the first tile holds column 0
           top2_push(m1, m2, i1, v, c);
         }
       }
@@ -1598,6 +1604,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
         float x = v[e];
         if (g.w_scale) x *= sc;
         if (g.bias) x += bi;
+        x = nan0_as_inf(x, col);
         float m1 = ok ? x : -INFINITY, m2 = -INFINITY;
         int i1 = ok ? col : 0x7FFFFFFF;
         top2_row16(m1, m2, i1);
@@ -1631,7 +1638,7 @@ __global__ __launch_bounds__(256) void top2_reduce_kernel(const void* src, int n
   if (row < M) {
     if constexpr (RAW) {
       const float* r = (const float*)src + (int64_t)row * ld;
-      for (int c = t; c < n_parts; c += TPR) top2_push(m1, m2, i1, r[c], c);
+      for (int c = t; c < n_parts; c += TPR) top2_push(m1, m2, i1, nan0_as_inf(r[c], c), c);
     } else {
       const float4* r = (const float4*)src + (int64_t)row * ld;
       for (int c = t; c < n_parts; c += TPR) {

@@ -141,6 +141,9 @@ __global__ __launch_bounds__(256) void scatter_kv_kernel(int rows, int D, const 
 // ---------------------------------------------------------------------------
 // Greedy argmax: one 256-thread block per row; (value, index) pairs reduced
 // with the lowest index winning ties, as a sequential strict-> scan does.
+// NaN never wins, except at column 0: that scan starts from the row's first
+// value, and no comparison with a NaN succeeds, so a NaN there is the row's
+// answer (taken as +inf below, which keeps the lowest index among equals).
 // ---------------------------------------------------------------------------
 __device__ inline void argmax_combine(float& v, int& i, float v2, int i2) {
   if (v2 > v || (v2 == v && i2 < i)) {
@@ -161,6 +164,10 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int N, const flo
   const float* row = L + (int64_t)blockIdx.x * ld;
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
+  if (threadIdx.x == 0 && N > 0 && row[0] != row[0]) {
+    bv = INFINITY;
+    bi = 0;
+  }
   if (((N | ld) & 3) == 0 && ((uintptr_t)L & 15) == 0) {
     const int n4 = N >> 2;
     constexpr int U = 8;

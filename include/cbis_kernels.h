@@ -156,7 +156,10 @@ int cbis_gemm_layernorm(const cbis_gemm_desc* d, const float* ln_gamma, const fl
  * next_token[r] = the first index of the maximum of row r of
  * Y = X . W^T * w_scale + bias (strict >, as argmax_row), and, when margin is
  * not NULL, margin[r] = that maximum minus the largest value at any other
- * index (0 for a tied maximum).  The kernels that reduce in their epilogue
+ * index (0 for a tied maximum).  NaN logits never win, except at column 0:
+ * the reference's scan starts from the row's first value, so a NaN there makes
+ * the token 0 (its margin is then +inf, or NaN when another logit is +inf).
+ * The kernels that reduce in their epilogue
  * (M <= 64, and bf16 weights on the wave-specialised tilings) never store Y;
  * the others store the logits in d->Y (when it is an fp32 [M, N] buffer) or
  * the workspace and reduce them.  The epilogue must be scale and bias only
@@ -273,7 +276,9 @@ int cbis_layernorm_gemm(const cbis_gemm_desc* d, const float* x, int64_t ldx, co
                         const float* ln_beta, float eps, cbis_stream_t stream);
 
 /* out[r] = first index of the maximum of logits[r, 0:N] (strict >), the
- * greedy rule of src/bench_batching.cpp:66-73. */
+ * greedy rule of src/bench_batching.cpp:66-73, NaN included: a NaN at column
+ * 0 gives 0 (the scan's first value is never displaced), NaN elsewhere never
+ * wins. */
 int cbis_argmax_rows(int T, int N, const float* logits, int64_t ld, int* out, cbis_stream_t stream);
 
 /* ----------------------------------------------------------------------- */

@@ -1039,6 +1039,122 @@ def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows, tile):
     assert np.abs(got - ref).mean() < 2e-3
 
 
+def _lazy_raises(scores, qpos, kv_end, waves=2, thr=8.0):
+    """The prefill kernel's lazy softmax reference, simulated per query row:
+    a head's waves take its 32-key blocks round-robin (wave w: blocks w,
+    w + waves, ...), m starts at -inf, a block's first unmasked key sets m,
+    and a finite m is raised only when the block's maximum over the row's
+    visible keys exceeds it by more than `thr` (log2 units).  scores
+    [rows, keys] in log2 units.  Returns, per row, how many finite-m raises
+    its waves made."""
+    n_rows = scores.shape[0]
+    out = np.zeros(n_rows, np.int64)
+    nblk = (kv_end + 31) // 32
+    for r in range(n_rows):
+        vis = min(int(qpos[r]) + 1, kv_end)
+        for w in range(waves):
+            m = -np.inf
+            for b in range(w, nblk, waves):
+                lo, hi = 32 * b, min(32 * b + 32, vis)
+                if hi <= lo:
+                    continue
+                smax = scores[r, lo:hi].max()
+                if m == -np.inf:
+                    m = smax
+                elif smax - m > thr:
+                    m = smax
+                    out[r] += 1
+    return out
+
+
+@pytest.mark.parametrize("mode", ["planted", "q_scaled"])
+def test_prefill_attention_lazy_rescale(cbis, oracle, dev, mode):
+    """Inputs whose later key blocks dominate, so a wave's finite softmax
+    reference m is raised mid-sequence (o and the row sums rescaled by
+    2^(m_old - m_new), the block's scores shifted, -m reloaded) -- a path
+    N(0, 1) inputs never take (their scaled scores spread ~1.4 log2 units).
+
+    planted: every query row of a head is the same vector u and key j is
+    a_j u / |u|^2 / qscale, so its score is a_j log2 units: ~400 flat keys
+    (a ~ N(0, 0.3)), then one spike key per wave at +9.5, past the 8-unit
+    threshold.  The flat keys then still carry ~20% of the softmax mass
+    after the rescale, so a wrong correction factor moves the output by
+    several percent.  q_scaled: Q ~ N(0, 16) (scores spread ~5.8 log2
+    units), K / V ~ N(0, 1).  Both: 100 query rows after 380 cached keys,
+    tiles of 64 (the second ragged), blocks straddling the causal diagonal.
+    A host simulation of the kernel's block order asserts the raises happen.
+    The output is checked against the fp64 oracle with the per-row metric,
+    and, tighter, against the oracle given the kernel's bf16-rounded Q (the
+    scaled Q is an MFMA operand; at scores of tens of log2 units its
+    rounding alone moves the softmax weights by a few percent, which is not
+    what this test is about)."""
+    import torch
+    H, P, cached, n_rows, HD = 64, 64, 380, 100, 32
+    qscale = np.log2(np.e) / np.sqrt(HD)
+    total = cached + n_rows
+    npages = (total + 15) // 16
+    bt = rng(71).permutation(P)[:npages].astype(np.int32)[None, :]
+    g = rng(72)
+    v = g.standard_normal((total, H, HD)).astype(np.float32)
+    if mode == "planted":
+        u = g.standard_normal((H, HD))
+        a = g.normal(0.0, 0.3, total)
+        spikes = [405, 440]  # key blocks 12 (wave 0) and 13 (wave 1)
+        a[spikes] = 9.5
+        k = (a[:, None, None] * u[None] / (u * u).sum(-1)[None, :, None] / qscale).astype(np.float32)
+        qh = np.broadcast_to(u[None], (n_rows, H, HD)).astype(np.float32).reshape(n_rows, H * HD)
+    else:
+        k = g.standard_normal((total, H, HD)).astype(np.float32)
+        qh = (4.0 * g.standard_normal((n_rows, H * HD))).astype(np.float32)
+    kd, kvals = bf16_dev(k, dev)
+    vd, _ = bf16_dev(v, dev)
+    kp = torch.zeros((P, 16, H, HD), dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros_like(kp)
+    for j in range(npages):
+        n = min(16, total - 16 * j)
+        kp[int(bt[0, j]), :n] = kd[16 * j: 16 * j + n]
+        vp[int(bt[0, j]), :n] = vd[16 * j: 16 * j + n]
+    q = to_dev(qh, dev)
+    pos = (cached + np.arange(n_rows)).astype(np.int32)
+    tiles = []
+    for r in range(0, n_rows, 64):
+        tiles += [r, min(64, n_rows - r), 0, cached + r]
+    T = to_dev(np.array(tiles, np.int32), dev)
+    out = torch.empty((n_rows, H * HD), dtype=torch.bfloat16, device=dev)
+    d = _attn_desc(cbis, n_rows, H, q, kp, vp, P, to_dev(bt, dev), bt.shape[1], None, out, cbis.BF16,
+                   out_dtype=cbis.BF16)
+    cbis.check(cbis.kernels().cbis_paged_prefill_attention(ctypes.byref(d), len(tiles) // 4, ptr(T), stream()))
+    sync()
+    # The raises the kernel's block order makes, from the bf16 operands it
+    # reads (Q rounded after the scale, as the kernel does).
+    qb = torch.from_numpy(qh * np.float32(qscale)).to(torch.bfloat16).float().numpy().reshape(n_rows, H, HD)
+    raises = np.zeros(n_rows, np.int64)
+    for h in range(H):
+        s = qb[:, h, :].astype(np.float64) @ kvals[:, h, :].astype(np.float64).T
+        raises += _lazy_raises(s, pos, total)
+    rows_raised = int((raises > 0).sum())
+    ref = oracle.paged_attention(qh, bits_u16(kp), bits_u16(vp), np.repeat(bt, n_rows, 0), pos, H, HD, 16,
+                                 kv_dtype=1)
+    got = out.float().cpu().numpy()
+    err_row = row_rel_err(got, ref)
+    err_head = row_rel_err(got.reshape(n_rows * H, HD), ref.reshape(n_rows * H, HD))
+    q_rounded = (qb.reshape(n_rows, H * HD) / np.float32(qscale)).astype(np.float32)
+    ref_qb = oracle.paged_attention(q_rounded, bits_u16(kp), bits_u16(vp), np.repeat(bt, n_rows, 0), pos, H, HD,
+                                    16, kv_dtype=1)
+    err_qb = row_rel_err(got, ref_qb)
+    print(f"prefill lazy rescale ({mode}): {int(raises.sum())} finite-m raises over {rows_raised} rows; "
+          f"per-row rel {err_row:.3e}, per-(row, head) rel {err_head:.3e}; against bf16-Q oracle {err_qb:.3e}",
+          flush=True)
+    assert err_qb < 1e-2
+    if mode == "planted":
+        # every row past a spike raises in the wave that holds it, every head
+        assert (raises[pos >= 405] >= H).all() and (raises[pos >= 440] >= 2 * H).all()
+    else:
+        assert rows_raised >= n_rows // 2
+    assert err_row < LOWP_TOL
+    assert err_head < LOWP_TOL * 2
+
+
 @pytest.mark.parametrize("kv_dtype,H", [("f32", 12), ("f32", 4), ("bf16", 24), ("bf16", 8)])
 def test_decode_attention_any_head_count(cbis, oracle, dev, kv_dtype, H):
     """Head counts that do not fill the last 1 KiB head block (8 fp32 or 16
@@ -1207,3 +1323,73 @@ def test_gemm_argmax_matches_logits(cbis, oracle, dev, M, N, K, wdt):
     assert (idx[:4] == 37).all() and (margin[:4] == 0).all()
     if need >= 16:
         assert K_.cbis_gemm_argmax(ctypes.byref(d), ptr(nxt), ptr(mar), ptr(ws), need - 16, stream()) == 3
+
+
+@pytest.mark.parametrize("M,N,K,wdt", [
+    (7, 32000, 2048, "bf16"),     # skinny kernel
+    (16, 4000, 512, "fp8"),       # skinny, fp8 codes with channel scales
+    (8, 512, 256, "f32"),         # skinny fp32
+    (300, 32000, 512, "bf16"),    # wave-specialised (greedy epilogue)
+    (100, 1000, 256, "bf16"),     # small grid: logits stored, then reduced
+    (100, 512, 256, "f32"),       # fp32 at M > 64: stored, then reduced
+])
+@pytest.mark.parametrize("nan_col", ["first", "middle"])
+def test_argmax_nan_rule(cbis, oracle, dev, M, N, K, wdt, nan_col):
+    """A NaN logit (planted through the bias, so every row has it in the same
+    column) follows the reference's scan (src/bench_batching.cpp:66-73, whose
+    first value is never displaced since no comparison with NaN succeeds): at
+    column 0 the token is 0 (margin +inf); elsewhere it never wins and the
+    margin is the top two of the other columns.  cbis_gemm_argmax on every
+    path, and cbis_argmax_rows over the stored logits, against
+    orc_argmax_rows."""
+    import torch
+    K_ = cbis.kernels()
+    w = oracle.normal(73, 2, N * K, 0.02).reshape(N, K)
+    x = oracle.normal(73, 1, M * K).reshape(M, K)
+    b = oracle.normal(73, 3, N, 0.02)
+    col = 0 if nan_col == "first" else N // 2 + 3
+    b[col] = np.nan
+    if wdt == "f32":
+        X, W, xdt, wd, S = to_dev(x, dev), to_dev(w, dev), cbis.F32, cbis.F32, None
+    elif wdt == "bf16":
+        (X, _), (W, _) = bf16_dev(x, dev), bf16_dev(w, dev)
+        xdt, wd, S = cbis.BF16, cbis.BF16, None
+    else:
+        codes, sc = oracle.quantize_e4m3_rows(w)
+        (X, _), W, S = bf16_dev(x, dev), to_dev(codes, dev), to_dev(sc, dev)
+        xdt, wd = cbis.BF16, cbis.FP8E4M3
+    B = to_dev(b, dev)
+    Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    d = cbis.GemmDesc()
+    d.M, d.N, d.K = M, N, K
+    d.x_dtype, d.X, d.ldx = xdt, ptr(X), K
+    d.w_dtype, d.W, d.ldw = wd, ptr(W), K
+    d.w_scale, d.bias = ptr(S), ptr(B)
+    d.y_dtype, d.Y, d.ldy = cbis.F32, ptr(Y), N
+    gneed = K_.cbis_gemm_workspace_size(ctypes.byref(d))
+    gws = torch.empty(max(1, gneed // 4), dtype=torch.float32, device=dev)
+    d.workspace, d.workspace_bytes = ptr(gws), gneed
+    cbis.check(K_.cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
+    sync()
+    d.workspace, d.workspace_bytes = None, 0
+    logits = Y.cpu().numpy()
+    assert np.isnan(logits[:, col]).all() and not np.isnan(np.delete(logits, col, axis=1)).any()
+    want = oracle.argmax_rows(logits)
+    rows = torch.full((M,), -1, dtype=torch.int32, device=dev)
+    cbis.check(K_.cbis_argmax_rows(M, N, ptr(Y), N, ptr(rows), stream()), "cbis_argmax_rows")
+    need = K_.cbis_gemm_argmax_workspace_size(ctypes.byref(d))
+    ws = torch.empty(max(4, need // 4), dtype=torch.float32, device=dev)
+    nxt = torch.full((M,), -1, dtype=torch.int32, device=dev)
+    mar = torch.full((M,), -1.0, dtype=torch.float32, device=dev)
+    cbis.check(K_.cbis_gemm_argmax(ctypes.byref(d), ptr(nxt), ptr(mar), ptr(ws), need, stream()), "cbis_gemm_argmax")
+    sync()
+    assert np.array_equal(rows.cpu().numpy(), want)
+    assert np.array_equal(nxt.cpu().numpy(), want)
+    if nan_col == "first":
+        assert (want == 0).all() and np.isposinf(mar.cpu().numpy()).all()
+    else:
+        rest = logits.copy()
+        rest[:, col] = -np.inf
+        idx, margin = _top2_np(rest)
+        assert np.array_equal(want, idx)
+        assert np.array_equal(mar.cpu().numpy().view(np.uint32), margin.view(np.uint32))

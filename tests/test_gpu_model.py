@@ -11,7 +11,7 @@ import os
 import numpy as np
 import pytest
 
-from helpers import bits_u16, row_rel_err
+from helpers import bits_u16, check_logits as _check_logits, row_rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -337,23 +337,6 @@ def _big_setup(cbis, oracle, wdt, n_layers, max_pages, max_seq, fill_seed):
     return w, cache, om, ocache
 
 
-def _check_logits(got, ref, what):
-    """north_star's bf16/fp8 bar: per row ||d||_inf / ||ref||_inf <= 2e-2,
-    and the greedy token equal wherever the oracle's top-2 margin exceeds
-    twice the row's measured error."""
-    err = row_rel_err(got, ref)
-    abs_err = np.abs(got - ref).max(axis=1)
-    srt = np.sort(ref, axis=1)
-    margin = srt[:, -1] - srt[:, -2]
-    sure = margin > 2 * abs_err
-    agree = got.argmax(axis=1) == ref.argmax(axis=1)
-    print(f"{what}: rows={len(got)} per-row rel err {err:.3e}, max abs {abs_err.max():.3e}, "
-          f"argmax agrees on {int(agree.sum())}/{len(got)} ({int(sure.sum())} with margin > 2 err)", flush=True)
-    assert err < 2e-2, err
-    assert agree[sure].all()
-    return ref.argmax(axis=1)
-
-
 def test_c4_step_at_config_workload(cbis, oracle):
     """BASELINE config 4's step exactly as bench.py builds it, on 2 of the 16
     layers: 192 decode rows with kv U[256, 4096] (the seed-0 draw) over a
@@ -414,6 +397,7 @@ def test_c5_decode_at_config_workload(cbis, oracle):
     for step in range(3):
         pos = [ctx + step] * n_seq
         got = runner.forward_step(toks, pos, seqs)
+        assert len(runner.last_margins()) == 0  # the previous greedy step's margins are gone
         assert runner.last_plan()["split_tokens"] == 8192
         ref = oracle.forward_step_with_cache(om, ocache, toks, pos, oseqs)
         want = _check_logits(got, ref, f"config 5 step {step} (1 layer)")
