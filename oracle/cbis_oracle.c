@@ -23,7 +23,8 @@
  *   orc_scatter_kv       kernels/attention.cu:7-19
  *   orc_forward_step     src/transformer.cpp:44-99 (op order; scatter before
  *                        attention of the same layer; lm_head without bias,
- *                        python/model.py:61)
+ *                        python/model.py:61), also in parts:
+ *                        orc_step_embed / orc_step_layer / orc_step_head
  *   orc_argmax           src/bench_batching.cpp:66-73 (strict >, first max wins)
  *
  * The synthetic-data PRNG (orc_normal / orc_uniform) and the bf16 / OCP fp8
@@ -110,6 +111,7 @@ uint16_t orc_f32_to_bf16(float f) {
 float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 
 void orc_round_bf16(float* x, int64_t n) {
+#pragma omp parallel for schedule(static) if (n > (1 << 20))
   for (int64_t i = 0; i < n; ++i) x[i] = orc_bf16_to_f32(orc_f32_to_bf16(x[i]));
 }
 
@@ -140,6 +142,23 @@ uint8_t orc_f32_to_e4m3(float f) {
   int code = ((E + 7) << 3) | ((int)q - 8);
   if (code > 0x7E) code = 0x7E;
   return sign | (uint8_t)code;
+}
+
+/* Per-output-channel absmax quantisation of w [N, K] (fp32): scale[n] =
+ * max_k |w[n,k]| / 448 in fp32 (1 for an all-zero row), codes[n,k] =
+ * e4m3_rne(w[n,k] / scale[n]) with the quotient rounded to fp32 first.
+ * BASELINE config 5's weight format; rows in parallel. */
+void orc_quantize_e4m3_rows(int64_t N, int64_t K, const float* w, uint8_t* codes, float* scale) {
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    const float* r = w + n * K;
+    float amax = 0.f;
+    for (int64_t k = 0; k < K; ++k) amax = fabsf(r[k]) > amax ? fabsf(r[k]) : amax;
+    float sc = amax / 448.0f;
+    if (sc == 0.f) sc = 1.0f;
+    scale[n] = sc;
+    for (int64_t k = 0; k < K; ++k) codes[n * K + k] = orc_f32_to_e4m3(r[k] / sc);
+  }
 }
 
 /* ------------------------------------------------------------------------ */
@@ -308,60 +327,84 @@ static void to_float_rounded(const double* src, float* dst, int64_t n, int round
   }
 }
 
-/* One flattened continuous-batch step.  Rows are (token_ids[i], positions[i])
- * with row i's page table at block_table + row_bt[i]*bt_stride; K/V of every
- * row are written into layer l's pools (kpools[l], vpools[l]) at
- * (wpage[i], woff[i]) before layer l's attention runs, as
- * src/transformer.cpp:75-80 orders them.  logits is [M, vocab] (double). */
+/* The step in three parts, so a caller can run it one layer at a time over
+ * that layer's pools alone (a 16-layer pool set need not be on the host at
+ * once): orc_step_embed forms the residual stream x [M, d] (fp64),
+ * orc_step_layer runs layer l on it in place, orc_step_head the final
+ * LayerNorm and lm_head.  orc_forward_step is the three in sequence. */
+void orc_step_embed(const orc_model_t* mdl, int M, const int32_t* token_ids, const int32_t* positions, double* x) {
+  orc_embed(M, mdl->d_model, token_ids, positions, mdl->tok_emb, mdl->pos_emb, x);
+}
+
+/* Layer l of src/transformer.cpp:65-90 on x [M, d] in place.  K/V of every
+ * row are written into this layer's pools (kpool, vpool) at
+ * (wpage[i], woff[i]) before its attention runs, as src/transformer.cpp:75-80
+ * orders them; row i's page table is block_table + row_bt[i] * bt_stride. */
+void orc_step_layer(const orc_model_t* mdl, int l, int M, double* x, const int32_t* positions,
+                    const int32_t* wpage, const int32_t* woff, const int32_t* block_table, int bt_stride,
+                    const int32_t* row_bt, void* kpool, void* vpool) {
+  const int D = mdl->d_model, F = mdl->mlp, H = mdl->n_heads, hd = mdl->head_dim;
+  const int rb = mdl->act_bf16;
+  const orc_layer_t* w = &mdl->layers[l];
+  double* t = (double*)malloc(sizeof(double) * (size_t)M * D);
+  double* kd = (double*)malloc(sizeof(double) * (size_t)M * D);
+  double* vd = (double*)malloc(sizeof(double) * (size_t)M * D);
+  double* hbuf = (double*)malloc(sizeof(double) * (size_t)M * F);
+  float* xf = (float*)calloc((size_t)M * D, sizeof(float));
+  float* af = (float*)malloc(sizeof(float) * (size_t)M * (F > D ? F : D));
+  float* qf = (float*)malloc(sizeof(float) * (size_t)M * D);
+  /* LN1 */
+  to_float_rounded(x, xf, (int64_t)M * D, 0);
+  orc_layernorm(M, D, xf, D, w->ln1_w, w->ln1_b, 1e-5, t, D);
+  to_float_rounded(t, af, (int64_t)M * D, rb);
+  /* Q, K, V */
+  orc_gemm(M, D, D, af, D, w->wq, D, w->sq, w->bq, 0, NULL, 0, t, D);
+  to_float_rounded(t, qf, (int64_t)M * D, 0);
+  orc_gemm(M, D, D, af, D, w->wk, D, w->sk, w->bk, 0, NULL, 0, kd, D);
+  orc_gemm(M, D, D, af, D, w->wv, D, w->sv, w->bv, 0, NULL, 0, vd, D);
+  orc_scatter_kv(M, D, kd, vd, kpool, vpool, mdl->kv_dtype, wpage, woff, mdl->page_size);
+  /* attention */
+  orc_paged_attention(M, H, hd, mdl->page_size, kpool, vpool, mdl->kv_dtype, block_table, bt_stride, row_bt,
+                      positions, qf, D, t, D);
+  to_float_rounded(t, af, (int64_t)M * D, rb);
+  /* out-projection + residual */
+  to_float_rounded(x, xf, (int64_t)M * D, 0);
+  orc_gemm(M, D, D, af, D, w->wo, D, w->so, w->bo, 0, xf, D, x, D);
+  /* LN2, fc1 + GELU, fc2 + residual */
+  to_float_rounded(x, xf, (int64_t)M * D, 0);
+  orc_layernorm(M, D, xf, D, w->ln2_w, w->ln2_b, 1e-5, t, D);
+  to_float_rounded(t, af, (int64_t)M * D, rb);
+  orc_gemm(M, F, D, af, D, w->fc1, D, w->s1, w->b1, 1, NULL, 0, hbuf, F);
+  to_float_rounded(hbuf, af, (int64_t)M * F, rb);
+  orc_gemm(M, D, F, af, F, w->fc2, F, w->s2, w->b2, 0, xf, D, x, D);
+  free(t); free(kd); free(vd); free(hbuf); free(xf); free(af); free(qf);
+}
+
+/* Final LayerNorm and lm_head (no bias, python/model.py:61): logits [M, vocab]. */
+void orc_step_head(const orc_model_t* mdl, int M, const double* x, double* logits) {
+  const int D = mdl->d_model;
+  double* t = (double*)malloc(sizeof(double) * (size_t)M * D);
+  float* xf = (float*)calloc((size_t)M * D, sizeof(float));
+  float* af = (float*)malloc(sizeof(float) * (size_t)M * D);
+  to_float_rounded(x, xf, (int64_t)M * D, 0);
+  orc_layernorm(M, D, xf, D, mdl->ln_f_w, mdl->ln_f_b, 1e-5, t, D);
+  to_float_rounded(t, af, (int64_t)M * D, mdl->act_bf16);
+  orc_gemm(M, mdl->vocab, D, af, D, mdl->lm_head, D, mdl->lm_scale, NULL, 0, NULL, 0, logits, mdl->vocab);
+  free(t); free(xf); free(af);
+}
+
+/* One flattened continuous-batch step, src/transformer.cpp:44-99: rows are
+ * (token_ids[i], positions[i]); layer l uses the pools kpools[l], vpools[l].
+ * logits is [M, vocab] (double). */
 void orc_forward_step(const orc_model_t* mdl, int M, const int32_t* token_ids, const int32_t* positions,
                       const int32_t* wpage, const int32_t* woff, const int32_t* block_table, int bt_stride,
                       const int32_t* row_bt, void* const* kpools, void* const* vpools, double* logits) {
-  const int D = mdl->d_model, F = mdl->mlp, H = mdl->n_heads, hd = mdl->head_dim;
-  const int rb = mdl->act_bf16;
-  double* x = (double*)malloc(sizeof(double) * (size_t)M * D);
-  double* t = (double*)malloc(sizeof(double) * (size_t)M * (F > D ? F : D));
-  double* kd = (double*)malloc(sizeof(double) * (size_t)M * D);
-  double* vd = (double*)malloc(sizeof(double) * (size_t)M * D);
-  float* xf = (float*)malloc(sizeof(float) * (size_t)M * D);
-  float* af = (float*)malloc(sizeof(float) * (size_t)M * (F > D ? F : D));
-  float* qf = (float*)malloc(sizeof(float) * (size_t)M * D);
-
-  orc_embed(M, D, token_ids, positions, mdl->tok_emb, mdl->pos_emb, x);
-  for (int l = 0; l < mdl->n_layers; ++l) {
-    const orc_layer_t* w = &mdl->layers[l];
-    /* LN1 */
-    to_float_rounded(x, xf, (int64_t)M * D, 0);
-    orc_layernorm(M, D, xf, D, w->ln1_w, w->ln1_b, 1e-5, t, D);
-    to_float_rounded(t, af, (int64_t)M * D, rb);
-    /* Q, K, V */
-    orc_gemm(M, D, D, af, D, w->wq, D, w->sq, w->bq, 0, NULL, 0, t, D);
-    to_float_rounded(t, qf, (int64_t)M * D, 0);
-    orc_gemm(M, D, D, af, D, w->wk, D, w->sk, w->bk, 0, NULL, 0, kd, D);
-    orc_gemm(M, D, D, af, D, w->wv, D, w->sv, w->bv, 0, NULL, 0, vd, D);
-    orc_scatter_kv(M, D, kd, vd, kpools[l], vpools[l], mdl->kv_dtype, wpage, woff, mdl->page_size);
-    /* attention */
-    orc_paged_attention(M, H, hd, mdl->page_size, kpools[l], vpools[l], mdl->kv_dtype, block_table,
-                        bt_stride, row_bt, positions, qf, D, t, D);
-    to_float_rounded(t, af, (int64_t)M * D, rb);
-    /* out-projection + residual */
-    to_float_rounded(x, xf, (int64_t)M * D, 0);
-    orc_gemm(M, D, D, af, D, w->wo, D, w->so, w->bo, 0, xf, D, x, D);
-    /* LN2, fc1 + GELU, fc2 + residual */
-    to_float_rounded(x, xf, (int64_t)M * D, 0);
-    orc_layernorm(M, D, xf, D, w->ln2_w, w->ln2_b, 1e-5, t, D);
-    to_float_rounded(t, af, (int64_t)M * D, rb);
-    double* hbuf = (double*)malloc(sizeof(double) * (size_t)M * F);
-    orc_gemm(M, F, D, af, D, w->fc1, D, w->s1, w->b1, 1, NULL, 0, hbuf, F);
-    to_float_rounded(hbuf, af, (int64_t)M * F, rb);
-    free(hbuf);
-    orc_gemm(M, D, F, af, F, w->fc2, F, w->s2, w->b2, 0, xf, D, x, D);
-  }
-  to_float_rounded(x, xf, (int64_t)M * D, 0);
-  orc_layernorm(M, D, xf, D, mdl->ln_f_w, mdl->ln_f_b, 1e-5, t, D);
-  to_float_rounded(t, af, (int64_t)M * D, rb);
-  orc_gemm(M, mdl->vocab, D, af, D, mdl->lm_head, D, mdl->lm_scale, NULL, 0, NULL, 0, logits, mdl->vocab);
-
-  free(x); free(t); free(kd); free(vd); free(xf); free(af); free(qf);
+  double* x = (double*)malloc(sizeof(double) * (size_t)M * mdl->d_model);
+  orc_step_embed(mdl, M, token_ids, positions, x);
+  for (int l = 0; l < mdl->n_layers; ++l)
+    orc_step_layer(mdl, l, M, x, positions, wpage, woff, block_table, bt_stride, row_bt, kpools[l], vpools[l]);
+  orc_step_head(mdl, M, x, logits);
+  free(x);
 }
 
 int orc_num_threads(void) {

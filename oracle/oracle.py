@@ -79,6 +79,7 @@ def _declare(L):
     L.orc_bf16_to_f32.restype = ctypes.c_float
     L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
     L.orc_round_bf16.argtypes = [_P, _I64]
+    L.orc_quantize_e4m3_rows.argtypes = [_I64, _I64, _P, _P, _P]
     L.orc_e4m3_to_f32.restype = ctypes.c_float
     L.orc_e4m3_to_f32.argtypes = [ctypes.c_uint8]
     L.orc_f32_to_e4m3.restype = ctypes.c_uint8
@@ -90,6 +91,9 @@ def _declare(L):
     L.orc_paged_attention.argtypes = [_I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _P, _P, _I, _P, _I]
     L.orc_argmax_rows.argtypes = [_I, _I, _P, _I, _P]
     L.orc_forward_step.argtypes = [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P]
+    L.orc_step_embed.argtypes = [_P, _I, _P, _P, _P]
+    L.orc_step_layer.argtypes = [_P, _I, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P]
+    L.orc_step_head.argtypes = [_P, _I, _P, _P]
     L.orc_num_threads.restype = _I
     L.orc_set_num_threads.restype = _I
     L.orc_set_num_threads.argtypes = [_I]
@@ -159,7 +163,19 @@ def f32_to_e4m3(x: np.ndarray) -> np.ndarray:
 
 def quantize_e4m3_rows(w: np.ndarray):
     """Per-output-channel absmax fp8 e4m3: scale[n] = absmax(w[n,:]) / 448
-    (fp32), q = e4m3_rne(w / scale).  Returns (codes uint8 [N,K], scale fp32 [N])."""
+    (fp32), q = e4m3_rne(w / scale).  Returns (codes uint8 [N,K], scale fp32 [N]).
+    orc_quantize_e4m3_rows (C, rows in parallel); quantize_e4m3_rows_np is
+    the same rule in numpy, the cross-check."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    N, K = w.shape
+    codes = np.empty((N, K), np.uint8)
+    scale = np.empty(N, np.float32)
+    lib().orc_quantize_e4m3_rows(N, K, _ptr(w), _ptr(codes), _ptr(scale))
+    return codes, scale
+
+
+def quantize_e4m3_rows_np(w: np.ndarray):
+    """quantize_e4m3_rows in numpy (vectorised encoder)."""
     w = np.asarray(w, dtype=np.float32)
     absmax = np.max(np.abs(w), axis=1).astype(np.float32)
     scale = (absmax / np.float32(448.0)).astype(np.float32)
@@ -379,7 +395,7 @@ def _derive_used(w: Weights) -> None:
             w.used[name] = round_bf16(arr)
         else:  # fp8 linear weights
             codes, sc = quantize_e4m3_rows(arr)
-            w.used[name] = e4m3_table()[codes]
+            w.used[name] = e4m3_table().take(codes.astype(np.intp))
             w.scale[name] = sc
 
 
@@ -483,9 +499,38 @@ class OracleModel:
         return out
 
 
-def forward_step_with_cache(model: OracleModel, cache: PagedKVCacheOracle, token_ids, positions, seq_ids):
-    """src/transformer.cpp:51-57: resolve each row's write slot and page table
-    from the cache (the caller already ran ensure_capacity), then run."""
+    # The same step one layer at a time (orc_step_embed / orc_step_layer /
+    # orc_step_head; forward_step is exactly their sequence): a caller can
+    # hold one layer's pools on the host at a time.
+    def embed(self, token_ids, positions) -> np.ndarray:
+        """Residual stream [M, d_model] (float64) of the step's rows."""
+        tok, pos = _i32(token_ids), _i32(positions)
+        x = np.empty((tok.size, self.spec.d_model), dtype=np.float64)
+        lib().orc_step_embed(ctypes.byref(self._mdl), tok.size, _ptr(tok), _ptr(pos), _ptr(x))
+        return x
+
+    def layer(self, l, x, positions, wpage, woff, block_table, row_bt, kpool, vpool) -> None:
+        """Layer l on x in place; K/V of the rows are written into kpool /
+        vpool (this layer's [P, page, H, hd] pools, float32 or uint16 bf16
+        bits, contiguous) before its attention reads them."""
+        assert x.dtype == np.float64 and x.flags.c_contiguous
+        assert kpool.flags.c_contiguous and vpool.flags.c_contiguous
+        pos, bt = _i32(positions), _i32(block_table)
+        lib().orc_step_layer(ctypes.byref(self._mdl), l, x.shape[0], _ptr(x), _ptr(pos), _ptr(_i32(wpage)),
+                             _ptr(_i32(woff)), _ptr(bt), bt.shape[1], _ptr(_i32(row_bt)), _ptr(kpool), _ptr(vpool))
+
+    def head(self, x) -> np.ndarray:
+        """Final LayerNorm + lm_head: [M, vocab] float64 logits."""
+        out = np.empty((x.shape[0], self.spec.vocab), dtype=np.float64)
+        lib().orc_step_head(ctypes.byref(self._mdl), x.shape[0], _ptr(np.ascontiguousarray(x)), _ptr(out))
+        return out
+
+
+def step_tables(cache, token_ids, positions, seq_ids):
+    """src/transformer.cpp:51-57: each row's write slot and a compact block
+    table (one row per distinct sequence, row_bt[i] its index) from a cache
+    with the reference's API (resolve_slot, and pages(seq) or seq_pages).
+    Returns (wpage, woff, block_table, row_bt)."""
     M = len(token_ids)
     wpage = np.empty(M, np.int32)
     woff = np.empty(M, np.int32)
@@ -496,11 +541,18 @@ def forward_step_with_cache(model: OracleModel, cache: PagedKVCacheOracle, token
         if seq_ids[i] not in uniq:
             uniq[seq_ids[i]] = len(uniq)
         row_bt[i] = uniq[seq_ids[i]]
-    width = max(1, max(len(cache.seq_pages[s]) for s in uniq))
+    pages = {s: (cache.pages(s) if hasattr(cache, "pages") else cache.seq_pages[s]) for s in uniq}
+    width = max(1, max(len(p) for p in pages.values()))
     table = np.zeros((len(uniq), width), np.int32)
     for s, j in uniq.items():
-        pg = cache.seq_pages[s]
-        table[j, : len(pg)] = pg
+        table[j, : len(pages[s])] = pages[s]
+    return wpage, woff, table, row_bt
+
+
+def forward_step_with_cache(model: OracleModel, cache: PagedKVCacheOracle, token_ids, positions, seq_ids):
+    """src/transformer.cpp:51-57: resolve each row's write slot and page table
+    from the cache (the caller already ran ensure_capacity), then run."""
+    wpage, woff, table, row_bt = step_tables(cache, token_ids, positions, seq_ids)
     return model.forward_step(token_ids, positions, wpage, woff, table, row_bt)
 
 

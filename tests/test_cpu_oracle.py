@@ -30,6 +30,31 @@ def test_g1_oracle_matches_model_py(oracle):
         assert np.abs(lg - g[f"logits{i}"]).max() < 1e-5
 
 
+def test_g1_oracle_layer_by_layer(oracle):
+    """The step run one layer at a time (orc_step_embed / orc_step_layer /
+    orc_step_head, each layer given its own pools, as the full-depth GPU
+    checks run it) against model.py's golden logits, and bit-identical to
+    the whole-step call."""
+    g = np.load(os.path.join(GOLDEN, "g1_refmodel.npz"))
+    w = oracle.synthetic_weights(oracle.ModelSpec(), seed=0, pos_rows=64)
+    for i in range(len(g["lens"])):
+        ids = [int(t) for t in g[f"ids{i}"]]
+        pos = list(range(len(ids)))
+        whole = _prefill(oracle, oracle.OracleModel(w, max_pages=8), ids)
+        om = oracle.OracleModel(w, max_pages=8)
+        cache = oracle.PagedKVCacheOracle(8)
+        sid = cache.allocate_sequence()
+        for p in pos:
+            assert cache.ensure_capacity(sid, p)
+        wpage, woff, bt, row_bt = oracle.step_tables(cache, ids, pos, [sid] * len(ids))
+        x = om.embed(ids, pos)
+        for l in range(om.spec.n_layers):
+            om.layer(l, x, pos, wpage, woff, bt, row_bt, om.kpools[l], om.vpools[l])
+        lg = om.head(x)
+        assert np.array_equal(lg, whole)
+        assert np.abs(lg - g[f"logits{i}"]).max() < 1e-5
+
+
 @pytest.mark.skipif(not os.path.exists(REF_WEIGHTS), reason="reference weights.bin not present")
 def test_g1_oracle_matches_reference_weights_bin(oracle):
     """The reference's own weights.bin and export_reference batch (seed 777):
@@ -185,6 +210,18 @@ def test_e4m3_codec_exhaustive(oracle):
     assert np.array_equal(ours, theirs)
     assert np.array_equal(oracle._e4m3_encode_vec(x), ours)
     assert oracle.f32_to_e4m3(np.array([1000.0, -1000.0], np.float32)).tolist() == [0x7E, 0xFE]
+    # per-channel absmax quantisation: the C rows (OpenMP) and numpy agree,
+    # including an all-zero row (scale 1) and a row whose max sits at a tie
+    w = (rng.standard_normal((64, 300)) * 0.02).astype(np.float32)
+    w[3] = 0.0
+    w[5, 7] = np.float32(1.0)
+    c_codes, c_scale = oracle.quantize_e4m3_rows(w)
+    n_codes, n_scale = oracle.quantize_e4m3_rows_np(w)
+    assert np.array_equal(c_codes, n_codes) and np.array_equal(c_scale.view(np.uint32), n_scale.view(np.uint32))
+    assert c_scale[3] == 1.0 and (c_codes[3] == 0).all()
+    dq = oracle.e4m3_table()[c_codes] * c_scale[:, None]
+    assert np.allclose(np.abs(dq).max(axis=1)[np.arange(64) != 3], np.abs(w).max(axis=1)[np.arange(64) != 3],
+                       rtol=1e-6)
 
 
 def test_prng_spec(oracle):
