@@ -567,7 +567,7 @@ __global__ __launch_bounds__(256) void splitk_layernorm_kernel(const GemmArgs g,
   const int64_t MN = (int64_t)g.M * N;
   const float* pp = g.partial + (int64_t)row * N;
   const float* rp = g.residual ? g.residual + (int64_t)row * g.ldr : nullptr;
-  float4 v[VPW], p[KS - 1][VPW], bi[VPW], r[VPW], gg[VPW], bb[VPW];
+  float4 v[VPW], p[KS - 1][VPW], sc[VPW], bi[VPW], r[VPW], gg[VPW], bb[VPW];
   // (Assignments under if, not conditional expressions: a ?: between a load
   // and a local zero is compiled to a load through a selected pointer, the
   // zero's in scratch memory.)
@@ -575,12 +575,14 @@ __global__ __launch_bounds__(256) void splitk_layernorm_kernel(const GemmArgs g,
   for (int j = 0; j < VPW; ++j) {
     const int c = ((j * 4 + wave) * 64 + lane) * 4;
     v[j] = bi[j] = r[j] = gg[j] = bb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    sc[j] = make_float4(1.f, 1.f, 1.f, 1.f);
 #pragma unroll
     for (int z = 1; z < KS; ++z) p[z - 1][j] = v[j];
     if (c < N) {
       v[j] = *(const float4*)(pp + c);
 #pragma unroll
       for (int z = 1; z < KS; ++z) p[z - 1][j] = *(const float4*)(pp + z * MN + c);
+      if (g.w_scale) sc[j] = *(const float4*)(g.w_scale + c);
       if (g.bias) bi[j] = *(const float4*)(g.bias + c);
       if (rp) r[j] = *(const float4*)(rp + c);
       gg[j] = *(const float4*)(lw + c);
@@ -595,6 +597,7 @@ __global__ __launch_bounds__(256) void splitk_layernorm_kernel(const GemmArgs g,
     for (int z = 1; z < KS; ++z) {
       v[j].x += p[z - 1][j].x; v[j].y += p[z - 1][j].y; v[j].z += p[z - 1][j].z; v[j].w += p[z - 1][j].w;
     }
+    if (g.w_scale) { v[j].x *= sc[j].x; v[j].y *= sc[j].y; v[j].z *= sc[j].z; v[j].w *= sc[j].w; }
     if (g.bias) { v[j].x += bi[j].x; v[j].y += bi[j].y; v[j].z += bi[j].z; v[j].w += bi[j].w; }
     if (rp) { v[j].x += r[j].x; v[j].y += r[j].y; v[j].z += r[j].z; v[j].w += r[j].w; }
     if (c < N) *(float4*)((float*)g.Y + (int64_t)row * g.ldy + c) = v[j];
@@ -1364,7 +1367,11 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
   const int c16 = lane & 15, q = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int n = min(n0 + c16, g.N - 1);
-  const int nkb = g.K / KB;
+  // Split-K (g.partial set, grid.y = g.ksplit): workgroup (x, z) sums K range
+  // [z k_per, (z + 1) k_per) and stores the raw sums as partial z; the
+  // epilogue then runs in the reduce.  Unsplit, k_per = K.
+  const int64_t kofs = (int64_t)blockIdx.y * g.k_per;
+  const int nkb = g.k_per / KB;
   const int kb0 = (nkb * wave) / kSkinnyWaves, kb1 = (nkb * (wave + 1)) / kSkinnyWaves;
 
   f32x4_t acc[MB];
@@ -1399,7 +1406,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
         pre_slot[i][e] = kv ? (int64_t)g.wpage[row] * g.page_size + g.woff[row] : 0;
       }
   };
-  if (PRE && wave == 0 && !g.amax) load_pre();
+  if (PRE && wave == 0 && !g.amax && !g.partial) load_pre();
 
   // LayerNorm prologue: each wave takes rows wave, wave + 8, ... of the
   // workgroup's 16 MB rows and forms their mean and 1/std exactly as
@@ -1472,10 +1479,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
   };
 
   if constexpr (F32) {
-    const float* wp = (const float*)g.W + (int64_t)n * g.ldw + 4 * q;
+    const float* wp = (const float*)g.W + (int64_t)n * g.ldw + kofs + 4 * q;
     const float* xp[MB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) xp[i] = (const float*)g.X + (int64_t)xrow[i] * g.ldx + 4 * q;
+    for (int i = 0; i < MB; ++i) xp[i] = (const float*)g.X + (int64_t)xrow[i] * g.ldx + kofs + 4 * q;
     // Four k blocks per round: all their loads are issued before the MFMAs.
     auto step = [&](int kb, auto U) {
       constexpr int NU = decltype(U)::value;
@@ -1509,11 +1516,11 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
     // k step lane quarter q holds k = 16 q + 0..7 for the first MFMA and
     // 16 q + 8..15 for the second, for W and X alike, so every product pairs
     // the same k.
-    const uint8_t* wp = (const uint8_t*)g.W + (int64_t)n * g.ldw + 16 * q;
+    const uint8_t* wp = (const uint8_t*)g.W + (int64_t)n * g.ldw + kofs + 16 * q;
     const uint16_t* xp[MB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) xp[i] = (const uint16_t*)g.X + (int64_t)xrow[i] * g.ldx + 16 * q;
-    const int nk2 = g.K / 64;
+    for (int i = 0; i < MB; ++i) xp[i] = (const uint16_t*)g.X + (int64_t)xrow[i] * g.ldx + kofs + 16 * q;
+    const int nk2 = g.k_per / 64;
     const int k0 = (nk2 * wave) / kSkinnyWaves, k1 = (nk2 * (wave + 1)) / kSkinnyWaves;
     auto step2 = [&](int kb, auto U) {
       constexpr int NU = decltype(U)::value;
@@ -1548,10 +1555,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
     for (; kb + 4 <= k1; kb += 4) step2(kb, std::integral_constant<int, 4>());
     for (; kb < k1; ++kb) step2(kb, std::integral_constant<int, 1>());
   } else {
-    const WT* wp = (const WT*)g.W + (int64_t)n * g.ldw + 8 * q;
+    const WT* wp = (const WT*)g.W + (int64_t)n * g.ldw + kofs + 8 * q;
     const uint16_t* xp[MB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) xp[i] = (const uint16_t*)g.X + (int64_t)xrow[i] * g.ldx + 8 * q;
+    for (int i = 0; i < MB; ++i) xp[i] = (const uint16_t*)g.X + (int64_t)xrow[i] * g.ldx + kofs + 8 * q;
     auto step = [&](int kb, auto U) {
       constexpr int NU = decltype(U)::value;
       bf16x8_t w[NU], x[NU][MB];
@@ -1585,7 +1592,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
   // before the first store: a load issued after a store would wait for the
   // store's write acknowledgement too (vmcnt counts both, in order), once per
   // element (config 2's M = 64 MLP down, whose residual is such a load).
-  if (!PRE && !g.amax) load_pre();
+  if (!PRE && !g.amax && !g.partial) load_pre();
   const bool ok = col < g.N;
   const float gsc = (g.amax && g.w_scale && ok) ? g.w_scale[col] : 1.f;
   const float gbi = (g.amax && g.bias && ok) ? g.bias[col] : 0.f;
@@ -1594,6 +1601,15 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_skinny_kernel(const Ge
     f32x4_t v = part[0][i][lane];
 #pragma unroll
     for (int w = 1; w < kSkinnyWaves; ++w) v += part[w][i][lane];
+    if (g.partial) {
+      float* pz = g.partial + (int64_t)blockIdx.y * g.M * g.N;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = i * 16 + 4 * q + e;
+        if (row < g.M && ok) pz[(int64_t)row * g.N + col] = v[e];
+      }
+      continue;
+    }
     if (g.amax) {
       // Greedy mode: the row's top-2 over this workgroup's 16 columns (lanes
       // 16 q .. 16 q + 15 hold the same rows), value = sum * scale + bias as
@@ -1682,7 +1698,7 @@ int top2_reduce(bool raw, const void* src, int n_parts, int64_t ld, int M, int* 
 
 template <typename XT, typename WT, bool LN>
 void launch_skinny_mb(const GemmArgs& g, hipStream_t s) {
-  const unsigned grid = (unsigned)cdiv(g.N, 16);
+  const dim3 grid((unsigned)cdiv(g.N, 16), (unsigned)g.ksplit);
   if (g.M <= 16) gemm_skinny_kernel<XT, WT, 1, LN><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
   else if (g.M <= 32) gemm_skinny_kernel<XT, WT, 2, LN><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
   else gemm_skinny_kernel<XT, WT, 4, LN><<<grid, kSkinnyWaves * 64, 0, s>>>(g);
@@ -1780,6 +1796,26 @@ SplitPlan plan_dma_split(int M, int N, int K) {
   const int per = (kt + ks - 1) / ks;
   p.ksplit = (kt + per - 1) / per;
   p.k_per = per * 64;
+  return p;
+}
+
+// Split-K of a skinny call whose reduce runs fused with the LayerNorm after it
+// (cbis_gemm_layernorm): when its 16-column workgroups cannot occupy the
+// CUs, K is split so the grid reaches up to two workgroups per CU while every
+// wave keeps at least two MFMA k steps (config 5's out-projection, K = 2048:
+// 2 parts; fc2, K = 8192: 4 parts, the most the fused reduce takes).
+SplitPlan plan_skinny_split(int M, int N, int K, int w_dtype) {
+  SplitPlan p;
+  p.k_per = K;
+  const int kstep = w_dtype == CBIS_FP8E4M3 ? 64 : (w_dtype == CBIS_BF16 ? 32 : 16);
+  const int64_t wgs = cdiv(N, 16);
+  if (M > 64 || wgs >= kCUs) return p;
+  for (int ks = 4; ks >= 2; --ks)
+    if (wgs * ks <= 2 * kCUs && K % (ks * kstep) == 0 && K / ks >= 2 * kSkinnyWaves * kstep) {
+      p.ksplit = ks;
+      p.k_per = K / ks;
+      break;
+    }
   return p;
 }
 
@@ -1900,8 +1936,10 @@ bool ln_prologue_ok(const cbis_gemm_desc* d, const float* x, int64_t ldx, const 
          a16(beta);
 }
 
+// fused_reduce: the caller folds split-K partials into the kernel that runs
+// next (cbis_gemm_layernorm), so a skinny call may split too.
 int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax = nullptr,
-             const LnPrologue* ln = nullptr) {
+             const LnPrologue* ln = nullptr, bool fused_reduce = false) {
   g.ksplit = 1;
   CBIS_REQUIRE(d, CBIS_ERR_INVALID, "cbis_gemm: null descriptor");
   CBIS_REQUIRE(d->M >= 0 && d->N > 0 && d->K > 0, CBIS_ERR_INVALID, "cbis_gemm: bad M/N/K %d/%d/%d", d->M, d->N, d->K);
@@ -1962,6 +2000,15 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax =
   // of 64 for fp8; W rows 16-byte aligned).
   const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * we) % 16 == 0;
   if (d->M <= kSkinnyMaxM && w_al && d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0) {
+    if (fused_reduce && !amax && !ln) {
+      const SplitPlan p = plan_skinny_split(d->M, d->N, d->K, d->w_dtype);
+      const size_t need = (size_t)p.ksplit * d->M * d->N * sizeof(float);
+      if (p.ksplit > 1 && d->workspace && d->workspace_bytes >= need && ((uintptr_t)d->workspace & 15u) == 0) {
+        g.ksplit = p.ksplit;
+        g.k_per = p.k_per;
+        g.partial = (float*)d->workspace;
+      }
+    }
     if (f32) return launch_skinny<float, float>(g, s);
     if (d->w_dtype == CBIS_BF16) return launch_skinny<uint16_t, uint16_t>(g, s);
     return launch_skinny<uint16_t, uint8_t>(g, s);
@@ -2083,15 +2130,15 @@ int cbis_gemm_layernorm(const cbis_gemm_desc* d, const float* ln_gamma, const fl
                CBIS_ERR_INVALID, "cbis_gemm_layernorm: misaligned rows");
   hipStream_t s = (hipStream_t)stream;
   GemmArgs g;
-  int rc = gemm_run(d, s, g);
+  int rc = gemm_run(d, s, g, nullptr, nullptr, true);
   if (rc || d->M == 0) return rc;
   // layernorm_kernel's chunk count for this row length (its VPL).
   const int nch = ln_chunks(d->N);
   const int vpw = (nch + 3) / 4;
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-  const bool fuse = g.ksplit > 1 && g.ksplit <= 4 && vpw <= 4 && !g.gelu && !g.w_scale && a16(g.partial) &&
-                    (!g.bias || a16(g.bias)) && (!g.residual || (a16(g.residual) && g.ldr % 4 == 0)) &&
-                    a16(ln_gamma) && a16(ln_beta);
+  const bool fuse = g.ksplit > 1 && g.ksplit <= 4 && vpw <= 4 && !g.gelu && a16(g.partial) &&
+                    (!g.w_scale || a16(g.w_scale)) && (!g.bias || a16(g.bias)) &&
+                    (!g.residual || (a16(g.residual) && g.ldr % 4 == 0)) && a16(ln_gamma) && a16(ln_beta);
   if (!fuse) {
     if (g.ksplit > 1 && (rc = splitk_reduce(g, s))) return rc;
     return cbis_layernorm(d->M, d->N, (const float*)d->Y, d->ldy, ln_gamma, ln_beta, eps, ln_dtype, ln_out, ld_ln,
@@ -2171,6 +2218,13 @@ int cbis_layernorm_gemm_argmax(const cbis_gemm_desc* d, const float* x, int64_t 
 
 size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {
   if (!d || d->M <= 0 || d->N <= 0 || d->K <= 0) return 0;
+  // Skinny calls split only under cbis_gemm_layernorm (plan_skinny_split).
+  const int we = d->w_dtype == CBIS_F32 ? 4 : (d->w_dtype == CBIS_BF16 ? 2 : 1);
+  if (d->M <= kSkinnyMaxM && ((uintptr_t)d->W & 15u) == 0 && (d->ldw * we) % 16 == 0 &&
+      d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0) {
+    const SplitPlan p = plan_skinny_split(d->M, d->N, d->K, d->w_dtype);
+    return p.ksplit > 1 ? (size_t)p.ksplit * d->M * d->N * sizeof(float) : 0;
+  }
   if (d->x_dtype == CBIS_F32 && d->w_dtype == CBIS_F32) {
     // gemm_run's fp32 paths: the skinny kernel (no split) or plan_f32.
     const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * 4) % 16 == 0;

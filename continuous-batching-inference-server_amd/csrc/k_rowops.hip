@@ -48,11 +48,16 @@ __global__ __launch_bounds__(256) void embed_kernel(int T, int D, const int* __r
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T) return;
   const int lane = threadIdx.x & 63;
-  const int t = min(max(tok[row], 0), vocab - 1);
-  const int p = min(max(pos[row], 0), max_pos - 1);
+  const int t = tok[row], p = pos[row];
+  float* o = out + (int64_t)row * D;
+  // An id outside its table is not read: its row comes out NaN, so a bad
+  // input shows in every value computed from it instead of being hidden.
+  if (t < 0 || t >= vocab || p < 0 || p >= max_pos) {
+    for (int c = lane * 4; c < D; c += 256) *(float4*)(o + c) = make_float4(NAN, NAN, NAN, NAN);
+    return;
+  }
   const ET* a = te + (int64_t)t * D;
   const ET* b = pe + (int64_t)p * D;
-  float* o = out + (int64_t)row * D;
   // Chunks of 256 columns, 8 at a time: all of a group's loads before its
   // stores (a load issued after a store would wait for the store's write
   // acknowledgement too: vmcnt counts both, in order).
@@ -413,7 +418,8 @@ int cbis_quantize_fp8_rows(uint8_t* codes, float* scale, const float* src, int N
 int cbis_embed_lookup_add(const int* token_ids, const int* positions, const float* tok_emb, const float* pos_emb,
                           float* out, int T, int d_model, cbis_stream_t stream) {
   // The reference launcher has no vocab / table sizes; ids are trusted as
-  // there (kernels/elementwise.cu:7-17).
+  // there (kernels/elementwise.cu:7-17), except that a negative one gives a
+  // NaN row instead of a read before the table.
   return cbis_embed(T, d_model, token_ids, positions, CBIS_F32, tok_emb, pos_emb, 0x7FFFFFFF, 0x7FFFFFFF, out,
                     stream);
 }

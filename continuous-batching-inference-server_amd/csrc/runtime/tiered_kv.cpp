@@ -206,7 +206,7 @@ void TieredKVBlockManager::admit_gpu_resident(uint64_t block_id, PagedKVCache& c
   check_cache(cache);
   if (physical_page < 0 || physical_page >= cache.max_pages())
     throw std::out_of_range("admit_gpu_resident: physical_page");
-  if (meta_.count(block_id)) throw std::runtime_error("admit_gpu_resident: block_id already tracked; use restore()");
+  if (meta_.count(block_id)) throw std::runtime_error("admit_gpu_resident: block_id is already managed (a block seen before comes back through restore)");
   if (gpu_resident_count_ >= gpu_capacity_blocks_) evict_one(now_step);
   BlockMeta m;
   m.tier = Tier::GPU;

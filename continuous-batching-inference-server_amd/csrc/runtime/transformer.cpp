@@ -283,11 +283,13 @@ void TransformerRunner::enqueue_forward(bool greedy) {
 
   // LayerNorms that follow a residual GEMM (ln2 after the out-projection,
   // the next layer's ln1 or ln_f after fc2) run with it (cbis_gemm_layernorm:
-  // fused with fc2's split-K reduce).  Decode-sized steps instead hand ln1
-  // and ln2 to the QKV and fc1 GEMMs that read them (cbis_layernorm_gemm:
-  // same values; for short rows formed inside the GEMM, two launches fewer
-  // per layer).
-  const bool ln_pro = M <= 64;
+  // fused with the GEMM's split-K reduce, where it splits).  Decode-sized
+  // steps with short rows instead hand ln1 and ln2 to the QKV and fc1 GEMMs
+  // that read them (cbis_layernorm_gemm forms them inside the skinny GEMM
+  // for M <= 64 and rows of at most 512: two launches fewer per layer);
+  // longer decode rows (config 5, d 2048) keep the fused reduce + LayerNorm,
+  // which lets their out-projection and fc2 split K.
+  const bool ln_pro = M <= 64 && D <= 512;
   if (!ln_pro)
     cbis_check(cbis_layernorm(M, D, d_x_, D, w_.layers[0].ln1_w, w_.layers[0].ln1_b, 1e-5f, act, d_xn_, D, s),
                "ln1");

@@ -324,6 +324,70 @@ def test_gemm_layernorm_matches_gemm_then_layernorm(cbis, oracle, dev, M, N, K, 
     assert np.array_equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("wdt", ["bf16", "fp8"])
+@pytest.mark.parametrize("M,N,K,parts", [(16, 2048, 8192, (4, 4)), (16, 2048, 2048, (4, 2)), (1, 2048, 8192, (4, 4)),
+                                         (64, 2048, 8192, (4, 4)), (33, 1000, 4096, (4, 4)),
+                                         (16, 6144, 2048, (1, 1))])
+def test_gemm_layernorm_skinny_split(cbis, oracle, dev, M, N, K, parts, wdt):
+    """Decode-sized cbis_gemm_layernorm (config 5's out-projection and fc2:
+    x += h . W^T * scale + b, then LayerNorm(x)): the skinny kernel splits K
+    into `parts` ranges (its 16-column workgroups alone would not occupy the
+    CUs) and the partials are summed, scaled, biased and added to the
+    residual in the LayerNorm's kernel.  x against the fp64 oracle
+    (1e-5 relative), the normalised rows against the oracle's LayerNorm of
+    the GPU's x (one bf16 rounding), and both against the unsplit cbis_gemm
+    then cbis_layernorm (summation order only)."""
+    import torch
+    K_ = cbis.kernels()
+    parts = parts[0] if wdt == "bf16" else parts[1]  # every wave keeps >= 2 MFMA k steps (32 / 64 k)
+    x = oracle.normal(19, 1, M * K).reshape(M, K)
+    w = oracle.normal(19, 2, N * K, 0.02).reshape(N, K)
+    b = oracle.normal(19, 3, N, 0.02)
+    x0 = oracle.normal(19, 4, M * N).reshape(M, N)
+    gam = 1.0 + oracle.normal(19, 5, N, 0.1)
+    bet = oracle.normal(19, 6, N, 0.1)
+    X, xv = bf16_dev(x, dev)
+    if wdt == "bf16":
+        W, wv = bf16_dev(w, dev)
+        S, sc = None, None
+        wd = cbis.BF16
+    else:
+        codes, sc = oracle.quantize_e4m3_rows(w)
+        W, S, wv, wd = to_dev(codes, dev), to_dev(sc, dev), oracle.e4m3_table()[codes], cbis.FP8E4M3
+    B, G, Be = to_dev(b, dev), to_dev(gam, dev), to_dev(bet, dev)
+    outs = []
+    for fused in (True, False):
+        Y = to_dev(x0, dev)
+        d = cbis.GemmDesc()
+        d.M, d.N, d.K = M, N, K
+        d.x_dtype, d.X, d.ldx = cbis.BF16, ptr(X), K
+        d.w_dtype, d.W, d.ldw, d.w_scale = wd, ptr(W), K, ptr(S)
+        d.bias = ptr(B)
+        d.residual, d.ldr = ptr(Y), N
+        d.y_dtype, d.Y, d.ldy = cbis.F32, ptr(Y), N
+        need = K_.cbis_gemm_workspace_size(ctypes.byref(d))
+        assert need == (parts * M * N * 4 if parts > 1 else 0)
+        ws = torch.empty(max(4, need // 4), dtype=torch.float32, device=dev)
+        d.workspace, d.workspace_bytes = ptr(ws), need
+        ln = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        if fused:
+            cbis.check(K_.cbis_gemm_layernorm(ctypes.byref(d), ptr(G), ptr(Be), 1e-5, cbis.BF16, ptr(ln), N,
+                                              stream()), "cbis_gemm_layernorm")
+        else:
+            d.workspace, d.workspace_bytes = None, 0
+            cbis.check(K_.cbis_gemm(ctypes.byref(d), stream()), "cbis_gemm")
+            cbis.check(K_.cbis_layernorm(M, N, ptr(Y), N, ptr(G), ptr(Be), 1e-5, cbis.BF16, ptr(ln), N, stream()),
+                       "cbis_layernorm")
+        sync()
+        outs.append((Y.cpu().numpy(), ln.float().cpu().numpy()))
+    ref = oracle.gemm(xv, wv, w_scale=sc, bias=b, residual=x0)
+    for got, lnv in outs:
+        assert (np.abs(got - ref) / (1.0 + np.abs(ref))).max() < 1e-5
+        lref = oracle.layernorm(got, gam, bet)
+        assert (np.abs(lnv - lref) / (1.0 + np.abs(lref))).max() < 2 ** -7
+    assert (np.abs(outs[0][0] - outs[1][0]) / (1.0 + np.abs(outs[1][0]))).max() < 1e-5
+
+
 @pytest.mark.parametrize("wdt", ["f32", "bf16", "fp8"])
 @pytest.mark.parametrize("M,K", [(1, 256), (8, 256), (33, 512), (64, 512), (16, 2048), (100, 256), (8, 4096)])
 def test_layernorm_gemm_matches_layernorm_then_gemm(cbis, oracle, dev, M, K, wdt):
@@ -637,6 +701,20 @@ def test_embed(cbis, oracle, dev, edt):
     sync()
     ref = tev[tok].astype(np.float64) + pev[pos]
     assert np.array_equal(out.cpu().numpy(), ref.astype(np.float32))
+    # ids outside the tables read nothing: those rows come out NaN, the rest exact
+    bad_tok, bad_pos = tok.copy(), pos.copy()
+    bad_tok[[3, 9]] = [V, -1]
+    bad_pos[[20, 41]] = [S, -7]
+    TOK, POS = to_dev(bad_tok, dev), to_dev(bad_pos, dev)
+    out.fill_(0.0)
+    cbis.check(cbis.kernels().cbis_embed(M, D, ptr(TOK), ptr(POS), cbis.DTYPES[edt], ptr(TE), ptr(PE), V, S,
+                                         ptr(out), stream()))
+    sync()
+    got = out.cpu().numpy()
+    bad = np.zeros(M, bool)
+    bad[[3, 9, 20, 41]] = True
+    assert np.isnan(got[bad]).all()
+    assert np.array_equal(got[~bad], ref.astype(np.float32)[~bad])
 
 
 @pytest.mark.parametrize("N", [32000, 1001, 4 * 1024 * 9 + 12])
