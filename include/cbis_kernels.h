@@ -64,7 +64,9 @@ int cbis_linear_forward(const float* X, const float* W, const float* b, float* Y
                         int in_features, int out_features, cbis_stream_t stream);
 
 /* out[r] = tok_emb[token_ids[r]] + pos_emb[positions[r]].
- * Replaces embed_lookup_add, include/elementwise.hpp:6-8. */
+ * Replaces embed_lookup_add, include/elementwise.hpp:6-8.  Like the reference
+ * the tables' sizes are not known here and ids are trusted, except that a
+ * negative id gives an all-NaN row instead of a read before the table. */
 int cbis_embed_lookup_add(const int* token_ids, const int* positions, const float* tok_emb,
                           const float* pos_emb, float* out, int T, int d_model, cbis_stream_t stream);
 
@@ -255,7 +257,8 @@ int cbis_paged_attention_mixed(const cbis_attn_desc* d, int n_tiles, const int* 
 /* ----------------------------------------------------------------------- */
 
 /* out[r,:] = tok_emb[token_ids[r],:] + pos_emb[positions[r],:] (fp32 out);
- * embeddings fp32 or bf16; ids are clamped to [0, vocab) and [0, max_pos). */
+ * embeddings fp32 or bf16.  A row whose token id is outside [0, vocab) or
+ * position outside [0, max_pos) reads nothing and comes out all NaN. */
 int cbis_embed(int T, int d_model, const int* token_ids, const int* positions, int emb_dtype,
                const void* tok_emb, const void* pos_emb, int vocab, int max_pos, float* out,
                cbis_stream_t stream);

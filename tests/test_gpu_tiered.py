@@ -260,7 +260,7 @@ def test_manager_errors(cbis, mgr_factory):
     mgr = mgr_factory(4, 4)
     fill_page(cache, 0, 1)
     mgr.admit_gpu_resident(1, cache, 0, 0)
-    with pytest.raises(cbis.CbisError, match="already tracked"):
+    with pytest.raises(cbis.CbisError, match="already managed"):
         mgr.admit_gpu_resident(1, cache, 1, 0)
     with pytest.raises(cbis.CbisError, match="unknown block_id"):
         mgr.restore(99, cache, 1, 0)
