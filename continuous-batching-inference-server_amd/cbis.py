@@ -95,6 +95,7 @@ KERNEL_SYMBOLS = {
     "cbis_kv_pages_gather": (_I, [_P, _P, _I, _I, ctypes.c_int64, _P, _I, _P]),
     "cbis_kv_pages_scatter": (_I, [_P, _P, _I, _I, ctypes.c_int64, _P, _I, _P]),
     "cbis_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
+    "cbis_gemm_layernorm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "cbis_gemm_argmax_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "cbis_gemm_argmax": (_I, [ctypes.POINTER(GemmDesc), _P, _P, _P, _SZ, _P]),
     "cbis_layernorm_gemm_argmax": (_I, [ctypes.POINTER(GemmDesc), _P, _I64, _P, _P, _F, _P, _P, _P, _SZ, _P]),

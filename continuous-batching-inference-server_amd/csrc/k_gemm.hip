@@ -72,7 +72,22 @@ struct GemmArgs {
   // destination (Y, the K/V pools or the partials) and in the residual: the
   // parked epilogue then takes its vector path on tiles inside N (with_vec).
   int vec_ok;
+  // Tile order of an XCD's contiguous run: N tile fastest when X is the
+  // larger operand (its rows are then fetched once per XCD), else M fastest
+  // (W's columns are).
+  int n_fast;
 };
+
+// Tile (m, n) of workgroup bid after xcd_contiguous.
+template <int BM, int BN>
+__device__ inline int2 tile_of(const GemmArgs& g, int bid) {
+  if (g.n_fast) {
+    const int nt = (g.N + BN - 1) / BN;
+    return make_int2(bid / nt, bid % nt);
+  }
+  const int mt = (g.M + BM - 1) / BM;
+  return make_int2(bid % mt, bid / mt);
+}
 
 // g with vec_ok set from its shapes, strides and pointers.
 GemmArgs with_vec(const GemmArgs& g) {
@@ -234,8 +249,9 @@ struct WLoad<uint8_t> {
 
 // Workgroup b is dispatched to XCD b % 8 (measured on gfx950 from the
 // XCC_ID hardware register).  Renumbering so that each XCD's workgroups take
-// one contiguous run of tiles (M fastest) keeps an XCD on few W columns, so
-// its 4 MB L2 serves the repeats instead of every XCD streaming all of W.
+// one contiguous run of tiles keeps an XCD on few column blocks of the larger
+// operand (tile_of: M fastest for a larger W, N fastest for a larger X), so
+// its 4 MB L2 serves the repeats instead of every XCD streaming all of it.
 __device__ inline int xcd_contiguous(int bid, int nwg) {
   const int q = nwg >> 3, r = nwg & 7, x = bid & 7;
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + (bid >> 3);
@@ -274,12 +290,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const GemmArgs g) {
   auto lB = [&](int b) { return smem + b * (BM + BN) * 128 + BM * 128; };
 
   // Tile index with XCD-contiguous renumbering.
-  const int mt = (g.M + BM - 1) / BM;
-  const int nwg = gridDim.x;
-  int bid = blockIdx.x;
-  bid = xcd_contiguous(bid, nwg);
-  const int tm = bid % mt, tn = bid / mt;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int2 tt = tile_of<BM, BN>(g, xcd_contiguous(blockIdx.x, gridDim.x));
+  const int m0 = tt.x * BM, n0 = tt.y * BN;
   const int kz = blockIdx.z;
   const int kbeg = kz * g.k_per;
   const int KT = min(g.k_per, g.K - kbeg) / BK;
@@ -652,12 +664,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_bf16_dma_kernel(const GemmAr
   constexpr int RING = STAGES * STAGE_BYTES;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[RING > parked_bytes<BM, BN>() ? RING : parked_bytes<BM, BN>()];
 
-  const int mt = (g.M + BM - 1) / BM;
-  const int nwg = gridDim.x;
-  int bid = blockIdx.x;
-  bid = xcd_contiguous(bid, nwg);
-  const int tm = bid % mt, tn = bid / mt;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int2 tt = tile_of<BM, BN>(g, xcd_contiguous(blockIdx.x, gridDim.x));
+  const int m0 = tt.x * BM, n0 = tt.y * BN;
   const int kz = blockIdx.z;
   const int kbeg = kz * g.k_per;
   const int KT = min(g.k_per, g.K - kbeg) / 64;
@@ -1123,9 +1131,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_ws_kernel(const GemmArgs g) {
   constexpr int LPW = T::LPW, STAGE_BYTES = T::STAGE_BYTES, FM = T::FM, FN = T::FN;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::LDS];
 
-  const int mt = (g.M + BM - 1) / BM;
-  const int bid = xcd_contiguous(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mt) * BM, n0 = (bid / mt) * BN;
+  const int2 tt = tile_of<BM, BN>(g, xcd_contiguous(blockIdx.x, gridDim.x));
+  const int m0 = tt.x * BM, n0 = tt.y * BN;
   const int kz = blockIdx.z;
   const int kbeg = kz * g.k_per;
   const int KT = min(g.k_per, g.K - kbeg) / 64;
@@ -1971,6 +1978,7 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax =
   CBIS_REQUIRE(amax || (kv && d->kv_col0 == 0) || d->Y, CBIS_ERR_INVALID, "cbis_gemm: null Y");
 
   g.M = d->M; g.N = d->N; g.K = d->K;
+  g.n_fast = (int64_t)d->M * xe > (int64_t)d->N * we ? 1 : 0;
   g.X = d->X; g.ldx = d->ldx;
   g.W = d->W; g.ldw = d->ldw;
   g.w_scale = d->w_scale;
@@ -2216,15 +2224,26 @@ int cbis_layernorm_gemm_argmax(const cbis_gemm_desc* d, const float* x, int64_t 
   return gemm_argmax(d, next_token, margin, workspace, workspace_bytes, (hipStream_t)stream, &ln, who);
 }
 
-size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {
+size_t cbis_gemm_layernorm_workspace_size(const cbis_gemm_desc* d) {
   if (!d || d->M <= 0 || d->N <= 0 || d->K <= 0) return 0;
-  // Skinny calls split only under cbis_gemm_layernorm (plan_skinny_split).
+  // Skinny calls split only here, where the LayerNorm kernel folds the
+  // partials in (plan_skinny_split).
   const int we = d->w_dtype == CBIS_F32 ? 4 : (d->w_dtype == CBIS_BF16 ? 2 : 1);
   if (d->M <= kSkinnyMaxM && ((uintptr_t)d->W & 15u) == 0 && (d->ldw * we) % 16 == 0 &&
       d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0) {
     const SplitPlan p = plan_skinny_split(d->M, d->N, d->K, d->w_dtype);
     return p.ksplit > 1 ? (size_t)p.ksplit * d->M * d->N * sizeof(float) : 0;
   }
+  return cbis_gemm_workspace_size(d);
+}
+
+size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {
+  if (!d || d->M <= 0 || d->N <= 0 || d->K <= 0) return 0;
+  // gemm_run's skinny path never splits in cbis_gemm.
+  const int wb = d->w_dtype == CBIS_F32 ? 4 : (d->w_dtype == CBIS_BF16 ? 2 : 1);
+  if (d->M <= kSkinnyMaxM && ((uintptr_t)d->W & 15u) == 0 && (d->ldw * wb) % 16 == 0 &&
+      d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0)
+    return 0;
   if (d->x_dtype == CBIS_F32 && d->w_dtype == CBIS_F32) {
     // gemm_run's fp32 paths: the skinny kernel (no split) or plan_f32.
     const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * 4) % 16 == 0;

@@ -62,7 +62,8 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   ws_bytes_ = (2048 + R) * (size_t)cfg_.n_heads * (cfg_.head_dim + 4) * 4;
   hip_check(hipMalloc(&d_ws_, ws_bytes_), "hipMalloc attention workspace");
   // Split-K workspace: the largest any of the step's GEMM shapes asks for at
-  // any row count up to max_total_rows.
+  // any row count up to max_total_rows (through cbis_gemm_layernorm, whose
+  // decode-sized calls split too).
   const int shapes[5][2] = {{3 * (int)D, (int)D}, {(int)D, (int)D}, {(int)F, (int)D}, {(int)D, (int)F}, {(int)V, (int)D}};
   cbis_gemm_desc q = {};
   q.x_dtype = cfg_.act_dtype();
@@ -71,7 +72,7 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   for (int m = 1; m <= max_total_rows; ++m)
     for (const auto& sh : shapes) {
       q.M = m; q.N = sh[0]; q.K = sh[1]; q.ldw = sh[1];
-      gemm_ws_bytes_ = std::max(gemm_ws_bytes_, cbis_gemm_workspace_size(&q));
+      gemm_ws_bytes_ = std::max(gemm_ws_bytes_, cbis_gemm_layernorm_workspace_size(&q));
     }
   if (gemm_ws_bytes_) hip_check(hipMalloc(&d_gemm_ws_, gemm_ws_bytes_), "hipMalloc gemm workspace");
   // Greedy lm_head partials (the logits buffer serves paths that store them).

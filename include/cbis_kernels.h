@@ -141,6 +141,10 @@ size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d);
 
 int cbis_gemm(const cbis_gemm_desc* d, cbis_stream_t stream);
 
+/* Bytes of workspace that let cbis_gemm_layernorm split K as it prefers: as
+ * cbis_gemm_workspace_size, and for decode-sized calls (M <= 64), whose
+ * reduce it folds into its LayerNorm kernel, the skinny kernel's split too. */
+size_t cbis_gemm_layernorm_workspace_size(const cbis_gemm_desc* d);
 /* cbis_gemm, then a row LayerNorm of its fp32 output Y [M, N] (gamma / beta
  * of N values, eps) into ln_out (fp32 or bf16, row pitch ld_ln): the step's
  * "x += h . W2^T + b2; xn = LayerNorm(x)" (src/transformer.cpp:88-89 with the

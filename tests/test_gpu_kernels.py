@@ -365,8 +365,9 @@ def test_gemm_layernorm_skinny_split(cbis, oracle, dev, M, N, K, parts, wdt):
         d.bias = ptr(B)
         d.residual, d.ldr = ptr(Y), N
         d.y_dtype, d.Y, d.ldy = cbis.F32, ptr(Y), N
-        need = K_.cbis_gemm_workspace_size(ctypes.byref(d))
+        need = K_.cbis_gemm_layernorm_workspace_size(ctypes.byref(d))
         assert need == (parts * M * N * 4 if parts > 1 else 0)
+        assert K_.cbis_gemm_workspace_size(ctypes.byref(d)) == 0  # plain cbis_gemm keeps the skinny kernel whole
         ws = torch.empty(max(4, need // 4), dtype=torch.float32, device=dev)
         d.workspace, d.workspace_bytes = ptr(ws), need
         ln = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
