@@ -170,6 +170,11 @@ RUNTIME_SYMBOLS = {
     "cbis_run_continuous_chunked": (_I, [_P, _P, _I, _IP, _IP, _IP, _I, _I, _I, _IP,
                                          ctypes.POINTER(ctypes.c_double), _I]),
     "cbis_schedule_dry_run": (_I, [_P, _I, _IP, _IP, _IP, _I, _I, _I, _I, _IP, _IP, _I, _IP, _IP, _IP, _I]),
+    "cbis_run_continuous_timed": (_I, [_P, _P, _I, _IP, _IP, _IP, ctypes.POINTER(ctypes.c_double), _I, _I, _I, _IP,
+                                       ctypes.POINTER(ctypes.c_double), _I, ctypes.POINTER(ctypes.c_double)]),
+    "cbis_schedule_dry_run_timed": (_I, [_P, _I, _IP, _IP, _IP, ctypes.POINTER(ctypes.c_double), ctypes.c_double, _I,
+                                         _I, _I, _I, _IP, _IP, _I, _IP, _IP, _IP, _I,
+                                         ctypes.POINTER(ctypes.c_double)]),
 }
 
 _kern = None
@@ -534,39 +539,53 @@ def block_inflate(comp: bytes, out_len: int) -> bytes:
     return buf.raw[:out_len]
 
 
+def _darr(values):
+    return (ctypes.c_double * max(1, len(values)))(*values)
+
+
 def run_continuous(runner: TransformerRunner, cache: PagedKVCache, prompts, decode_lens, max_slots=16,
-                   max_steps=4096, prefill_chunk=0, step_token_budget=0):
+                   max_steps=4096, prefill_chunk=0, step_token_budget=0, arrival_ms=None):
     """Continuous batching (src/bench_batching.cpp:98-179); prefill_chunk /
-    step_token_budget > 0 feed prompts in chunks.  Returns (tokens per
-    request, per-step wall ms)."""
+    step_token_budget > 0 feed prompts in chunks; arrival_ms (nondecreasing)
+    admits request i only once that many ms of the run have passed.  Returns
+    (tokens per request, per-step wall ms), plus the per-request finish
+    times (ms since the run began) when arrival_ms is given."""
     lens = [len(p) for p in prompts]
     flat = [t for p in prompts for t in p]
     out = (ctypes.c_int * max(1, sum(decode_lens)))()
     ms = (ctypes.c_double * max_steps)()
-    n = _rt_check(runtime().cbis_run_continuous_chunked(runner._h, cache._h, len(prompts), _iarr(lens), _iarr(flat),
-                                                        _iarr(decode_lens), max_slots, prefill_chunk,
-                                                        step_token_budget, out, ms, max_steps),
+    fin = (ctypes.c_double * max(1, len(prompts)))()
+    arr = _darr(arrival_ms) if arrival_ms is not None else None
+    n = _rt_check(runtime().cbis_run_continuous_timed(runner._h, cache._h, len(prompts), _iarr(lens), _iarr(flat),
+                                                      _iarr(decode_lens), arr, max_slots, prefill_chunk,
+                                                      step_token_budget, out, ms, max_steps, fin),
                   "run_continuous")
     toks, o = [], 0
     for d in decode_lens:
         toks.append(list(out[o: o + d]))
         o += d
-    return toks, list(ms[: min(n, max_steps)])
+    if arrival_ms is None:
+        return toks, list(ms[: min(n, max_steps)])
+    return toks, list(ms[: min(n, max_steps)]), list(fin[: len(prompts)])
 
 
 def schedule_dry_run(cache: PagedKVCache, prompts, decode_lens, vocab, max_slots=16, prefill_chunk=0,
-                     step_token_budget=0, max_steps=4096, max_rows=1 << 16):
+                     step_token_budget=0, max_steps=4096, max_rows=1 << 16, arrival_ms=None, step_time_ms=1.0):
     """The scheduler alone, on the host, with the stand-in step of
     cbis_schedule_dry_run.  Returns (tokens per request, [(tok, pos, sid)
-    rows of each step])."""
+    rows of each step]); with arrival_ms, on a virtual clock where a step
+    takes step_time_ms, and the per-request finish times as a third value."""
     lens = [len(p) for p in prompts]
     flat = [t for p in prompts for t in p]
     out = (ctypes.c_int * max(1, sum(decode_lens)))()
     rows = (ctypes.c_int * max_steps)()
     rt, rp, rs = (ctypes.c_int * max_rows)(), (ctypes.c_int * max_rows)(), (ctypes.c_int * max_rows)()
-    n = _rt_check(runtime().cbis_schedule_dry_run(cache._h, len(prompts), _iarr(lens), _iarr(flat),
-                                                  _iarr(decode_lens), max_slots, prefill_chunk, step_token_budget,
-                                                  vocab, out, rows, max_steps, rt, rp, rs, max_rows),
+    fin = (ctypes.c_double * max(1, len(prompts)))()
+    arr = _darr(arrival_ms) if arrival_ms is not None else None
+    n = _rt_check(runtime().cbis_schedule_dry_run_timed(cache._h, len(prompts), _iarr(lens), _iarr(flat),
+                                                        _iarr(decode_lens), arr, step_time_ms, max_slots,
+                                                        prefill_chunk, step_token_budget, vocab, out, rows,
+                                                        max_steps, rt, rp, rs, max_rows, fin),
                   "schedule_dry_run")
     if n > max_steps or sum(rows[:n]) > max_rows:
         raise RuntimeError("schedule_dry_run: trace larger than the buffers")
@@ -578,4 +597,6 @@ def schedule_dry_run(cache: PagedKVCache, prompts, decode_lens, vocab, max_slots
     for k in range(n):
         steps.append([(rt[r + i], rp[r + i], rs[r + i]) for i in range(rows[k])])
         r += rows[k]
-    return toks, steps
+    if arrival_ms is None:
+        return toks, steps
+    return toks, steps, list(fin[: len(prompts)])

@@ -277,6 +277,11 @@ std::vector<Request> make_requests(int n_requests, const int* prompt_lens, const
   return reqs;
 }
 
+void set_arrivals(std::vector<Request>& reqs, const double* arrival_ms) {
+  if (arrival_ms)
+    for (size_t i = 0; i < reqs.size(); ++i) reqs[i].arrival_ms = arrival_ms[i];
+}
+
 void copy_tokens(const ContinuousResult& res, int n_requests, const int* decode_lens, int* out_tokens) {
   size_t o = 0;
   for (int i = 0; i < n_requests; ++i)
@@ -302,13 +307,24 @@ int cbis_run_continuous(cbis_runner* r, cbis_cache* c, int n_requests, const int
 int cbis_run_continuous_chunked(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
                                 const int* prompt_tokens, const int* decode_lens, int max_slots, int prefill_chunk,
                                 int step_token_budget, int* out_tokens, double* step_ms, int max_steps) {
+  return cbis_run_continuous_timed(r, c, n_requests, prompt_lens, prompt_tokens, decode_lens, nullptr, max_slots,
+                                   prefill_chunk, step_token_budget, out_tokens, step_ms, max_steps, nullptr);
+}
+
+int cbis_run_continuous_timed(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
+                              const int* prompt_tokens, const int* decode_lens, const double* arrival_ms,
+                              int max_slots, int prefill_chunk, int step_token_budget, int* out_tokens,
+                              double* step_ms, int max_steps, double* finish_ms) {
   return guard([&] {
-    const std::vector<Request> reqs = make_requests(n_requests, prompt_lens, prompt_tokens, decode_lens);
+    std::vector<Request> reqs = make_requests(n_requests, prompt_lens, prompt_tokens, decode_lens);
+    set_arrivals(reqs, arrival_ms);
     const ContinuousResult res =
         run_continuous(*r->impl, *c->impl, reqs, options(max_slots, prefill_chunk, step_token_budget));
     copy_tokens(res, n_requests, decode_lens, out_tokens);
     if (step_ms)
       for (int i = 0; i < (int)res.step_ms.size() && i < max_steps; ++i) step_ms[i] = res.step_ms[i];
+    if (finish_ms)
+      for (int i = 0; i < n_requests; ++i) finish_ms[i] = res.finish_ms[i];
     return (int)res.step_ms.size();
   });
 }
@@ -317,19 +333,38 @@ int cbis_schedule_dry_run(cbis_cache* c, int n_requests, const int* prompt_lens,
                           const int* decode_lens, int max_slots, int prefill_chunk, int step_token_budget, int vocab,
                           int* out_tokens, int* step_rows, int max_steps, int* row_tok, int* row_pos, int* row_sid,
                           int max_rows) {
+  return cbis_schedule_dry_run_timed(c, n_requests, prompt_lens, prompt_tokens, decode_lens, nullptr, 1.0, max_slots,
+                                     prefill_chunk, step_token_budget, vocab, out_tokens, step_rows, max_steps, row_tok,
+                                     row_pos, row_sid, max_rows, nullptr);
+}
+
+int cbis_schedule_dry_run_timed(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens,
+                                const int* decode_lens, const double* arrival_ms, double step_time_ms, int max_slots,
+                                int prefill_chunk, int step_token_budget, int vocab, int* out_tokens, int* step_rows,
+                                int max_steps, int* row_tok, int* row_pos, int* row_sid, int max_rows,
+                                double* finish_ms) {
   return guard([&] {
     if (vocab <= 0) throw std::invalid_argument("schedule_dry_run: vocab must be > 0");
-    const std::vector<Request> reqs = make_requests(n_requests, prompt_lens, prompt_tokens, decode_lens);
+    if (!(step_time_ms >= 0.0)) throw std::invalid_argument("schedule_dry_run: step_time_ms must be >= 0");
+    std::vector<Request> reqs = make_requests(n_requests, prompt_lens, prompt_tokens, decode_lens);
+    set_arrivals(reqs, arrival_ms);
+    // Virtual clock: a step takes step_time_ms, an idle wait jumps to the arrival.
+    double clock = 0.0;
     const StepFn step = [&](const std::vector<int>& t, const std::vector<int>& p, const std::vector<int>& s) {
       std::vector<int> next(t.size());
       for (size_t i = 0; i < t.size(); ++i)
         next[i] = (int)(((uint32_t)t[i] * 31u + (uint32_t)p[i] * 7u + (uint32_t)s[i] * 13u + 1u) % (uint32_t)vocab);
+      clock += step_time_ms;
       return next;
     };
     std::vector<StepRows> trace;
-    const ContinuousResult res =
-        run_continuous(step, *c->impl, reqs, options(max_slots, prefill_chunk, step_token_budget), &trace);
+    ScheduleOptions opt = options(max_slots, prefill_chunk, step_token_budget);
+    opt.clock_ms = [&]() { return clock; };
+    opt.wait_ms = [&](double ms) { clock += ms; };
+    const ContinuousResult res = run_continuous(step, *c->impl, reqs, opt, &trace);
     copy_tokens(res, n_requests, decode_lens, out_tokens);
+    if (finish_ms)
+      for (int i = 0; i < n_requests; ++i) finish_ms[i] = res.finish_ms[i];
     int row = 0;
     for (size_t k = 0; k < trace.size(); ++k) {
       const int n = (int)trace[k].tok.size();

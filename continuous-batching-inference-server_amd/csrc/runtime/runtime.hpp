@@ -353,17 +353,20 @@ class TieredKVBlockManager {
 };
 
 // ---------------------------------------------------------------------------
-// Continuous batching (src/bench_batching.cpp:98-179), all requests present
-// at t = 0.
+// Continuous batching (src/bench_batching.cpp:98-179).
 // ---------------------------------------------------------------------------
 struct Request {
   std::vector<int> prompt;
   int decode_len = 0;
+  // Admitted once this many ms have passed since the run began
+  // (src/bench_batching.cpp:110-121); requests are given in arrival order.
+  double arrival_ms = 0.0;
 };
 
 struct ContinuousResult {
   std::vector<std::vector<int>> tokens;  // generated tokens per request
   std::vector<double> step_ms;           // wall time of each forward step
+  std::vector<double> finish_ms;         // per request: ms since the run began when its last token came back
 };
 
 // Scheduling knobs.  prefill_chunk = 0 and step_token_budget = 0 is the
@@ -372,6 +375,12 @@ struct ScheduleOptions {
   int max_slots = 16;
   int prefill_chunk = 0;      // prompt rows a slot contributes per step; 0 = the whole prompt
   int step_token_budget = 0;  // cap on prompt rows per step (decode rows always run); 0 = none
+  // The run's clock in ms since it began and the wait of an idle scheduler
+  // for the next arrival; unset: steady_clock and a sleep
+  // (src/bench_batching.cpp:153-158).  The host-only dry run sets a virtual
+  // clock.
+  std::function<double()> clock_ms;
+  std::function<void(double)> wait_ms;
 };
 
 // Rows of one scheduled step, in the order they were handed to the step.

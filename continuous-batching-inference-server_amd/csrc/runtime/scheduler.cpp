@@ -1,6 +1,8 @@
 // Continuous batching, the iteration-level scheduler of
-// src/bench_batching.cpp:98-179 with every request present at t = 0:
-//  * free slots admit requests in order (allocate_sequence);
+// src/bench_batching.cpp:98-179:
+//  * free slots admit requests in order (allocate_sequence), each once its
+//    arrival time has passed; with no active slot the scheduler waits for
+//    the next arrival;
 //  * slots are visited in order every step; a slot still feeding its prompt
 //    contributes its next prompt rows (ensure_capacity per row), a slot past
 //    its prompt one decode row at next_pos fed with its last generated token;
@@ -16,6 +18,8 @@
 // step_token_budget > 0 caps the prompt rows of one step, decode rows are
 // never deferred.
 #include <chrono>
+#include <cmath>
+#include <thread>
 
 #include "runtime.hpp"
 
@@ -30,20 +34,30 @@ ContinuousResult run_continuous(const StepFn& step, PagedKVCache& cache, const s
   if (opt.max_slots <= 0) throw std::invalid_argument("run_continuous: max_slots must be > 0");
   if (opt.prefill_chunk < 0 || opt.step_token_budget < 0)
     throw std::invalid_argument("run_continuous: prefill_chunk and step_token_budget must be >= 0");
+  double prev_arrival = 0.0;
   for (const auto& r : reqs) {
     if (r.prompt.empty()) throw std::invalid_argument("run_continuous: empty prompt");
     if (r.decode_len <= 0) throw std::invalid_argument("run_continuous: decode_len must be > 0");
+    if (!std::isfinite(r.arrival_ms) || r.arrival_ms < prev_arrival)
+      throw std::invalid_argument("run_continuous: arrival_ms must be finite, >= 0 and nondecreasing");
+    prev_arrival = r.arrival_ms;
   }
   ContinuousResult res;
   res.tokens.assign(reqs.size(), {});
+  res.finish_ms.assign(reqs.size(), 0.0);
   std::vector<Slot> slots(opt.max_slots);
   size_t next_req = 0;
   size_t completed = 0;
   using Clock = std::chrono::steady_clock;
+  const auto start = Clock::now();
+  auto now_ms = [&]() {
+    return opt.clock_ms ? opt.clock_ms() : std::chrono::duration<double, std::milli>(Clock::now() - start).count();
+  };
   while (completed < reqs.size()) {
+    const double now = now_ms();
     for (auto& s : slots) {
       if (s.active) continue;
-      if (next_req >= reqs.size()) break;
+      if (next_req >= reqs.size() || reqs[next_req].arrival_ms > now) break;
       s = Slot();
       s.active = true;
       s.req = (int)next_req++;
@@ -82,11 +96,22 @@ ContinuousResult run_continuous(const StepFn& step, PagedKVCache& cache, const s
         s.next_pos += 1;
       }
     }
+    bool any_active = false;
+    for (const auto& s : slots) any_active = any_active || s.active;
+    if (!any_active) {  // nothing admitted yet: wait for the next arrival (next_req < reqs.size() here)
+      const double wait = reqs[next_req].arrival_ms - now;
+      if (wait > 0) {
+        if (opt.wait_ms) opt.wait_ms(wait);
+        else std::this_thread::sleep_for(std::chrono::duration<double, std::milli>(wait));
+      }
+      continue;
+    }
     if (tok.empty()) throw std::runtime_error("run_continuous: no runnable rows");
     if (trace) trace->push_back({tok, pos, sid});
     const auto t0 = Clock::now();
     const std::vector<int> next = step(tok, pos, sid);
     res.step_ms.push_back(std::chrono::duration<double, std::milli>(Clock::now() - t0).count());
+    const double step_done = now_ms();
     if (next.size() != tok.size()) throw std::runtime_error("run_continuous: step returned a wrong row count");
     for (size_t i = 0; i < tok.size(); ++i) {
       if (!last[i]) continue;
@@ -95,6 +120,7 @@ ContinuousResult run_continuous(const StepFn& step, PagedKVCache& cache, const s
       s->generated += 1;
       res.tokens[s->req].push_back(next[i]);
       if (s->generated >= reqs[s->req].decode_len) {
+        res.finish_ms[s->req] = step_done;
         cache.free_sequence(s->seq_id);
         s->active = false;
         completed += 1;

@@ -184,6 +184,17 @@ int cbis_run_continuous_chunked(cbis_runner* r, cbis_cache* c, int n_requests, c
                                 const int* prompt_tokens, const int* decode_lens, int max_slots, int prefill_chunk,
                                 int step_token_budget, int* out_tokens, double* step_ms, int max_steps);
 
+/* cbis_run_continuous_chunked with request arrival times
+ * (src/bench_batching.cpp:110-121, 153-158): request i is admitted once
+ * arrival_ms[i] ms have passed since the run began (nondecreasing; NULL: all
+ * at 0), and a scheduler with no active request sleeps until the next
+ * arrival.  finish_ms (or NULL): per request, ms since the run began when its
+ * last token came back (the reference's Result::finish_ms). */
+int cbis_run_continuous_timed(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
+                              const int* prompt_tokens, const int* decode_lens, const double* arrival_ms,
+                              int max_slots, int prefill_chunk, int step_token_budget, int* out_tokens,
+                              double* step_ms, int max_steps, double* finish_ms);
+
 /* Runs the scheduler on the host only, with a stand-in step whose "greedy
  * token" of row (tok, pos, seq) is (31 tok + 7 pos + 13 seq + 1) mod vocab
  * (32-bit unsigned arithmetic), so the schedule can be checked without a
@@ -195,6 +206,14 @@ int cbis_schedule_dry_run(cbis_cache* c, int n_requests, const int* prompt_lens,
                           const int* decode_lens, int max_slots, int prefill_chunk, int step_token_budget, int vocab,
                           int* out_tokens, int* step_rows, int max_steps, int* row_tok, int* row_pos, int* row_sid,
                           int max_rows);
+/* The dry run with arrival times on a virtual clock: every step takes
+ * step_time_ms and an idle scheduler's wait jumps the clock to the next
+ * arrival; finish_ms (or NULL) as cbis_run_continuous_timed's. */
+int cbis_schedule_dry_run_timed(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens,
+                                const int* decode_lens, const double* arrival_ms, double step_time_ms, int max_slots,
+                                int prefill_chunk, int step_token_budget, int vocab, int* out_tokens, int* step_rows,
+                                int max_steps, int* row_tok, int* row_pos, int* row_sid, int max_rows,
+                                double* finish_ms);
 
 #ifdef __cplusplus
 }

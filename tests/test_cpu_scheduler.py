@@ -159,3 +159,97 @@ def test_schedule_rejects_bad_input(cbis):
         cbis.schedule_dry_run(c, [[1, 2]], [1], 100, prefill_chunk=-1)
     with pytest.raises(RuntimeError, match="out of KV pages"):
         cbis.schedule_dry_run(_cache(cbis, max_pages=2), [[1] * 40], [1], 100)
+
+
+def _restated_arrivals(prompts, decode_lens, arrivals, vocab, max_slots, step_ms):
+    """src/bench_batching.cpp:98-179 on a virtual clock: at the top of each
+    iteration free slots admit, in order, the requests whose arrival_ms has
+    passed (:108-121); with no active slot the loop waits for the next
+    arrival (:153-158); a forward step takes step_ms; a request finishes at
+    the clock after its last step (:162-172)."""
+    slots = [None] * max_slots
+    nxt, done, seq_counter, clock = 0, 0, 0, 0.0
+    toks = [[] for _ in prompts]
+    finish = [0.0] * len(prompts)
+    steps = []
+    while done < len(prompts):
+        now = clock
+        for k in range(max_slots):
+            if slots[k] is not None:
+                continue
+            if nxt >= len(prompts) or arrivals[nxt] > now:
+                break
+            slots[k] = {"req": nxt, "sid": seq_counter, "pos": 0, "pre": False, "last": 0, "gen": 0}
+            nxt += 1
+            seq_counter += 1
+        rows, owners, lasts = [], [], []
+        for s in slots:
+            if s is None:
+                continue
+            p = prompts[s["req"]]
+            if not s["pre"]:
+                for q in range(len(p)):
+                    rows.append((p[q], q, s["sid"]))
+                    owners.append(s)
+                    lasts.append(q == len(p) - 1)
+                s["pos"], s["pre"] = len(p), True
+            else:
+                rows.append((s["last"], s["pos"], s["sid"]))
+                owners.append(s)
+                lasts.append(True)
+                s["pos"] += 1
+        if not rows:
+            clock += max(0.0, arrivals[nxt] - now)
+            continue
+        steps.append(rows)
+        clock += step_ms
+        for (t, q, sid), s, last in zip(rows, owners, lasts):
+            if not last:
+                continue
+            tok = _stand_in(t, q, sid, vocab)
+            s["last"] = tok
+            s["gen"] += 1
+            toks[s["req"]].append(tok)
+            if s["gen"] >= decode_lens[s["req"]]:
+                finish[s["req"]] = clock
+                slots[slots.index(s)] = None
+                done += 1
+    return toks, steps, finish
+
+
+@settings(max_examples=30, deadline=None)
+@given(seed=st.integers(0, 10 ** 6), n=st.integers(1, 12), slots=st.integers(1, 6),
+       gap=st.sampled_from([0.0, 0.5, 2.0, 7.5]))
+def test_arrival_schedule_matches_restatement(cbis, seed, n, slots, gap):
+    """Arrival-time admission on the dry run's virtual clock (1 ms steps):
+    requests arriving on a random walk of mean `gap` ms are admitted only
+    once their time has passed, an idle scheduler jumps to the next arrival,
+    and the finish times are the clock after each request's last step."""
+    prompts, dl = _workload(seed, n, 1, 30, 1, 6)
+    rng = random.Random(seed + 1)
+    arrivals, t = [], 0.0
+    for _ in range(n):
+        t += rng.random() * 2 * gap
+        arrivals.append(round(t, 3))
+    c = _cache(cbis)
+    toks, steps, fin = cbis.schedule_dry_run(c, prompts, dl, 300, max_slots=slots, arrival_ms=arrivals,
+                                             step_time_ms=1.0)
+    rtoks, rsteps, rfin = _restated_arrivals(prompts, dl, arrivals, 300, slots, 1.0)
+    assert steps == rsteps and toks == rtoks
+    assert fin == pytest.approx(rfin)
+    assert all(f >= a for f, a in zip(fin, arrivals))
+    assert c.num_free_pages() == 4096
+
+
+def test_arrivals_at_zero_are_the_plain_schedule(cbis):
+    prompts, dl = _workload(5, 9, 1, 40, 1, 8)
+    plain = cbis.schedule_dry_run(_cache(cbis), prompts, dl, 500, max_slots=4)
+    timed = cbis.schedule_dry_run(_cache(cbis), prompts, dl, 500, max_slots=4, arrival_ms=[0.0] * 9)
+    assert timed[:2] == plain
+
+
+def test_arrivals_rejected_when_unordered(cbis):
+    with pytest.raises(RuntimeError, match="arrival_ms"):
+        cbis.schedule_dry_run(_cache(cbis), [[1], [2]], [1, 1], 100, arrival_ms=[5.0, 1.0])
+    with pytest.raises(RuntimeError, match="arrival_ms"):
+        cbis.schedule_dry_run(_cache(cbis), [[1]], [1], 100, arrival_ms=[-1.0])

@@ -60,6 +60,27 @@ def test_c1_greedy_continuous_batching(cbis, oracle):
     assert cache.num_free_pages() == 128  # every sequence freed its pages
 
 
+def test_c1_greedy_with_arrivals(cbis, oracle):
+    """Config 1's requests arriving over time (src/bench_batching.cpp:110-121:
+    admitted once their arrival_ms has passed, the scheduler idling until the
+    first arrives) with only 3 slots: every request's greedy tokens are still
+    python/model.py's -- each row of a step is computed independently of the
+    rows batched with it -- and each finishes after it arrives."""
+    g = np.load(os.path.join(GOLDEN, "g2_c1_greedy.npz"))
+    n = int(g["n"])
+    prompts = [[int(t) for t in g[f"prompt{i}"]] for i in range(n)]
+    cfg, w = _ref_model(cbis, vocab=512)
+    cache = cbis.PagedKVCache(4, 128, 16, 8, 32, "f32")
+    runner = cbis.TransformerRunner(w, cache, 512)
+    arrivals = [5.0 + 2.0 * i for i in range(n)]
+    toks, step_ms, fin = cbis.run_continuous(runner, cache, prompts, [32] * n, max_slots=3, arrival_ms=arrivals)
+    for i in range(n):
+        assert toks[i] == [int(t) for t in g[f"gen{i}"]], i
+    assert all(f > a for f, a in zip(fin, arrivals))
+    assert len(step_ms) > 32
+    assert cache.num_free_pages() == 128
+
+
 @pytest.mark.parametrize("chunk,budget", [(16, 0), (8, 40)])
 def test_c1_chunked_prefill_greedy(cbis, oracle, chunk, budget):
     """Config 1's workload with the prompts fed in chunks (at most `chunk`
