@@ -278,6 +278,84 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArg
   decode_merge(a, n_rows, (int64_t)blockIdx.x * 256 + threadIdx.x);
 }
 
+// The reference-signature attention for page sizes other than kPS (fp32
+// Q/K/V/out, head_dim kHD, any page_size > 0; kernels/attention.cu:57-98 takes
+// page_size at run time).  One wave per (row, head), four per workgroup.  Lane
+// l takes key j = c + l of every 64-key chunk c: it looks up page
+// table[j / page_size] and slot j % page_size, forms q.k over the head's 32
+// dims from 8 16-byte loads, and the wave runs one online-softmax step per
+// chunk (chunk maximum and probability sum by wave reductions, so m and l are
+// the same in every lane).  Each lane accumulates p_j v_j over its own keys;
+// the 32 output dims are summed across the wave at the end.
+__global__ __launch_bounds__(256) void paged_attention_any_page_kernel(const float* __restrict__ Q,
+                                                                       const float* __restrict__ kp,
+                                                                       const float* __restrict__ vp,
+                                                                       const int* __restrict__ table,
+                                                                       const int* __restrict__ row_pos,
+                                                                       float* __restrict__ out, int total_rows,
+                                                                       int n_heads, int page_size, int pages_per_seq,
+                                                                       float qscale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= (int64_t)total_rows * n_heads) return;
+  const int row = (int)(unit / n_heads), head = (int)(unit % n_heads);
+  const int64_t D = (int64_t)n_heads * kHD;
+  const int kv_len = (int)min((int64_t)row_pos[row] + 1, (int64_t)pages_per_seq * page_size);
+  if (kv_len <= 0) return;
+  const float* qp = Q + row * D + head * kHD;
+  float q[kHD];
+#pragma unroll
+  for (int e = 0; e < kHD; e += 4) {
+    const float4 v = *(const float4*)(qp + e);
+    q[e] = v.x * qscale; q[e + 1] = v.y * qscale; q[e + 2] = v.z * qscale; q[e + 3] = v.w * qscale;
+  }
+  const int* tab = table + (int64_t)row * pages_per_seq;
+  float m = -INFINITY, l = 0.f, acc[kHD];
+#pragma unroll
+  for (int e = 0; e < kHD; ++e) acc[e] = 0.f;
+  for (int c = 0; c < kv_len; c += 64) {
+    const int j = c + lane;
+    const bool valid = j < kv_len;
+    float s = -INFINITY;
+    float4 vv[kHD / 4];
+    if (valid) {
+      const int64_t slot = ((int64_t)tab[j / page_size] * page_size + j % page_size) * D + head * kHD;
+      float4 kk[kHD / 4];
+#pragma unroll
+      for (int i = 0; i < kHD / 4; ++i) kk[i] = *(const float4*)(kp + slot + 4 * i);
+#pragma unroll
+      for (int i = 0; i < kHD / 4; ++i) vv[i] = *(const float4*)(vp + slot + 4 * i);
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < kHD / 4; ++i)
+        d += q[4 * i] * kk[i].x + q[4 * i + 1] * kk[i].y + q[4 * i + 2] * kk[i].z + q[4 * i + 3] * kk[i].w;
+      s = d;
+    } else {
+#pragma unroll
+      for (int i = 0; i < kHD / 4; ++i) vv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float mn = fmaxf(m, wave_max(s));  // finite: lane 0's key is valid
+    const float corr = fast_exp2(m - mn);
+    const float p = valid ? fast_exp2(s - mn) : 0.f;
+    l = l * corr + wave_sum(p);
+#pragma unroll
+    for (int i = 0; i < kHD / 4; ++i) {
+      acc[4 * i] = acc[4 * i] * corr + p * vv[i].x;
+      acc[4 * i + 1] = acc[4 * i + 1] * corr + p * vv[i].y;
+      acc[4 * i + 2] = acc[4 * i + 2] * corr + p * vv[i].z;
+      acc[4 * i + 3] = acc[4 * i + 3] * corr + p * vv[i].w;
+    }
+    m = mn;
+  }
+  float mine = 0.f;
+#pragma unroll
+  for (int e = 0; e < kHD; ++e) {
+    const float t = wave_sum(acc[e]);
+    if (lane == e) mine = t;
+  }
+  if (lane < kHD) out[row * D + head * kHD + lane] = mine / l;
+}
+
 // ---------------------------------------------------------------------------
 // Prefill on MFMA.
 // ---------------------------------------------------------------------------
@@ -918,6 +996,22 @@ int cbis_paged_attention_mixed(const cbis_attn_desc* d, int n_tiles, const int* 
 int cbis_fused_paged_causal_attention(const float* Q, const float* kp, const float* vp, const int* row_page_table,
                                       const int* row_query_pos, float* out, int total_rows, int n_heads, int head_dim,
                                       int page_size, int pages_per_seq, cbis_stream_t stream) {
+  if (page_size != kPS && head_dim == kHD) {
+    const char* who = "cbis_fused_paged_causal_attention";
+    CBIS_REQUIRE(total_rows >= 0 && n_heads > 0 && page_size > 0 && pages_per_seq > 0, CBIS_ERR_INVALID,
+                 "%s: total_rows %d, n_heads %d, page_size %d, pages_per_seq %d", who, total_rows, n_heads, page_size,
+                 pages_per_seq);
+    CBIS_REQUIRE(Q && kp && vp && row_page_table && row_query_pos && out, CBIS_ERR_INVALID, "%s: null pointer", who);
+    CBIS_REQUIRE(((uintptr_t)Q & 15u) == 0 && ((uintptr_t)kp & 15u) == 0 && ((uintptr_t)vp & 15u) == 0, CBIS_ERR_INVALID,
+                 "%s: Q and the pools must be 16-byte aligned", who);
+    const int64_t units = (int64_t)total_rows * n_heads;
+    if (units == 0) return CBIS_OK;
+    CBIS_REQUIRE(cdiv(units, 4) < (1LL << 31), CBIS_ERR_UNSUPPORTED, "%s: grid too large", who);
+    paged_attention_any_page_kernel<<<(unsigned)cdiv(units, 4), 256, 0, (hipStream_t)stream>>>(
+        Q, kp, vp, row_page_table, row_query_pos, out, total_rows, n_heads, page_size, pages_per_seq,
+        kLog2e / sqrtf((float)kHD));
+    return check_launch(who);
+  }
   cbis_attn_desc d = {};
   d.n_rows = total_rows;
   d.n_heads = n_heads;

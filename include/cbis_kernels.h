@@ -90,9 +90,12 @@ int cbis_scatter_kv_to_cache(const float* K_proj, const float* V_proj, float* k_
 /* Causal paged attention with the reference's per-row page table
  * row_page_table[total_rows, pages_per_seq]; kv_len = row_query_pos[r] + 1.
  * Replaces fused_paged_causal_attention, include/attention.hpp:29-33
- * (kernels/attention.cu:57-127).  Runs the wave64 decode kernel in a single
- * pass per (row, head block): it needs no workspace.  Supported: head_dim 32,
- * page_size 16, any n_heads (the reference's grid(total_rows, n_heads)). */
+ * (kernels/attention.cu:57-127).  Needs no workspace.  page_size 16 runs the
+ * wave64 decode kernel in a single pass per (row, head block); any other
+ * page_size > 0 runs a one-wave-per-(row, head) kernel whose lanes take one
+ * key each (the reference takes page_size at run time).  head_dim 32, as the
+ * reference's one-warp-per-(row, head) kernel requires; any n_heads (the
+ * reference's grid(total_rows, n_heads)). */
 int cbis_fused_paged_causal_attention(const float* Q_proj, const float* k_pages, const float* v_pages,
                                       const int* row_page_table, const int* row_query_pos, float* attn_out,
                                       int total_rows, int n_heads, int head_dim, int page_size,

@@ -809,6 +809,65 @@ def _c3_inputs(oracle, n_seq=256, lo=128, hi=2048, pool=40000, seed=0):
     return kv.astype(np.int32), bt
 
 
+@pytest.mark.parametrize("page_size", [1, 3, 8, 16, 32, 64])
+def test_fused_attention_twin_any_page_size(cbis, oracle, dev, page_size):
+    """The reference signature takes page_size at run time
+    (include/attention.hpp:29-33).  Rows of kv 1, a page boundary either side,
+    a few chunks of 64 keys and 300; 5 heads; a permuted pool; rows 2 and 3
+    share a sequence's table; one row attends with pos past its table's
+    capacity (kv clamped to pages_per_seq * page_size, as the page_size 16
+    path clamps).  Against the fp64 oracle at the same page size."""
+    import torch
+    H, HD = 5, 32
+    kv = np.array([1, page_size, page_size + 1, 64, 65, 129, 300], np.int32)
+    S = kv.size
+    npages = (kv + page_size - 1) // page_size
+    stride = int(npages.max())
+    P = int(npages.sum()) + 7
+    perm = rng(page_size).permutation(P).astype(np.int32)
+    bt = np.zeros((S, stride), np.int32)
+    off = 0
+    for i in range(S):
+        bt[i, : npages[i]] = perm[off: off + npages[i]]
+        off += npages[i]
+    bt[3] = bt[2]  # row 3 reads row 2's sequence at a later position...
+    kv[3] = kv[2] + 3 if kv[2] + 3 <= npages[2] * page_size else kv[2]
+    pos = kv - 1
+    pos_dev = pos.copy()
+    pos_dev[-1] = stride * page_size + 50  # ...and the last row asks past its table
+    g = rng(100 + page_size)
+    kpool = g.standard_normal((P, page_size, H, HD)).astype(np.float32)
+    vpool = g.standard_normal((P, page_size, H, HD)).astype(np.float32)
+    q = g.standard_normal((S, H * HD)).astype(np.float32)
+    out = torch.full((S, H * HD), 7.0, dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    QD, KD, VD = to_dev(q, dev), to_dev(kpool, dev), to_dev(vpool, dev)
+    BT, POS = to_dev(bt, dev), to_dev(pos_dev.astype(np.int32), dev)
+    cbis.check(K.cbis_fused_paged_causal_attention(ptr(QD), ptr(KD), ptr(VD), ptr(BT), ptr(POS), ptr(out), S, H, HD,
+                                                   page_size, stride, stream()))
+    sync()
+    pos_ref = pos.copy()
+    pos_ref[-1] = stride * page_size - 1  # the clamp
+    ref = oracle.paged_attention(q, kpool, vpool, bt, pos_ref, H, HD, page_size)
+    assert np.abs(out.cpu().numpy() - ref).max() < FP32_TOL
+    # the single-key row is exactly its V
+    assert np.abs(out.cpu().numpy()[0] - vpool[bt[0, 0], 0].reshape(-1)).max() < 1e-6
+
+
+def test_fused_attention_twin_rejects_bad_page_size(cbis, dev):
+    import torch
+    x = torch.zeros(64, dtype=torch.float32, device=dev)
+    i = torch.zeros(4, dtype=torch.int32, device=dev)
+    K = cbis.kernels()
+    for ps in (0, -16):
+        rc = K.cbis_fused_paged_causal_attention(ptr(x), ptr(x), ptr(x), ptr(i), ptr(i), ptr(x), 1, 1, 32, ps, 1,
+                                                 stream())
+        assert rc == 1  # CBIS_ERR_INVALID
+    rc = K.cbis_fused_paged_causal_attention(ptr(x), ptr(x), ptr(x), ptr(i), ptr(i), ptr(x), 1, 1, 64, 8, 1, stream())
+    assert rc == 2  # CBIS_ERR_UNSUPPORTED: the reference kernel needs head_dim 32 too
+    sync()
+
+
 def test_decode_attention_c3_full_size(cbis, oracle, dev):
     """BASELINE config 3 at full size: 256 sequences, kv U[128, 2048], 8x32,
     fp32 K/V in a 40,000-page pool with a permuted page table."""
