@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the per-step forward on one MI355X.
 
-Default workload: the mid-size GPT (16 layers, d 2048,
+Default workload (config 4): the mid-size GPT (16 layers, d 2048,
 64x32 heads, MLP 8192, vocab 32000, bf16 weights with fp32 accumulation, bf16
 paged K/V) running one mixed continuous-batch step of 192 decode rows
 (kv_len U[256, 4096] over synthetic cached K/V) plus two 512-row prefill
@@ -909,7 +909,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=["c4", "c1", "c2", "c3", "c5", "gemm", "tiering"],
-                    help="c4: the bench line (default); c1 / c2 / c3 / c5: the other BASELINE configs; "
+                    help="c4: the bench line (default); c1 / c2 / c3 / c5: the other configs; "
                          "gemm: config 4's GEMM shapes alone; tiering: the tiered K/V prefix restore")
     ap.add_argument("--shapes", default=None, help="--config gemm: comma list of qkv,out,fc1,fc2,lm_head")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")

@@ -147,7 +147,7 @@ uint8_t orc_f32_to_e4m3(float f) {
 /* Per-output-channel absmax quantisation of w [N, K] (fp32): scale[n] =
  * max_k |w[n,k]| / 448 in fp32 (1 for an all-zero row), codes[n,k] =
  * e4m3_rne(w[n,k] / scale[n]) with the quotient rounded to fp32 first.
- * BASELINE config 5's weight format; rows in parallel. */
+ * config 5's weight format; rows in parallel. */
 void orc_quantize_e4m3_rows(int64_t N, int64_t K, const float* w, uint8_t* codes, float* scale) {
 #pragma omp parallel for schedule(static)
   for (int64_t n = 0; n < N; ++n) {

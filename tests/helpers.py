@@ -45,7 +45,7 @@ def row_rel_err(got, ref):
 
 
 def check_logits(got, ref, what):
-    """north_star's bf16/fp8 bar: per row ||d||_inf / ||ref||_inf <= 2e-2,
+    """The bf16/fp8 parity bar: per row ||d||_inf / ||ref||_inf <= 2e-2,
     and the greedy token equal wherever the oracle's top-2 margin exceeds
     twice the row's measured error.  Returns the oracle's argmax per row."""
     err = row_rel_err(got, ref)

@@ -6,7 +6,7 @@ layer runs: 3.6 GB for config 4, 4.3 GB for config 5, where the whole
 correctness harness, which diffs the whole model's logits
 (src/correctness_check.cpp:55-94).
 
-Bar (north_star): per row ||d||_inf / ||ref||_inf <= 2e-2 over the logits,
+Bar: per row ||d||_inf / ||ref||_inf <= 2e-2 over the logits,
 greedy tokens equal wherever the oracle's top-2 margin exceeds twice the
 row's measured error, the fused greedy path's tokens and margins bit-equal
 to the argmax and top-2 of the full logits.

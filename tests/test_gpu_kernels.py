@@ -1,7 +1,7 @@
 """Kernel-level parity of the HIP path (through the C-ABI) against the CPU
 oracle on the same seeded inputs.
 
-Tolerances (north_star): fp32 paths 1e-4 max-abs; bf16 / fp8 paths 2e-2
+Tolerances: fp32 paths 1e-4 max-abs; bf16 / fp8 paths 2e-2
 relative (per row ||d||_inf / ||ref||_inf); integer / byte work bit-exact.
 """
 import ctypes
@@ -87,7 +87,7 @@ def test_convert_bf16_and_fp8_quantise_bit_exact(cbis, oracle, dev):
 # GEMM
 # --------------------------------------------------------------------------
 
-C2_SHAPES = [  # (name, N, K, bias, gelu, residual)
+C2_SHAPES = [  # (name, N, K, bias, gelu, residual): config 2
     ("qkv", 768, 256, True, False, False),
     ("out", 256, 256, True, False, False),
     ("up", 1024, 256, True, True, False),
@@ -869,7 +869,7 @@ def test_fused_attention_twin_rejects_bad_page_size(cbis, dev):
 
 
 def test_decode_attention_c3_full_size(cbis, oracle, dev):
-    """BASELINE config 3 at full size: 256 sequences, kv U[128, 2048], 8x32,
+    """Config 3 at full size: 256 sequences, kv U[128, 2048], 8x32,
     fp32 K/V in a 40,000-page pool with a permuted page table."""
     import torch
     H, P = 8, 40000
@@ -1166,7 +1166,7 @@ def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows, tile):
     ref = oracle.paged_attention(q.cpu().numpy(), bits_u16(kp), bits_u16(vp), np.repeat(bt, n_rows, 0), pos, H, 32,
                                  16, kv_dtype=1)
     got = out.float().cpu().numpy()
-    # north_star's bf16 metric: per row, ||d||_inf / ||ref||_inf over the
+    # The bf16 parity metric: per row, ||d||_inf / ||ref||_inf over the
     # row's H * head_dim outputs.  Q and P are rounded to bf16 for the MFMAs.
     err_row = row_rel_err(got, ref)
     err_head = row_rel_err(got.reshape(n_rows * H, 32), ref.reshape(n_rows * H, 32))

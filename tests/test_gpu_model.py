@@ -44,7 +44,7 @@ def test_g1_reference_dims_logits(cbis):
 
 
 def test_c1_greedy_continuous_batching(cbis, oracle):
-    """8 prompts U[16,64], 32 greedy tokens each through
+    """Config 1: 8 prompts U[16,64], 32 greedy tokens each through
     the continuous-batching scheduler -- tokens identical to python/model.py's
     full-recompute greedy decode (tests/golden/g2_c1_greedy.npz)."""
     g = np.load(os.path.join(GOLDEN, "g2_c1_greedy.npz"))
@@ -320,7 +320,7 @@ def test_packed_checkpoint_round_trip(cbis, tmp_path, wdt):
 
 
 # --------------------------------------------------------------------------
-# Whole steps at the BASELINE configs' own workloads (1-2 of their 16
+# Whole steps at configs 4 and 5's own workloads (1-2 of their 16
 # layers), the counterpart of src/correctness_check.cpp:55-94 (a full step
 # diffed against the model).
 # --------------------------------------------------------------------------
@@ -359,7 +359,7 @@ def _big_setup(cbis, oracle, wdt, n_layers, max_pages, max_seq, fill_seed):
 
 
 def test_c4_step_at_config_workload(cbis, oracle):
-    """BASELINE config 4's step exactly as bench.py builds it, on 2 of the 16
+    """Config 4's step exactly as bench.py builds it, on 2 of the 16
     layers: 192 decode rows with kv U[256, 4096] (the seed-0 draw) over a
     shuffled page table plus two 512-row prefill chunks (a fresh sequence at
     positions 0..511 and one with 512 cached tokens at 512..1023), M = 1216.
@@ -398,7 +398,7 @@ def test_c4_step_at_config_workload(cbis, oracle):
 
 
 def test_c5_decode_at_config_workload(cbis, oracle):
-    """BASELINE config 5's decode on 1 of the 16 layers: fp8-e4m3 weights
+    """Config 5's decode on 1 of the 16 layers: fp8-e4m3 weights
     with per-channel scales, bf16 K/V, 16 sequences whose caches hold 32704
     synthetic tokens, greedy steps at positions 32704, 32705, 32706 through
     the runner's own split choice (8192-token splits: one CU's share of the
