@@ -171,22 +171,71 @@ void orc_quantize_e4m3_rows(int64_t N, int64_t K, const float* w, uint8_t* codes
  * docs/gemm_layout.md:16-41) with the separate bias/GELU/residual launches of
  * kernels/linear.cu:6-12 and kernels/elementwise.cu:59-73 applied in the
  * order src/transformer.cpp:82-89 uses. */
+typedef double orc_v4d __attribute__((vector_size(32)));
+enum { kGemmRows = 4, kGemmCols = 8 };
+
+/* acc[i][j] = sum over k = 0 .. K-1, in that order, of x_i[k] * wt[k][j] for
+ * kGemmRows rows x_i and the kGemmCols columns packed in wt ([K][8] doubles).
+ * Every output keeps one accumulator summed in k order, so the result is the
+ * plain loop's bit for bit (a float x float product is exact in fp64); the
+ * vectors only run 8 outputs side by side.  Built for AVX2 and for the
+ * baseline ISA, chosen at load time. */
+__attribute__((target_clones("avx2", "default"))) static void gemm_tile(int K, const float* const* xr,
+                                                                         const double* wt,
+                                                                         double out[kGemmRows][kGemmCols]) {
+  orc_v4d acc[kGemmRows][2];
+  for (int i = 0; i < kGemmRows; ++i) acc[i][0] = acc[i][1] = (orc_v4d){0.0, 0.0, 0.0, 0.0};
+  for (int k = 0; k < K; ++k) {
+    const orc_v4d w0 = *(const orc_v4d*)(wt + 8 * (int64_t)k);
+    const orc_v4d w1 = *(const orc_v4d*)(wt + 8 * (int64_t)k + 4);
+    for (int i = 0; i < kGemmRows; ++i) {
+      const double xv = (double)xr[i][k];
+      const orc_v4d xb = {xv, xv, xv, xv};
+      acc[i][0] += xb * w0;
+      acc[i][1] += xb * w1;
+    }
+  }
+  for (int i = 0; i < kGemmRows; ++i)
+    for (int j = 0; j < 4; ++j) {
+      out[i][j] = acc[i][0][j];
+      out[i][4 + j] = acc[i][1][j];
+    }
+}
+
 void orc_gemm(int M, int N, int K, const float* X, int ldx, const float* W, int ldw,
               const float* w_scale, const float* bias, int gelu, const float* residual, int ldr,
               double* Y, int ldy) {
-#pragma omp parallel for schedule(dynamic, 1)
-  for (int m = 0; m < M; ++m) {
-    const float* x = X + (int64_t)m * ldx;
-    for (int n = 0; n < N; ++n) {
-      const float* w = W + (int64_t)n * ldw;
-      double acc = 0.0;
-      for (int k = 0; k < K; ++k) acc += (double)x[k] * (double)w[k];
-      if (w_scale) acc *= (double)w_scale[n];
-      if (bias) acc += (double)bias[n];
-      if (gelu) acc = 0.5 * acc * (1.0 + erf(acc * 0.70710678118654752440));
-      if (residual) acc += (double)residual[(int64_t)m * ldr + n];
-      Y[(int64_t)m * ldy + n] = acc;
+  const int nblocks = (N + kGemmCols - 1) / kGemmCols;
+#pragma omp parallel
+  {
+    /* this thread's packed column block: W[n0 .. n0 + 7][0 .. K-1] as [K][8]
+     * doubles, zero past N (those columns are never stored) */
+    double* wt = (double*)aligned_alloc(64, ((size_t)(K > 0 ? K : 1) * kGemmCols * sizeof(double) + 63) / 64 * 64);
+#pragma omp for schedule(dynamic, 1)
+    for (int nb = 0; nb < nblocks; ++nb) {
+      const int n0 = nb * kGemmCols;
+      for (int j = 0; j < kGemmCols; ++j) {
+        const float* w = W + (int64_t)(n0 + j) * ldw;
+        for (int k = 0; k < K; ++k) wt[(int64_t)k * kGemmCols + j] = n0 + j < N ? (double)w[k] : 0.0;
+      }
+      for (int m0 = 0; m0 < M; m0 += kGemmRows) {
+        const float* xr[kGemmRows];
+        for (int i = 0; i < kGemmRows; ++i) xr[i] = X + (int64_t)(m0 + i < M ? m0 + i : M - 1) * ldx;
+        double t[kGemmRows][kGemmCols];
+        gemm_tile(K, xr, wt, t);
+        for (int i = 0; i < kGemmRows && m0 + i < M; ++i)
+          for (int j = 0; j < kGemmCols && n0 + j < N; ++j) {
+            const int m = m0 + i, n = n0 + j;
+            double acc = t[i][j];
+            if (w_scale) acc *= (double)w_scale[n];
+            if (bias) acc += (double)bias[n];
+            if (gelu) acc = 0.5 * acc * (1.0 + erf(acc * 0.70710678118654752440));
+            if (residual) acc += (double)residual[(int64_t)m * ldr + n];
+            Y[(int64_t)m * ldy + n] = acc;
+          }
+      }
     }
+    free(wt);
   }
 }
 
