@@ -126,6 +126,31 @@ def test_gemm_pins(oracle):
     assert np.allclose(oracle.gemm(Xf, Wf, gelu=True), torch.nn.functional.gelu(z).numpy(), atol=1e-12)
 
 
+def test_gemm_sums_each_output_in_k_order(oracle):
+    """orc_gemm runs blocks of outputs side by side on fp64 vectors; every
+    output must still be the plain loop's fp64 sum over k in order (bit for
+    bit), including ragged row and column blocks, K = 0 and the epilogues."""
+    import math
+    rng = np.random.default_rng(5)
+    for M, N, K in ((1, 1, 1), (3, 5, 7), (6, 9, 33), (4, 8, 0), (9, 17, 70)):
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        W = rng.standard_normal((N, K)).astype(np.float32)
+        s = rng.uniform(0.5, 2, N).astype(np.float32)
+        b = rng.standard_normal(N).astype(np.float32)
+        R = rng.standard_normal((M, N)).astype(np.float32)
+        for kw in ({}, {"w_scale": s, "bias": b, "gelu": True, "residual": R}):
+            got = oracle.gemm(X, W, **kw)
+            for m in range(M):
+                for n in range(N):
+                    acc = 0.0
+                    for k in range(K):
+                        acc += float(X[m, k]) * float(W[n, k])
+                    if kw:
+                        acc = acc * float(s[n]) + float(b[n])
+                        acc = 0.5 * acc * (1.0 + math.erf(acc * 0.70710678118654752440)) + float(R[m, n])
+                    assert got[m, n] == acc, (M, N, K, m, n, kw != {})
+
+
 def test_layernorm_pins(oracle):
     import torch
     rng = np.random.default_rng(1)
