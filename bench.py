@@ -587,7 +587,9 @@ def run_c1(args, cbis, oracle):
     """Config 1: tiny fp32 GPT (V=512, d=256, 8x32, L=4, MLP 1024), 8 prompts
     U[16,64], 32 greedy tokens each through the C++ continuous-batching
     scheduler (1 prefill step + 31 decode steps of 8 rows).  value = decode
-    tokens / decode-step wall time (median of `steps` runs)."""
+    tokens / decode wall time (median of `steps` runs) of the pipelined
+    scheduler, which queues each step before the previous step's tokens are
+    back; the synchronous scheduler's rate is reported beside it."""
     reqs = oracle.c1_requests()
     cfg = cbis.ModelConfig.make(vocab=512, n_layers=4)
     w = cbis.ModelWeights.synthetic(cfg, seed=0)
@@ -595,20 +597,29 @@ def run_c1(args, cbis, oracle):
     runner = cbis.TransformerRunner(w, cache, 512)
     prompts = [r.prompt for r in reqs]
     dl = [r.decode_len for r in reqs]
-    dec, tot, toks = [], [], None
-    with gc_paused():
-        for _ in range(max(1, args.warmup)):
-            cbis.run_continuous(runner, cache, prompts, dl)
-        for _ in range(args.steps):
-            toks, ms = cbis.run_continuous(runner, cache, prompts, dl)
-            dec.append(sum(ms[1:]))
-            tot.append(sum(ms))
     n_dec = sum(d - 1 for d in dl)
     n_prompt = sum(len(p) for p in prompts)
-    dec_ms, tot_ms = float(np.median(dec)), float(np.median(tot))
-    value = n_dec / dec_ms * 1000.0
-    _log(f"c1: decode {dec_ms:.3f} ms for {n_dec} tokens -> {value:.0f} tok/s; whole run {tot_ms:.3f} ms "
-         f"({(n_prompt + sum(dl)) / tot_ms * 1000.0:.0f} prompt+generated tok/s)")
+    rate = {}
+    toks = {}
+    with gc_paused():
+        for pipe in (False, True):
+            dec, tot = [], []
+            for _ in range(max(1, args.warmup)):
+                cbis.run_continuous(runner, cache, prompts, dl, pipeline=pipe)
+            for _ in range(args.steps):
+                toks[pipe], ms = cbis.run_continuous(runner, cache, prompts, dl, pipeline=pipe)
+                # Step 0 is the prefill; the rest, in the pipelined mode the
+                # intervals between consecutive steps' results, the decode.
+                dec.append(sum(ms[1:]))
+                tot.append(sum(ms))
+            dec_ms, tot_ms = float(np.median(dec)), float(np.median(tot))
+            rate[pipe] = (n_dec / dec_ms * 1000.0, dec_ms, tot_ms)
+            _log(f"c1 {'pipelined' if pipe else 'synchronous'}: decode {dec_ms:.3f} ms for {n_dec} tokens -> "
+                 f"{rate[pipe][0]:.0f} tok/s; whole run {tot_ms:.3f} ms "
+                 f"({(n_prompt + sum(dl)) / tot_ms * 1000.0:.0f} prompt+generated tok/s)")
+    assert toks[True] == toks[False], "pipelined and synchronous greedy tokens differ"
+    value, dec_ms, tot_ms = rate[True]
+    toks = toks[True]
     cpu = None
     if not args.no_cpu:
         spec = oracle.ModelSpec(vocab=512, n_layers=4, max_seq=128)
@@ -625,7 +636,8 @@ def run_c1(args, cbis, oracle):
             "unit": "decode tokens/s", "ms_per_step": round(dec_ms / (len(dl) and 31), 4), "dtype": "f32",
             "data": "synthetic (seeded weights N(0,0.02); prompt ids U[0,511])",
             "config": {"workload": "c1_tiny_gpt_greedy", "requests": len(dl), "prompt_len": "U[16,64]",
-                       "decode_len": 32, "whole_run_ms": round(tot_ms, 3)},
+                       "decode_len": 32, "scheduler": "pipelined", "whole_run_ms": round(tot_ms, 3),
+                       "synchronous_decode_tok_s": round(rate[False][0], 1)},
             "cpu_baseline": cpu}
 
 

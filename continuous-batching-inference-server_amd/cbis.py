@@ -105,6 +105,7 @@ KERNEL_SYMBOLS = {
     "cbis_paged_prefill_attention": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
     "cbis_paged_attention_mixed": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
     "cbis_embed": (_I, [_I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P]),
+    "cbis_embed_from": (_I, [_I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _SZ, _P]),
     "cbis_layernorm": (_I, [_I, _I, _P, _I64, _P, _P, _F, _I, _P, _I64, _P]),
     "cbis_argmax_rows": (_I, [_I, _I, _P, _I64, _P, _P]),
     "cbis_fill_normal_exact": (_I, [_P, _I, _I64, _U64, _U64, _U64, _F, _P]),
@@ -141,6 +142,8 @@ RUNTIME_SYMBOLS = {
     "cbis_runner_destroy": (None, [_P]),
     "cbis_runner_forward_step": (_I, [_P, _I, _IP, _IP, _IP, ctypes.POINTER(ctypes.c_float)]),
     "cbis_runner_forward_step_greedy": (_I, [_P, _I, _IP, _IP, _IP, _IP]),
+    "cbis_runner_enqueue_greedy": (_I, [_P, _I, _IP, _IP, _IP, _IP, ctypes.POINTER(ctypes.c_int64)]),
+    "cbis_runner_wait_greedy": (_I, [_P, ctypes.c_int64, _IP, _I]),
     "cbis_runner_logits_device": (_P, [_P]),
     "cbis_runner_stream": (_P, [_P]),
     "cbis_runner_set_graphs": (None, [_P, _I]),
@@ -175,6 +178,11 @@ RUNTIME_SYMBOLS = {
     "cbis_schedule_dry_run_timed": (_I, [_P, _I, _IP, _IP, _IP, ctypes.POINTER(ctypes.c_double), ctypes.c_double, _I,
                                          _I, _I, _I, _IP, _IP, _I, _IP, _IP, _IP, _I,
                                          ctypes.POINTER(ctypes.c_double)]),
+    "cbis_run_continuous_pipelined": (_I, [_P, _P, _I, _IP, _IP, _IP, ctypes.POINTER(ctypes.c_double), _I, _I, _I,
+                                           _IP, ctypes.POINTER(ctypes.c_double), _I, ctypes.POINTER(ctypes.c_double)]),
+    "cbis_schedule_dry_run_pipelined": (_I, [_P, _I, _IP, _IP, _IP, ctypes.POINTER(ctypes.c_double), ctypes.c_double,
+                                             _I, _I, _I, _I, _IP, _IP, _I, _IP, _IP, _IP, _I,
+                                             ctypes.POINTER(ctypes.c_double)]),
 }
 
 _kern = None
@@ -366,6 +374,7 @@ class TransformerRunner:
     def __init__(self, weights: ModelWeights, cache: PagedKVCache, max_total_rows: int):
         self.weights, self.cache = weights, cache  # keep them alive
         self.vocab = weights.cfg.vocab
+        self._max_rows = max_total_rows
         self._h = _rt_check(runtime().cbis_runner_create(weights._h, cache._h, max_total_rows), "TransformerRunner")
 
     def close(self):
@@ -398,6 +407,23 @@ class TransformerRunner:
                                                             _iarr(seq_ids), out), "forward_step_greedy")
         return list(out[:n])
 
+    def enqueue_greedy(self, token_ids, positions, seq_ids, token_src=None) -> int:
+        """Queues a greedy step without waiting; returns its ticket.  A row
+        with token_src[i] >= 0 takes the greedy token of row token_src[i] of
+        the greedy step enqueued just before (token_ids[i] is not used)."""
+        n = len(token_ids)
+        ticket = ctypes.c_int64()
+        src = _iarr(token_src) if token_src is not None else None
+        _rt_check(runtime().cbis_runner_enqueue_greedy(self._h, n, _iarr(token_ids), _iarr(positions), _iarr(seq_ids),
+                                                       src, ctypes.byref(ticket)), "enqueue_greedy")
+        return ticket.value
+
+    def wait_greedy(self, ticket: int):
+        """Waits for a queued greedy step; returns the next token of every row."""
+        out = (ctypes.c_int * max(1, self._max_rows))()
+        n = _rt_check(runtime().cbis_runner_wait_greedy(self._h, ticket, out, len(out)), "wait_greedy")
+        return list(out[:n])
+
     def last_margins(self):
         """Top-2 margins of the last forward_step_greedy's rows (numpy fp32)."""
         n = _rt_check(runtime().cbis_runner_last_margins(self._h, None, 0), "last_margins")
@@ -411,12 +437,13 @@ class TransformerRunner:
 
     def last_device_ms(self) -> float:
         """Device time of the last step's forward (events on the runner's
-        stream around its kernels; the H2D / D2H of the step excluded)."""
+        stream around its kernels, which move the step's metadata and
+        results to and from pinned host memory themselves)."""
         return float(runtime().cbis_runner_last_device_ms(self._h))
 
     def last_host_ms(self):
-        """Host wall time of the last greedy step's phases: (preparation +
-        H2D enqueue, launch, wait for the results), ms."""
+        """Host wall time of the last greedy step's phases: (preparation,
+        launch, wait for the results), ms."""
         out = (ctypes.c_double * 3)()
         runtime().cbis_runner_last_host_ms(self._h, out)
         return tuple(out)
@@ -544,10 +571,13 @@ def _darr(values):
 
 
 def run_continuous(runner: TransformerRunner, cache: PagedKVCache, prompts, decode_lens, max_slots=16,
-                   max_steps=4096, prefill_chunk=0, step_token_budget=0, arrival_ms=None):
+                   max_steps=4096, prefill_chunk=0, step_token_budget=0, arrival_ms=None, pipeline=False):
     """Continuous batching (src/bench_batching.cpp:98-179); prefill_chunk /
     step_token_budget > 0 feed prompts in chunks; arrival_ms (nondecreasing)
-    admits request i only once that many ms of the run have passed.  Returns
+    admits request i only once that many ms of the run have passed.
+    pipeline=True queues each step before the previous one's tokens come
+    back (decode rows read their input token on the device): the same steps
+    and tokens, with the host's work hidden behind the device's.  Returns
     (tokens per request, per-step wall ms), plus the per-request finish
     times (ms since the run began) when arrival_ms is given."""
     lens = [len(p) for p in prompts]
@@ -556,10 +586,9 @@ def run_continuous(runner: TransformerRunner, cache: PagedKVCache, prompts, deco
     ms = (ctypes.c_double * max_steps)()
     fin = (ctypes.c_double * max(1, len(prompts)))()
     arr = _darr(arrival_ms) if arrival_ms is not None else None
-    n = _rt_check(runtime().cbis_run_continuous_timed(runner._h, cache._h, len(prompts), _iarr(lens), _iarr(flat),
-                                                      _iarr(decode_lens), arr, max_slots, prefill_chunk,
-                                                      step_token_budget, out, ms, max_steps, fin),
-                  "run_continuous")
+    fn = runtime().cbis_run_continuous_pipelined if pipeline else runtime().cbis_run_continuous_timed
+    n = _rt_check(fn(runner._h, cache._h, len(prompts), _iarr(lens), _iarr(flat), _iarr(decode_lens), arr, max_slots,
+                     prefill_chunk, step_token_budget, out, ms, max_steps, fin), "run_continuous")
     toks, o = [], 0
     for d in decode_lens:
         toks.append(list(out[o: o + d]))
@@ -570,11 +599,14 @@ def run_continuous(runner: TransformerRunner, cache: PagedKVCache, prompts, deco
 
 
 def schedule_dry_run(cache: PagedKVCache, prompts, decode_lens, vocab, max_slots=16, prefill_chunk=0,
-                     step_token_budget=0, max_steps=4096, max_rows=1 << 16, arrival_ms=None, step_time_ms=1.0):
+                     step_token_budget=0, max_steps=4096, max_rows=1 << 16, arrival_ms=None, step_time_ms=1.0,
+                     pipeline=False):
     """The scheduler alone, on the host, with the stand-in step of
-    cbis_schedule_dry_run.  Returns (tokens per request, [(tok, pos, sid)
-    rows of each step]); with arrival_ms, on a virtual clock where a step
-    takes step_time_ms, and the per-request finish times as a third value."""
+    cbis_schedule_dry_run (pipeline=True: the pipelined scheduler, whose
+    rows report the tokens the stand-in device resolved).  Returns (tokens
+    per request, [(tok, pos, sid) rows of each step]); with arrival_ms, on a
+    virtual clock where a step takes step_time_ms, and the per-request
+    finish times as a third value."""
     lens = [len(p) for p in prompts]
     flat = [t for p in prompts for t in p]
     out = (ctypes.c_int * max(1, sum(decode_lens)))()
@@ -582,11 +614,10 @@ def schedule_dry_run(cache: PagedKVCache, prompts, decode_lens, vocab, max_slots
     rt, rp, rs = (ctypes.c_int * max_rows)(), (ctypes.c_int * max_rows)(), (ctypes.c_int * max_rows)()
     fin = (ctypes.c_double * max(1, len(prompts)))()
     arr = _darr(arrival_ms) if arrival_ms is not None else None
-    n = _rt_check(runtime().cbis_schedule_dry_run_timed(cache._h, len(prompts), _iarr(lens), _iarr(flat),
-                                                        _iarr(decode_lens), arr, step_time_ms, max_slots,
-                                                        prefill_chunk, step_token_budget, vocab, out, rows,
-                                                        max_steps, rt, rp, rs, max_rows, fin),
-                  "schedule_dry_run")
+    fn = runtime().cbis_schedule_dry_run_pipelined if pipeline else runtime().cbis_schedule_dry_run_timed
+    n = _rt_check(fn(cache._h, len(prompts), _iarr(lens), _iarr(flat), _iarr(decode_lens), arr, step_time_ms,
+                     max_slots, prefill_chunk, step_token_budget, vocab, out, rows, max_steps, rt, rp, rs, max_rows,
+                     fin), "schedule_dry_run")
     if n > max_steps or sum(rows[:n]) > max_rows:
         raise RuntimeError("schedule_dry_run: trace larger than the buffers")
     toks, o = [], 0

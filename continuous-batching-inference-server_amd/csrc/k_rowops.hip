@@ -40,15 +40,24 @@ namespace {
 // ---------------------------------------------------------------------------
 // Embedding: one wave per row, 16-byte accesses.
 // ---------------------------------------------------------------------------
+// With src set, row r whose tok_src[r] >= 0 takes token src[tok_src[r]]
+// (a previous step's greedy result).  The grid also copies n16 16-byte
+// words from stage_src to stage_dst on the way (a step's metadata, from
+// device-visible host memory to the device, for the kernels after this one).
 template <typename ET>
 __global__ __launch_bounds__(256) void embed_kernel(int T, int D, const int* __restrict__ tok,
+                                                    const int* __restrict__ tok_src, const int* __restrict__ src,
                                                     const int* __restrict__ pos, const ET* __restrict__ te,
                                                     const ET* __restrict__ pe, int vocab, int max_pos,
-                                                    float* __restrict__ out) {
+                                                    float* __restrict__ out, const int4* __restrict__ stage_src,
+                                                    int4* __restrict__ stage_dst, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+    stage_dst[i] = stage_src[i];
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T) return;
   const int lane = threadIdx.x & 63;
-  const int t = tok[row], p = pos[row];
+  const int from = src ? tok_src[row] : -1;
+  const int t = from >= 0 ? src[from] : tok[row], p = pos[row];
   float* o = out + (int64_t)row * D;
   // An id outside its table is not read: its row comes out NaN, so a bad
   // input shows in every value computed from it instead of being hidden.
@@ -302,12 +311,18 @@ extern "C" {
 
 const char* cbis_last_error(void) { return g_last_error.c_str(); }
 
-int cbis_embed(int T, int D, const int* tok, const int* pos, int emb_dtype, const void* te, const void* pe, int vocab,
-               int max_pos, float* out, cbis_stream_t stream) {
+int cbis_embed_from(int T, int D, const int* tok, const int* tok_src, const int* src_tokens, const int* pos,
+                    int emb_dtype, const void* te, const void* pe, int vocab, int max_pos, float* out,
+                    const void* stage_src, void* stage_dst, size_t stage_bytes, cbis_stream_t stream) {
   CBIS_REQUIRE(T >= 0 && D > 0 && D % 4 == 0, CBIS_ERR_INVALID, "cbis_embed: bad T=%d d_model=%d", T, D);
   CBIS_REQUIRE(vocab > 0 && max_pos > 0, CBIS_ERR_INVALID, "cbis_embed: vocab/max_pos must be > 0");
+  CBIS_REQUIRE(stage_bytes == 0 || (T > 0 && aligned16(stage_src) && aligned16(stage_dst) && stage_bytes % 16 == 0),
+               CBIS_ERR_INVALID, "cbis_embed_from: staging needs rows, 16-byte aligned buffers and a 16-byte "
+               "multiple of bytes");
   if (T == 0) return CBIS_OK;
   CBIS_REQUIRE(tok && pos && te && pe && out, CBIS_ERR_INVALID, "cbis_embed: null pointer");
+  CBIS_REQUIRE((tok_src == nullptr) == (src_tokens == nullptr), CBIS_ERR_INVALID,
+               "cbis_embed_from: token_src and src_tokens go together");
   // Each lane moves 4 columns: 16-byte fp32 (8-byte bf16) table loads and
   // 16-byte stores.
   const uintptr_t tal = emb_dtype == CBIS_BF16 ? 7u : 15u;
@@ -315,14 +330,23 @@ int cbis_embed(int T, int D, const int* tok, const int* pos, int emb_dtype, cons
                "cbis_embed: tables and out must be %d-byte / 16-byte aligned", (int)tal + 1);
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)cdiv(T, 4));
+  const int64_t n16 = (int64_t)(stage_bytes / 16);
   if (emb_dtype == CBIS_F32)
-    embed_kernel<float><<<grid, 256, 0, s>>>(T, D, tok, pos, (const float*)te, (const float*)pe, vocab, max_pos, out);
+    embed_kernel<float><<<grid, 256, 0, s>>>(T, D, tok, tok_src, src_tokens, pos, (const float*)te, (const float*)pe,
+                                             vocab, max_pos, out, (const int4*)stage_src, (int4*)stage_dst, n16);
   else if (emb_dtype == CBIS_BF16)
-    embed_kernel<uint16_t><<<grid, 256, 0, s>>>(T, D, tok, pos, (const uint16_t*)te, (const uint16_t*)pe, vocab,
-                                                max_pos, out);
+    embed_kernel<uint16_t><<<grid, 256, 0, s>>>(T, D, tok, tok_src, src_tokens, pos, (const uint16_t*)te,
+                                                (const uint16_t*)pe, vocab, max_pos, out, (const int4*)stage_src,
+                                                (int4*)stage_dst, n16);
   else
     return fail(CBIS_ERR_UNSUPPORTED, "cbis_embed: embedding dtype %d", emb_dtype);
   return check_launch("cbis_embed");
+}
+
+int cbis_embed(int T, int D, const int* tok, const int* pos, int emb_dtype, const void* te, const void* pe, int vocab,
+               int max_pos, float* out, cbis_stream_t stream) {
+  return cbis_embed_from(T, D, tok, nullptr, nullptr, pos, emb_dtype, te, pe, vocab, max_pos, out, nullptr, nullptr,
+                         0, stream);
 }
 
 int cbis_layernorm(int T, int D, const float* X, int64_t ldx, const float* g, const float* b, float eps, int y_dtype,

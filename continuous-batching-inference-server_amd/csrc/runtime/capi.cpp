@@ -2,6 +2,7 @@
 // exceptions stop here: they become negative return codes (or NULL) with the
 // message in cbis_runtime_last_error().
 #include <cstring>
+#include <map>
 
 #include "cbis_runtime.h"
 #include "runtime.hpp"
@@ -234,6 +235,27 @@ int cbis_runner_forward_step_greedy(cbis_runner* r, int n, const int* token_ids,
   });
 }
 
+int cbis_runner_enqueue_greedy(cbis_runner* r, int n, const int* token_ids, const int* positions, const int* seq_ids,
+                               const int* token_src, int64_t* ticket) {
+  return guard([&] {
+    if (n <= 0) throw std::invalid_argument("enqueue_greedy: n must be > 0");
+    if (!ticket) throw std::invalid_argument("enqueue_greedy: null ticket");
+    std::vector<int> t(token_ids, token_ids + n), p(positions, positions + n), s(seq_ids, seq_ids + n);
+    std::vector<int> src;
+    if (token_src) src.assign(token_src, token_src + n);
+    *ticket = r->impl->enqueue_greedy(t, p, s, src);
+    return 0;
+  });
+}
+
+int cbis_runner_wait_greedy(cbis_runner* r, int64_t ticket, int* next_tokens, int capacity) {
+  return guard([&] {
+    const std::vector<int> nx = r->impl->wait_greedy(ticket);
+    for (int i = 0; i < capacity && i < (int)nx.size(); ++i) next_tokens[i] = nx[i];
+    return (int)nx.size();
+  });
+}
+
 const float* cbis_runner_logits_device(cbis_runner* r) { return r->impl->logits_device(); }
 
 float cbis_runner_last_device_ms(const cbis_runner* r) { return r->impl->last_device_ms(); }
@@ -338,11 +360,17 @@ int cbis_schedule_dry_run(cbis_cache* c, int n_requests, const int* prompt_lens,
                                      row_pos, row_sid, max_rows, nullptr);
 }
 
-int cbis_schedule_dry_run_timed(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens,
-                                const int* decode_lens, const double* arrival_ms, double step_time_ms, int max_slots,
-                                int prefill_chunk, int step_token_budget, int vocab, int* out_tokens, int* step_rows,
-                                int max_steps, int* row_tok, int* row_pos, int* row_sid, int max_rows,
-                                double* finish_ms) {
+namespace {
+// The dry run's stand-in for a forward step: row (tok, pos, seq) -> (31 tok +
+// 7 pos + 13 seq + 1) mod vocab.
+int stand_in(int t, int p, int s, int vocab) {
+  return (int)(((uint32_t)t * 31u + (uint32_t)p * 7u + (uint32_t)s * 13u + 1u) % (uint32_t)vocab);
+}
+
+int dry_run(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens, const int* decode_lens,
+            const double* arrival_ms, double step_time_ms, int max_slots, int prefill_chunk, int step_token_budget,
+            int vocab, int* out_tokens, int* step_rows, int max_steps, int* row_tok, int* row_pos, int* row_sid,
+            int max_rows, double* finish_ms, bool pipelined) {
   return guard([&] {
     if (vocab <= 0) throw std::invalid_argument("schedule_dry_run: vocab must be > 0");
     if (!(step_time_ms >= 0.0)) throw std::invalid_argument("schedule_dry_run: step_time_ms must be >= 0");
@@ -352,16 +380,42 @@ int cbis_schedule_dry_run_timed(cbis_cache* c, int n_requests, const int* prompt
     double clock = 0.0;
     const StepFn step = [&](const std::vector<int>& t, const std::vector<int>& p, const std::vector<int>& s) {
       std::vector<int> next(t.size());
-      for (size_t i = 0; i < t.size(); ++i)
-        next[i] = (int)(((uint32_t)t[i] * 31u + (uint32_t)p[i] * 7u + (uint32_t)s[i] * 13u + 1u) % (uint32_t)vocab);
+      for (size_t i = 0; i < t.size(); ++i) next[i] = stand_in(t[i], p[i], s[i], vocab);
       clock += step_time_ms;
       return next;
     };
+    // Pipelined: the stand-in "device" keeps each step's outputs, resolves a
+    // row's token source against the step queued before it and runs the step
+    // (on the virtual clock) when it is queued.  The trace reports the
+    // resolved tokens, so both modes' traces read alike.
+    std::map<int64_t, std::vector<int>> outputs;
+    std::vector<std::vector<int>> resolved;
+    int64_t queued = 0;
+    PipelinedStep pstep;
+    pstep.enqueue = [&](const std::vector<int>& t, const std::vector<int>& p, const std::vector<int>& s,
+                        const std::vector<int>& src) {
+      std::vector<int> tok = t;
+      for (size_t i = 0; i < src.size(); ++i) {
+        if (src[i] < 0) continue;
+        const auto prev = outputs.find(queued - 1);
+        if (prev == outputs.end() || src[i] >= (int)prev->second.size())
+          throw std::logic_error("schedule_dry_run: token source past the previous step");
+        tok[i] = prev->second[src[i]];
+      }
+      outputs[queued] = step(tok, p, s);
+      resolved.push_back(tok);
+      outputs.erase(queued - 2);  // a source is always the step just before
+      return queued++;
+    };
+    pstep.wait = [&](int64_t ticket) { return outputs.at(ticket); };
     std::vector<StepRows> trace;
     ScheduleOptions opt = options(max_slots, prefill_chunk, step_token_budget);
     opt.clock_ms = [&]() { return clock; };
     opt.wait_ms = [&](double ms) { clock += ms; };
-    const ContinuousResult res = run_continuous(step, *c->impl, reqs, opt, &trace);
+    const ContinuousResult res = pipelined ? run_continuous_pipelined(pstep, *c->impl, reqs, opt, &trace)
+                                           : run_continuous(step, *c->impl, reqs, opt, &trace);
+    if (pipelined)
+      for (size_t k = 0; k < trace.size(); ++k) trace[k].tok = resolved.at(k);
     copy_tokens(res, n_requests, decode_lens, out_tokens);
     if (finish_ms)
       for (int i = 0; i < n_requests; ++i) finish_ms[i] = res.finish_ms[i];
@@ -378,6 +432,45 @@ int cbis_schedule_dry_run_timed(cbis_cache* c, int n_requests, const int* prompt
       }
     }
     return (int)trace.size();
+  });
+}
+}  // namespace
+
+int cbis_schedule_dry_run_timed(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens,
+                                const int* decode_lens, const double* arrival_ms, double step_time_ms, int max_slots,
+                                int prefill_chunk, int step_token_budget, int vocab, int* out_tokens, int* step_rows,
+                                int max_steps, int* row_tok, int* row_pos, int* row_sid, int max_rows,
+                                double* finish_ms) {
+  return dry_run(c, n_requests, prompt_lens, prompt_tokens, decode_lens, arrival_ms, step_time_ms, max_slots,
+                 prefill_chunk, step_token_budget, vocab, out_tokens, step_rows, max_steps, row_tok, row_pos, row_sid,
+                 max_rows, finish_ms, false);
+}
+
+int cbis_schedule_dry_run_pipelined(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens,
+                                    const int* decode_lens, const double* arrival_ms, double step_time_ms,
+                                    int max_slots, int prefill_chunk, int step_token_budget, int vocab,
+                                    int* out_tokens, int* step_rows, int max_steps, int* row_tok, int* row_pos,
+                                    int* row_sid, int max_rows, double* finish_ms) {
+  return dry_run(c, n_requests, prompt_lens, prompt_tokens, decode_lens, arrival_ms, step_time_ms, max_slots,
+                 prefill_chunk, step_token_budget, vocab, out_tokens, step_rows, max_steps, row_tok, row_pos, row_sid,
+                 max_rows, finish_ms, true);
+}
+
+int cbis_run_continuous_pipelined(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
+                                  const int* prompt_tokens, const int* decode_lens, const double* arrival_ms,
+                                  int max_slots, int prefill_chunk, int step_token_budget, int* out_tokens,
+                                  double* step_ms, int max_steps, double* finish_ms) {
+  return guard([&] {
+    std::vector<Request> reqs = make_requests(n_requests, prompt_lens, prompt_tokens, decode_lens);
+    set_arrivals(reqs, arrival_ms);
+    const ContinuousResult res =
+        run_continuous_pipelined(*r->impl, *c->impl, reqs, options(max_slots, prefill_chunk, step_token_budget));
+    copy_tokens(res, n_requests, decode_lens, out_tokens);
+    if (step_ms)
+      for (int i = 0; i < (int)res.step_ms.size() && i < max_steps; ++i) step_ms[i] = res.step_ms[i];
+    if (finish_ms)
+      for (int i = 0; i < n_requests; ++i) finish_ms[i] = res.finish_ms[i];
+    return (int)res.step_ms.size();
   });
 }
 

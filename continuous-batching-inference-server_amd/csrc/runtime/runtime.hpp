@@ -166,14 +166,29 @@ class TransformerRunner {
   // each row's top-2 margin (max logit minus the runner-up).
   std::vector<int> forward_step_greedy(const std::vector<int>& token_ids, const std::vector<int>& positions,
                                        const std::vector<int>& seq_ids);
+  // Pipelined greedy steps (no reference counterpart).  enqueue_greedy
+  // queues the step of forward_step_greedy and returns at once with a ticket;
+  // wait_greedy(ticket) waits for that step and returns its tokens (and sets
+  // last_margins / last_device_ms / last_host_ms).  token_src (empty, or one
+  // entry per row) lets a row take its input token from the device: row i
+  // with token_src[i] >= 0 uses the greedy token of row token_src[i] of the
+  // greedy step enqueued just before this one (token_ids[i] is then
+  // ignored), so a decode loop can queue step t + 1 before step t's tokens
+  // reach the host.  At most two steps are outstanding: a step's buffers are
+  // reused two steps later, and enqueue_greedy throws std::logic_error if
+  // that step has not been waited for.
+  int64_t enqueue_greedy(const std::vector<int>& token_ids, const std::vector<int>& positions,
+                         const std::vector<int>& seq_ids, const std::vector<int>& token_src);
+  std::vector<int> wait_greedy(int64_t ticket);
   // Empty after a plain forward_step: margins belong to greedy steps only.
   const std::vector<float>& last_margins() const { return margins_; }
-  // Device time of the last step's forward (embedding through lm_head and
-  // the argmax, between two events on the runner's stream; the metadata H2D
-  // before it and the result D2H after it are not included), in ms.
+  // Device time of the last step's forward (embedding, which also stages
+  // the step's metadata, through lm_head and the argmax, between two events
+  // on the runner's stream), in ms.
   float last_device_ms() const { return last_device_ms_; }
-  // Host wall time of the last step's phases, in ms: {host preparation and
-  // the metadata H2D enqueue, the forward's launch, the wait for its results}.
+  // Host wall time of the last greedy step's phases, in ms: {host
+  // preparation of the metadata, the forward's launch, the wait for its
+  // results}.
   const double* last_host_ms() const { return host_ms_; }
   // Device logits of the last forward_step (not of a greedy step).
   const float* logits_device() const { return d_logits_; }
@@ -185,25 +200,42 @@ class TransformerRunner {
   std::vector<int> last_plan() const { return signature(); }
 
  private:
-  void prepare(const int* tok, const int* pos, const int* seq, int M);
-  void enqueue_forward(bool greedy);
-  void run_step(bool greedy);
-  void timed_step(bool greedy);
+  // One step's own buffers; consecutive steps alternate between two of them,
+  // so a step can be prepared and queued while the one before it runs.
+  // A step's host<->device traffic goes through pinned, coherent host memory
+  // that the kernels read and write themselves: no copy commands between
+  // two steps' kernels on the stream.
+  struct StepBuf {
+    uint8_t* h_meta = nullptr;   // the step's metadata, written by the host
+    uint8_t* hd_meta = nullptr;  // h_meta's device address
+    uint8_t* d_meta = nullptr;   // its device copy (staged by the embed launch)
+    size_t cap = 0;
+    int* h_next = nullptr;  // [M] tokens then [M] margins (fp32) of a greedy step, written by the argmax launch
+    int* d_next = nullptr;  // h_next's device address (the next step's embed reads tokens there)
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;  // around the forward
+    int64_t ticket = -1;    // the greedy step these buffers hold, -1 if none
+    bool pending = false;   // enqueued, not yet waited for
+    int M = 0;
+    double host_ms[2] = {0, 0};
+  };
+  void prepare(int b, const int* tok, const int* pos, const int* seq, const int* src, int M);
+  void enqueue_forward(int b, bool greedy, bool from_prev);
+  void run_step(int b, bool greedy, bool from_prev);
+  void timed_step(int b, bool greedy, bool from_prev);
 
   const ModelWeights& w_;
   PagedKVCache& cache_;
   ModelConfig cfg_;
   int max_rows_;
   hipStream_t stream_ = nullptr;
-  hipEvent_t ev_start_ = nullptr, ev_stop_ = nullptr;
   float last_device_ms_ = 0.f;
   double host_ms_[3] = {0, 0, 0};
   bool use_graphs_ = true;
 
-  // metadata staging (pinned host, one H2D per step)
-  uint8_t* h_meta_ = nullptr;
-  uint8_t* d_meta_ = nullptr;
-  size_t meta_cap_ = 0;
+  StepBuf bufs_[2];
+  int next_buf_ = 0;          // the buffers the next step takes
+  int64_t tickets_ = 0;       // greedy steps enqueued so far
+  int prev_greedy_rows_ = -1; // rows of the step just before, if it was greedy (its tokens can be sources)
 
   // activations
   float* d_x_ = nullptr;
@@ -212,8 +244,6 @@ class TransformerRunner {
   void* d_attn_ = nullptr;
   void* d_h_ = nullptr;
   float* d_logits_ = nullptr;
-  int* d_next_ = nullptr;  // [M] tokens then [M] margins (fp32) of a greedy step
-  int* h_next_ = nullptr;  // pinned host copy of d_next_
   void* d_amax_ws_ = nullptr;  // cbis_gemm_argmax partials
   size_t amax_ws_bytes_ = 0;
   std::vector<float> margins_;
@@ -226,8 +256,13 @@ class TransformerRunner {
   int M_ = 0;
   int n_decode_ = 0, n_tiles_ = 0, n_seqs_ = 0, bt_width_ = 0, max_kv_ = 0, split_tokens_ = 0;
   size_t meta_bytes_ = 0;
-  int *d_tok_ = nullptr, *d_pos_ = nullptr, *d_wpage_ = nullptr, *d_woff_ = nullptr, *d_rowbt_ = nullptr,
-      *d_drows_ = nullptr, *d_tiles_ = nullptr, *d_bt_ = nullptr;
+  const uint8_t* stage_src_ = nullptr;  // the step's metadata in host memory (device address) ...
+  uint8_t* stage_dst_ = nullptr;        // ... and its device copy, which the step's embed launch fills
+  // Read by the embed launch straight from host memory:
+  const int *hd_tok_ = nullptr, *hd_pos_ = nullptr, *hd_src_ = nullptr;
+  // Read from the device copy by every later launch:
+  int *d_pos_ = nullptr, *d_wpage_ = nullptr, *d_woff_ = nullptr, *d_rowbt_ = nullptr, *d_drows_ = nullptr,
+      *d_tiles_ = nullptr, *d_bt_ = nullptr;
 
   // graph cache: one executable graph per step shape signature
   struct GraphEntry {
@@ -399,5 +434,32 @@ ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, 
                                 const ScheduleOptions& opt);
 ContinuousResult run_continuous(TransformerRunner& runner, PagedKVCache& cache, const std::vector<Request>& reqs,
                                 int max_slots);
+
+// A forward step queued without waiting for it (no reference counterpart):
+// enqueue(tok, pos, sid, src) returns a ticket; a row with src[i] >= 0 takes
+// as its input token the greedy token of row src[i] of the step enqueued
+// just before (tok[i] is not used); wait(ticket) returns the greedy next
+// token of every row of that step.
+struct PipelinedStep {
+  std::function<int64_t(const std::vector<int>&, const std::vector<int>&, const std::vector<int>&,
+                        const std::vector<int>&)>
+      enqueue;
+  std::function<std::vector<int>(int64_t)> wait;
+};
+
+// run_continuous with one step in flight: step t + 1 is built and queued
+// before step t's tokens come back (its decode rows name the rows of step t
+// that produce their tokens), then step t's tokens are collected.  The rows,
+// tokens and page order are run_continuous's for the same admissions; a
+// request whose arrival falls while step t runs is seen when step t + 2 is
+// built, one step later than there.  step_ms: per step, host wall time from
+// the later of its enqueue and the previous collection to its collection;
+// finish_ms: when the host collected the request's last token.  In the
+// trace, rows that take their token from the previous step hold tok -1.
+ContinuousResult run_continuous_pipelined(const PipelinedStep& step, PagedKVCache& cache,
+                                          const std::vector<Request>& reqs, const ScheduleOptions& opt,
+                                          std::vector<StepRows>* trace = nullptr);
+ContinuousResult run_continuous_pipelined(TransformerRunner& runner, PagedKVCache& cache,
+                                          const std::vector<Request>& reqs, const ScheduleOptions& opt);
 
 }  // namespace cbis

@@ -4,8 +4,10 @@
 // Differences from the reference's step that keep its contract:
 //  * per-step metadata (token ids, positions, write slots, a compact block
 //    table per distinct sequence instead of a kPagesPerSeq-wide copy per row,
-//    decode-row list, prefill tiles) is packed into one pinned buffer and
-//    sent with a single H2D copy;
+//    decode-row list, prefill tiles) is packed into one block of pinned,
+//    device-visible host memory that the step's embed launch copies to the
+//    device on its way (no copy command on the stream); a greedy step's
+//    argmax stores its tokens straight into pinned host memory;
 //  * per layer: LayerNorm -> one fused QKV GEMM whose epilogue adds the bias
 //    and scatters K/V into their page slots (scatter-before-attention order
 //    of src/transformer.cpp:75-80 kept) -> split-KV decode attention for
@@ -42,22 +44,24 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   // The attention kernels are built for head_dim 32 (any head count).
   if (cfg_.head_dim != 32) throw std::invalid_argument("TransformerRunner: attention needs head_dim 32");
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
-  hip_check(hipEventCreate(&ev_start_), "hipEventCreate");
-  hip_check(hipEventCreate(&ev_stop_), "hipEventCreate");
   const size_t R = max_total_rows, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
   const size_t ae = dtype_size(cfg_.act_dtype());
+  for (StepBuf& b : bufs_) {
+    hip_check(hipEventCreate(&b.ev_start), "hipEventCreate");
+    hip_check(hipEventCreate(&b.ev_stop), "hipEventCreate");
+    // Greedy results: a step's M tokens, then its M margins right after
+    // them, stored by the argmax launch straight into host memory (a copy
+    // command after the step would cost more than the step's last kernel).
+    hip_check(hipHostMalloc((void**)&b.h_next, R * 8, hipHostMallocMapped | hipHostMallocCoherent),
+              "hipHostMalloc next");
+    hip_check(hipHostGetDevicePointer((void**)&b.d_next, b.h_next, 0), "hipHostGetDevicePointer next");
+  }
   hip_check(hipMalloc((void**)&d_x_, R * D * 4), "hipMalloc x");
   hip_check(hipMalloc(&d_xn_, R * D * ae), "hipMalloc xn");
   hip_check(hipMalloc((void**)&d_q_, R * D * 4), "hipMalloc q");
   hip_check(hipMalloc(&d_attn_, R * D * ae), "hipMalloc attn");
   hip_check(hipMalloc(&d_h_, R * F * ae), "hipMalloc h");
   hip_check(hipMalloc((void**)&d_logits_, R * V * 4), "hipMalloc logits");
-  // Greedy results: a step's M tokens, then its M margins right after them
-  // (one D2H copy brings both back).
-  hip_check(hipMalloc((void**)&d_next_, R * 8), "hipMalloc next");
-  // Pinned, so the per-step D2H of the results is a plain DMA (a pageable
-  // destination makes the runtime stage or lock host pages on every copy).
-  hip_check(hipHostMalloc((void**)&h_next_, R * 8, 0), "hipHostMalloc next");
   // Split-KV partials: the automatic split keeps rows * splits <= 2048 + rows.
   ws_bytes_ = (2048 + R) * (size_t)cfg_.n_heads * (cfg_.head_dim + 4) * 4;
   hip_check(hipMalloc(&d_ws_, ws_bytes_), "hipMalloc attention workspace");
@@ -86,24 +90,32 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
 }
 
 TransformerRunner::~TransformerRunner() {
+  if (stream_) (void)hipStreamSynchronize(stream_);  // queued steps still use the buffers
   for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
   if (stream_) (void)hipStreamDestroy(stream_);
-  if (ev_start_) (void)hipEventDestroy(ev_start_);
-  if (ev_stop_) (void)hipEventDestroy(ev_stop_);
+  for (StepBuf& b : bufs_) {
+    if (b.ev_start) (void)hipEventDestroy(b.ev_start);
+    if (b.ev_stop) (void)hipEventDestroy(b.ev_stop);
+    if (b.h_next) (void)hipHostFree(b.h_next);
+    if (b.d_meta) (void)hipFree(b.d_meta);
+    if (b.h_meta) (void)hipHostFree(b.h_meta);
+  }
   (void)hipFree(d_x_); (void)hipFree(d_xn_); (void)hipFree(d_q_); (void)hipFree(d_attn_);
-  (void)hipFree(d_h_); (void)hipFree(d_logits_); (void)hipFree(d_next_);
+  (void)hipFree(d_h_); (void)hipFree(d_logits_);
   (void)hipFree(d_ws_);
   if (d_amax_ws_) (void)hipFree(d_amax_ws_);
   if (d_gemm_ws_) (void)hipFree(d_gemm_ws_);
-  (void)hipFree(d_meta_);
-  if (h_meta_) (void)hipHostFree(h_meta_);
-  if (h_next_) (void)hipHostFree(h_next_);
 }
 
-void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, int M) {
+void TransformerRunner::prepare(int b, const int* tok, const int* pos, const int* seq, const int* src, int M) {
   if (M > max_rows_) throw std::runtime_error("forward_step: total_rows exceeds max_total_rows");
   for (int i = 0; i < M; ++i) {
-    if (tok[i] < 0 || tok[i] >= cfg_.vocab) throw std::out_of_range("forward_step: token id out of range");
+    if (src && src[i] >= 0) {
+      if (src[i] >= prev_greedy_rows_)
+        throw std::out_of_range("enqueue_greedy: token_src beyond the previous greedy step's rows");
+    } else if (tok[i] < 0 || tok[i] >= cfg_.vocab) {
+      throw std::out_of_range("forward_step: token id out of range");
+    }
     if (pos[i] < 0 || pos[i] >= cfg_.max_seq) throw std::out_of_range("forward_step: position out of range");
   }
   std::vector<int> wpage(M), woff(M), rowbt(M);
@@ -212,18 +224,26 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
 
   const size_t o_tok = 0, o_pos = o_tok + align_ints(M), o_wp = o_pos + align_ints(M), o_wo = o_wp + align_ints(M),
                o_rb = o_wo + align_ints(M), o_dr = o_rb + align_ints(M), o_ti = o_dr + align_ints(drows.size()),
-               o_bt = o_ti + align_ints(tiles.size()), n_ints = o_bt + align_ints((size_t)n_seqs_ * width);
+               o_bt = o_ti + align_ints(tiles.size()), o_src = o_bt + align_ints((size_t)n_seqs_ * width),
+               n_ints = o_src + (src ? align_ints(M) : 0);
   const size_t bytes = n_ints * 4;
-  if (bytes > meta_cap_) {
+  StepBuf& sb = bufs_[b];
+  if (bytes > sb.cap) {
+    // The captured graphs name the old buffers; a step still queued on the
+    // other buffers may be running one of them.
+    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
     for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
     graphs_.clear();
-    if (d_meta_) hip_check(hipFree(d_meta_), "hipFree meta");
-    if (h_meta_) hip_check(hipHostFree(h_meta_), "hipHostFree meta");
-    meta_cap_ = std::max(bytes, (size_t)1 << 20) * 2;
-    hip_check(hipMalloc((void**)&d_meta_, meta_cap_), "hipMalloc meta");
-    hip_check(hipHostMalloc((void**)&h_meta_, meta_cap_, 0), "hipHostMalloc meta");
+    if (sb.d_meta) hip_check(hipFree(sb.d_meta), "hipFree meta");
+    if (sb.h_meta) hip_check(hipHostFree(sb.h_meta), "hipHostFree meta");
+    sb.d_meta = sb.h_meta = sb.hd_meta = nullptr;
+    sb.cap = std::max(bytes, (size_t)1 << 20) * 2;
+    hip_check(hipMalloc((void**)&sb.d_meta, sb.cap), "hipMalloc meta");
+    hip_check(hipHostMalloc((void**)&sb.h_meta, sb.cap, hipHostMallocMapped | hipHostMallocCoherent),
+              "hipHostMalloc meta");
+    hip_check(hipHostGetDevicePointer((void**)&sb.hd_meta, sb.h_meta, 0), "hipHostGetDevicePointer meta");
   }
-  int* h = (int*)h_meta_;
+  int* h = (int*)sb.h_meta;
   std::memcpy(h + o_tok, tok, M * 4);
   std::memcpy(h + o_pos, pos, M * 4);
   std::memcpy(h + o_wp, wpage.data(), M * 4);
@@ -238,23 +258,37 @@ void TransformerRunner::prepare(const int* tok, const int* pos, const int* seq, 
     std::copy(pg.begin(), pg.end(), row);
     std::fill(row + pg.size(), row + width, 0);
   }
-  int* d = (int*)d_meta_;
-  d_tok_ = d + o_tok; d_pos_ = d + o_pos; d_wpage_ = d + o_wp; d_woff_ = d + o_wo; d_rowbt_ = d + o_rb;
+  if (src) std::memcpy(h + o_src, src, M * 4);
+  // No copy command: the step's embed launch reads its own inputs from the
+  // host block and stages the whole block into d_meta for the launches after
+  // it.  The other buffers' block may still be in use by the step queued
+  // before; this one's last reader was the step two back, already waited for.
+  const int* hd = (const int*)sb.hd_meta;
+  hd_tok_ = hd + o_tok; hd_pos_ = hd + o_pos; hd_src_ = src ? hd + o_src : nullptr;
+  int* d = (int*)sb.d_meta;
+  d_pos_ = d + o_pos; d_wpage_ = d + o_wp; d_woff_ = d + o_wo; d_rowbt_ = d + o_rb;
   d_drows_ = d + o_dr; d_tiles_ = d + o_ti; d_bt_ = d + o_bt;
+  stage_src_ = sb.hd_meta;
+  stage_dst_ = sb.d_meta;
   meta_bytes_ = bytes;
-  hip_check(hipMemcpyAsync(d_meta_, h_meta_, bytes, hipMemcpyHostToDevice, stream_), "H2D step metadata");
+  sb.M = M;
 }
 
 std::vector<int> TransformerRunner::signature() const {
   return {M_, n_decode_, n_tiles_, n_seqs_, bt_width_, max_kv_, split_tokens_};
 }
 
-void TransformerRunner::enqueue_forward(bool greedy) {
+void TransformerRunner::enqueue_forward(int b, bool greedy, bool from_prev) {
   const int M = M_, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
   const int act = cfg_.act_dtype(), wd = cfg_.weight_dtype;
   hipStream_t s = stream_;
-  cbis_check(cbis_embed(M, D, d_tok_, d_pos_, w_.emb_dtype(), w_.tok_emb, w_.pos_emb, V, cfg_.max_seq, d_x_, s),
-             "embed");
+  int* const d_next = bufs_[b].d_next;
+  // Rows with a token source read the previous step's greedy tokens (the
+  // other buffers' results, which that step wrote earlier on this stream).
+  cbis_check(cbis_embed_from(M, D, hd_tok_, from_prev ? hd_src_ : nullptr, from_prev ? bufs_[b ^ 1].d_next : nullptr,
+                             hd_pos_, w_.emb_dtype(), w_.tok_emb, w_.pos_emb, V, cfg_.max_seq, d_x_, stage_src_,
+                             stage_dst_, meta_bytes_, s),
+             "embed + metadata staging");
 
   cbis_gemm_desc g = {};
   g.M = M;
@@ -355,30 +389,33 @@ void TransformerRunner::enqueue_forward(bool greedy) {
   g.x_dtype = act; g.X = d_xn_; g.ldx = D;
   g.w_dtype = wd; g.W = w_.lm_head; g.ldw = D; g.w_scale = w_.lm_scale;
   g.y_dtype = CBIS_F32; g.Y = d_logits_; g.ldy = V;
-  float* margins = (float*)(d_next_ + M);
+  float* margins = (float*)(d_next + M);
   if (ln_pro && greedy)
-    cbis_check(cbis_layernorm_gemm_argmax(&g, d_x_, D, w_.ln_f_w, w_.ln_f_b, 1e-5f, d_next_, margins, d_amax_ws_,
+    cbis_check(cbis_layernorm_gemm_argmax(&g, d_x_, D, w_.ln_f_w, w_.ln_f_b, 1e-5f, d_next, margins, d_amax_ws_,
                                           amax_ws_bytes_, s),
                "ln_f + lm_head gemm + argmax");
   else if (ln_pro)
     cbis_check(cbis_layernorm_gemm(&g, d_x_, D, w_.ln_f_w, w_.ln_f_b, 1e-5f, s), "ln_f + lm_head gemm");
   else if (greedy)
-    cbis_check(cbis_gemm_argmax(&g, d_next_, margins, d_amax_ws_, amax_ws_bytes_, s), "lm_head gemm + argmax");
+    cbis_check(cbis_gemm_argmax(&g, d_next, margins, d_amax_ws_, amax_ws_bytes_, s), "lm_head gemm + argmax");
   else
     cbis_check(cbis_gemm(&g, s), "lm_head gemm");
 }
 
-void TransformerRunner::run_step(bool greedy) {
-  auto body = [&]() { enqueue_forward(greedy); };
+void TransformerRunner::run_step(int b, bool greedy, bool from_prev) {
+  auto body = [&]() { enqueue_forward(b, greedy, from_prev); };
   if (!use_graphs_) {
     body();
     return;
   }
+  // A graph names one set of step buffers (and, reading the previous step's
+  // tokens, the other set's results).
   std::vector<int> sig = signature();
-  sig.push_back(greedy ? 1 : 0);
+  sig.insert(sig.end(), {greedy ? 1 : 0, b, from_prev ? 1 : 0});
   auto it = graphs_.find(sig);
   if (it == graphs_.end()) {
     if (graphs_.size() >= kMaxGraphs) {
+      hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");  // a queued step may run one of them
       for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second.exec);
       graphs_.clear();
     }
@@ -401,10 +438,10 @@ void TransformerRunner::run_step(bool greedy) {
   hip_check(hipGraphLaunch(it->second.exec, stream_), "hipGraphLaunch");
 }
 
-void TransformerRunner::timed_step(bool greedy) {
-  hip_check(hipEventRecord(ev_start_, stream_), "hipEventRecord");
-  run_step(greedy);
-  hip_check(hipEventRecord(ev_stop_, stream_), "hipEventRecord");
+void TransformerRunner::timed_step(int b, bool greedy, bool from_prev) {
+  hip_check(hipEventRecord(bufs_[b].ev_start, stream_), "hipEventRecord");
+  run_step(b, greedy, from_prev);
+  hip_check(hipEventRecord(bufs_[b].ev_stop, stream_), "hipEventRecord");
 }
 
 std::vector<float> TransformerRunner::forward_step(const std::vector<int>& token_ids, const std::vector<int>& positions,
@@ -414,40 +451,77 @@ std::vector<float> TransformerRunner::forward_step(const std::vector<int>& token
   if (M == 0) return {};
   if ((int)positions.size() != M || (int)seq_ids.size() != M)
     throw std::invalid_argument("forward_step: token_ids/positions/seq_ids sizes differ");
-  prepare(token_ids.data(), positions.data(), seq_ids.data(), M);
-  timed_step(false);
+  const int b = next_buf_;
+  if (bufs_[b].pending) throw std::logic_error("forward_step: a queued greedy step has not been waited for");
+  prepare(b, token_ids.data(), positions.data(), seq_ids.data(), nullptr, M);
+  timed_step(b, false, false);
   std::vector<float> logits((size_t)M * cfg_.vocab);
   hip_check(hipMemcpyAsync(logits.data(), d_logits_, logits.size() * 4, hipMemcpyDeviceToHost, stream_), "D2H logits");
   hip_check(hipStreamSynchronize(stream_), "forward_step sync");
-  hip_check(hipEventElapsedTime(&last_device_ms_, ev_start_, ev_stop_), "hipEventElapsedTime");
+  hip_check(hipEventElapsedTime(&last_device_ms_, bufs_[b].ev_start, bufs_[b].ev_stop), "hipEventElapsedTime");
+  bufs_[b].ticket = -1;
+  next_buf_ ^= 1;
+  prev_greedy_rows_ = -1;  // no greedy tokens for the next step to read
   return logits;
+}
+
+int64_t TransformerRunner::enqueue_greedy(const std::vector<int>& token_ids, const std::vector<int>& positions,
+                                          const std::vector<int>& seq_ids, const std::vector<int>& token_src) {
+  const int M = (int)token_ids.size();
+  if (M == 0) throw std::invalid_argument("enqueue_greedy: no rows");
+  if ((int)positions.size() != M || (int)seq_ids.size() != M)
+    throw std::invalid_argument("enqueue_greedy: token_ids/positions/seq_ids sizes differ");
+  if (!token_src.empty() && (int)token_src.size() != M)
+    throw std::invalid_argument("enqueue_greedy: token_src must be empty or have one entry per row");
+  const int b = next_buf_;
+  StepBuf& sb = bufs_[b];
+  if (sb.pending) throw std::logic_error("enqueue_greedy: the step two before this one has not been waited for");
+  bool from_prev = false;
+  for (int v : token_src) from_prev = from_prev || v >= 0;
+  if (from_prev && prev_greedy_rows_ < 0)
+    throw std::logic_error("enqueue_greedy: token_src needs a greedy step enqueued just before");
+  using clk = std::chrono::steady_clock;
+  const auto t0 = clk::now();
+  prepare(b, token_ids.data(), positions.data(), seq_ids.data(), from_prev ? token_src.data() : nullptr, M);
+  const auto t1 = clk::now();
+  timed_step(b, true, from_prev);  // its argmax stores tokens and margins in sb.h_next
+  const auto t2 = clk::now();
+  auto ms = [](clk::duration d) { return std::chrono::duration<double, std::milli>(d).count(); };
+  sb.host_ms[0] = ms(t1 - t0);
+  sb.host_ms[1] = ms(t2 - t1);
+  sb.pending = true;
+  sb.ticket = tickets_++;
+  next_buf_ ^= 1;
+  prev_greedy_rows_ = M;
+  return sb.ticket;
+}
+
+std::vector<int> TransformerRunner::wait_greedy(int64_t ticket) {
+  int b = -1;
+  for (int i = 0; i < 2; ++i)
+    if (bufs_[i].pending && bufs_[i].ticket == ticket) b = i;
+  if (b < 0) throw std::invalid_argument("wait_greedy: no queued greedy step has this ticket");
+  StepBuf& sb = bufs_[b];
+  using clk = std::chrono::steady_clock;
+  const auto t0 = clk::now();
+  hip_check(hipEventSynchronize(sb.ev_stop), "wait_greedy sync");
+  const auto t1 = clk::now();
+  sb.pending = false;
+  hip_check(hipEventElapsedTime(&last_device_ms_, sb.ev_start, sb.ev_stop), "hipEventElapsedTime");
+  host_ms_[0] = sb.host_ms[0];
+  host_ms_[1] = sb.host_ms[1];
+  host_ms_[2] = std::chrono::duration<double, std::milli>(t1 - t0).count();
+  const int M = sb.M;
+  margins_.assign((const float*)(sb.h_next + M), (const float*)(sb.h_next + M) + M);
+  return std::vector<int>(sb.h_next, sb.h_next + M);
 }
 
 std::vector<int> TransformerRunner::forward_step_greedy(const std::vector<int>& token_ids,
                                                         const std::vector<int>& positions,
                                                         const std::vector<int>& seq_ids) {
   margins_.clear();
-  const int M = (int)token_ids.size();
-  if (M == 0) return {};
-  if ((int)positions.size() != M || (int)seq_ids.size() != M)
-    throw std::invalid_argument("forward_step_greedy: token_ids/positions/seq_ids sizes differ");
-  using clk = std::chrono::steady_clock;
-  const auto t0 = clk::now();
-  prepare(token_ids.data(), positions.data(), seq_ids.data(), M);
-  const auto t1 = clk::now();
-  timed_step(true);
-  hip_check(hipMemcpyAsync(h_next_, d_next_, (size_t)M * 8, hipMemcpyDeviceToHost, stream_),
-            "D2H tokens and margins");
-  const auto t2 = clk::now();
-  hip_check(hipStreamSynchronize(stream_), "forward_step_greedy sync");
-  const auto t3 = clk::now();
-  hip_check(hipEventElapsedTime(&last_device_ms_, ev_start_, ev_stop_), "hipEventElapsedTime");
-  auto ms = [](clk::duration d) { return std::chrono::duration<double, std::milli>(d).count(); };
-  host_ms_[0] = ms(t1 - t0);
-  host_ms_[1] = ms(t2 - t1);
-  host_ms_[2] = ms(t3 - t2);
-  margins_.assign((const float*)(h_next_ + M), (const float*)(h_next_ + M) + M);
-  return std::vector<int>(h_next_, h_next_ + M);
+  if (token_ids.empty()) return {};
+  return wait_greedy(enqueue_greedy(token_ids, positions, seq_ids, {}));
 }
 
 }  // namespace cbis

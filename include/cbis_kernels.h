@@ -270,6 +270,23 @@ int cbis_embed(int T, int d_model, const int* token_ids, const int* positions, i
                const void* tok_emb, const void* pos_emb, int vocab, int max_pos, float* out,
                cbis_stream_t stream);
 
+/* cbis_embed where a row's token may come from the device (no reference
+ * counterpart: it lets a decode step take its input tokens from the step
+ * before without a round trip through the host).  Row r uses token
+ * src_tokens[token_src[r]] when token_src[r] >= 0, else token_ids[r];
+ * token_src and src_tokens are both NULL (plain cbis_embed) or both set.
+ * The same rule for ids out of range applies to the token used.
+ * stage_bytes > 0 (a multiple of 16, both buffers 16-byte aligned, T > 0)
+ * also copies stage_src to stage_dst within the same launch: a caller that
+ * keeps a step's metadata in device-visible pinned host memory has it on the
+ * device for the kernels after this one without a separate copy.  The
+ * indices read here (token_ids, token_src, positions) may point into that
+ * host memory; the copy is not visible to this launch itself. */
+int cbis_embed_from(int T, int d_model, const int* token_ids, const int* token_src, const int* src_tokens,
+                    const int* positions, int emb_dtype, const void* tok_emb, const void* pos_emb, int vocab,
+                    int max_pos, float* out, const void* stage_src, void* stage_dst, size_t stage_bytes,
+                    cbis_stream_t stream);
+
 /* Row LayerNorm of fp32 X into fp32 or bf16 Y. */
 int cbis_layernorm(int T, int d_model, const float* X, int64_t ldx, const float* gamma, const float* beta,
                    float eps, int y_dtype, void* Y, int64_t ldy, cbis_stream_t stream);

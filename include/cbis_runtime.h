@@ -96,17 +96,32 @@ int cbis_runner_forward_step(cbis_runner* r, int n, const int* token_ids, const 
  * that reduce in the GEMM epilogue); next_tokens: host [n]. */
 int cbis_runner_forward_step_greedy(cbis_runner* r, int n, const int* token_ids, const int* positions,
                                     const int* seq_ids, int* next_tokens);
+/* Pipelined greedy steps (no reference counterpart: they let a decode loop
+ * queue step t + 1 before step t's tokens reach the host).
+ * cbis_runner_enqueue_greedy queues the step of cbis_runner_forward_step_greedy
+ * and returns at once with *ticket.  token_src (NULL, or n entries): row i
+ * with token_src[i] >= 0 takes as its input token the greedy token of row
+ * token_src[i] of the greedy step enqueued just before this one, and
+ * token_ids[i] is not used.  cbis_runner_wait_greedy waits for that step and
+ * writes min(capacity, rows) tokens; it returns its row count, and
+ * last_margins / last_device_ms / last_host_ms then describe it.  At most two
+ * steps are outstanding: enqueueing a third before the first was waited for
+ * fails. */
+int cbis_runner_enqueue_greedy(cbis_runner* r, int n, const int* token_ids, const int* positions, const int* seq_ids,
+                               const int* token_src, int64_t* ticket);
+int cbis_runner_wait_greedy(cbis_runner* r, int64_t ticket, int* next_tokens, int capacity);
 /* Top-2 margins (max logit minus the runner-up) of the last greedy step's
  * rows (no reference counterpart): writes min(capacity, n); returns n, which
  * is 0 after a plain forward_step. */
 int cbis_runner_last_margins(const cbis_runner* r, float* out, int capacity);
 /* Device time in ms of the last step's forward (no reference counterpart: a
  * diagnostic): two events on the runner's stream around the forward's
- * kernels, after the step's metadata H2D and before its result D2H. */
+ * kernels (the first of which also brings the step's metadata from pinned
+ * host memory; a greedy step's last one stores its tokens there). */
 float cbis_runner_last_device_ms(const cbis_runner* r);
 /* Host wall time in ms of the last greedy step's phases (no reference
- * counterpart: a diagnostic): out[0] host preparation and the metadata H2D
- * enqueue, out[1] the forward's launch, out[2] the wait for its results. */
+ * counterpart: a diagnostic): out[0] host preparation of the step's
+ * metadata, out[1] the forward's launch, out[2] the wait for its results. */
 void cbis_runner_last_host_ms(const cbis_runner* r, double out[3]);
 /* Device pointer of the last forward_step's [n, vocab] fp32 logits. */
 const float* cbis_runner_logits_device(cbis_runner* r);
@@ -195,6 +210,19 @@ int cbis_run_continuous_timed(cbis_runner* r, cbis_cache* c, int n_requests, con
                               int max_slots, int prefill_chunk, int step_token_budget, int* out_tokens,
                               double* step_ms, int max_steps, double* finish_ms);
 
+/* cbis_run_continuous_timed with one step in flight (no reference
+ * counterpart): step t + 1 is built and queued before step t's tokens come
+ * back, its decode rows taking their input tokens from step t on the device
+ * (cbis_runner_enqueue_greedy's token_src).  Same rows, tokens and page
+ * order for the same admissions; a request arriving while step t runs is
+ * admitted from step t + 2 at the earliest.  step_ms[k]: host ms from the
+ * later of step k's enqueue and the previous collection to its collection;
+ * finish_ms: when the host collected the request's last token. */
+int cbis_run_continuous_pipelined(cbis_runner* r, cbis_cache* c, int n_requests, const int* prompt_lens,
+                                  const int* prompt_tokens, const int* decode_lens, const double* arrival_ms,
+                                  int max_slots, int prefill_chunk, int step_token_budget, int* out_tokens,
+                                  double* step_ms, int max_steps, double* finish_ms);
+
 /* Runs the scheduler on the host only, with a stand-in step whose "greedy
  * token" of row (tok, pos, seq) is (31 tok + 7 pos + 13 seq + 1) mod vocab
  * (32-bit unsigned arithmetic), so the schedule can be checked without a
@@ -214,6 +242,17 @@ int cbis_schedule_dry_run_timed(cbis_cache* c, int n_requests, const int* prompt
                                 int prefill_chunk, int step_token_budget, int vocab, int* out_tokens, int* step_rows,
                                 int max_steps, int* row_tok, int* row_pos, int* row_sid, int max_rows,
                                 double* finish_ms);
+/* The timed dry run through cbis_run_continuous_pipelined's scheduler: the
+ * stand-in step resolves a row's token source against the outputs of the
+ * step queued before it and runs (on the virtual clock) when it is queued,
+ * so rows, tokens and admissions equal the timed dry run's; rows that take
+ * their token from the device come back with row_tok -1, and finish_ms is the
+ * virtual time at which the request's last token was collected. */
+int cbis_schedule_dry_run_pipelined(cbis_cache* c, int n_requests, const int* prompt_lens, const int* prompt_tokens,
+                                    const int* decode_lens, const double* arrival_ms, double step_time_ms,
+                                    int max_slots, int prefill_chunk, int step_token_budget, int vocab,
+                                    int* out_tokens, int* step_rows, int max_steps, int* row_tok, int* row_pos,
+                                    int* row_sid, int max_rows, double* finish_ms);
 
 #ifdef __cplusplus
 }

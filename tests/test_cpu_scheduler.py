@@ -253,3 +253,29 @@ def test_arrivals_rejected_when_unordered(cbis):
         cbis.schedule_dry_run(_cache(cbis), [[1], [2]], [1, 1], 100, arrival_ms=[5.0, 1.0])
     with pytest.raises(RuntimeError, match="arrival_ms"):
         cbis.schedule_dry_run(_cache(cbis), [[1]], [1], 100, arrival_ms=[-1.0])
+
+
+@settings(max_examples=30, deadline=None)
+@given(seed=st.integers(0, 10 ** 6), n=st.integers(1, 12), slots=st.integers(1, 6), chunk=st.sampled_from([0, 1, 7]),
+       budget=st.sampled_from([0, 9]), gap=st.sampled_from([0.0, 0.5, 3.0]))
+def test_pipelined_schedule_is_the_synchronous_one(cbis, seed, n, slots, chunk, budget, gap):
+    """The pipelined scheduler queues step t + 1 before step t's tokens are
+    back; its decode rows name the previous step's row that holds their input
+    token and the stand-in device resolves it there.  Steps, resolved row
+    tokens, generated tokens and page use must equal the synchronous
+    schedule's; a request's finish is seen one step later at most (its last
+    step is collected after the next one is queued)."""
+    prompts, dl = _workload(seed, n, 1, 30, 1, 6)
+    rng = random.Random(seed + 2)
+    arrivals, t = [], 0.0
+    for _ in range(n):
+        t += rng.random() * 2 * gap
+        arrivals.append(round(t, 3))
+    kw = dict(max_slots=slots, prefill_chunk=chunk, step_token_budget=budget, arrival_ms=arrivals, step_time_ms=1.0)
+    c_sync, c_pipe = _cache(cbis), _cache(cbis)
+    toks, steps, fin = cbis.schedule_dry_run(c_sync, prompts, dl, 300, **kw)
+    ptoks, psteps, pfin = cbis.schedule_dry_run(c_pipe, prompts, dl, 300, pipeline=True, **kw)
+    assert psteps == steps and ptoks == toks
+    for f, pf in zip(fin, pfin):
+        assert f <= pf <= f + 1.0
+    assert c_pipe.num_free_pages() == c_sync.num_free_pages() == 4096

@@ -718,6 +718,58 @@ def test_embed(cbis, oracle, dev, edt):
     assert np.array_equal(got[~bad], ref.astype(np.float32)[~bad])
 
 
+@pytest.mark.parametrize("edt", ["f32", "bf16"])
+@pytest.mark.parametrize("stage_words", [0, 1, 777, 70000])
+def test_embed_from_token_src_and_staging(cbis, oracle, dev, edt, stage_words):
+    """cbis_embed_from: rows with token_src >= 0 take src_tokens[token_src]
+    (ids out of range there still give NaN rows), the others token_ids; the
+    same launch copies stage_words 16-byte words (here device to device; the
+    runner's host-memory case is covered by its whole-step tests) and
+    touches nothing past them.  Misaligned or unpaired arguments are
+    rejected."""
+    import torch
+    V, S, D, M = 512, 100, 256, 50
+    te = oracle.normal(19, 1, V * D, 0.02).reshape(V, D)
+    pe = oracle.normal(19, 2, S * D, 0.02).reshape(S, D)
+    tok = oracle.uniform_int(19, 3, M, 0, V - 1)
+    pos = oracle.uniform_int(19, 4, M, 0, S - 1)
+    prev = oracle.uniform_int(19, 5, 20, 0, V - 1)
+    prev[7] = V + 3  # an out-of-range token left by the previous step
+    rng = np.random.default_rng(19)
+    tsrc = np.where(rng.random(M) < 0.6, rng.integers(0, 20, M), -1).astype(np.int32)
+    tsrc[0], tsrc[1] = 7, -1
+    tok[tsrc >= 0] = -5  # not read for those rows
+    if edt == "f32":
+        TE, PE, tev, pev = to_dev(te, dev), to_dev(pe, dev), te, pe
+    else:
+        (TE, tev), (PE, pev) = bf16_dev(te, dev), bf16_dev(pe, dev)
+    out = torch.empty((M, D), dtype=torch.float32, device=dev)
+    TOK, POS, TSRC, PREV = to_dev(tok, dev), to_dev(pos, dev), to_dev(tsrc, dev), to_dev(prev, dev)
+    src_words = torch.randint(-2 ** 31, 2 ** 31 - 1, (max(stage_words, 1) * 4,), dtype=torch.int32, device=dev)
+    dst_words = torch.full(((stage_words + 8) * 4,), 12345, dtype=torch.int32, device=dev)
+    k = cbis.kernels()
+    cbis.check(k.cbis_embed_from(M, D, ptr(TOK), ptr(TSRC), ptr(PREV), ptr(POS), cbis.DTYPES[edt], ptr(TE), ptr(PE),
+                                 V, S, ptr(out), ptr(src_words), ptr(dst_words), stage_words * 16, stream()))
+    sync()
+    used = np.where(tsrc >= 0, prev[np.maximum(tsrc, 0)], tok)
+    bad = used >= V
+    ref = tev[np.where(bad, 0, used)].astype(np.float64) + pev[pos]
+    got = out.cpu().numpy()
+    assert bad[0] and np.isnan(got[bad]).all()
+    assert np.array_equal(got[~bad], ref.astype(np.float32)[~bad])
+    d = dst_words.cpu().numpy()
+    assert np.array_equal(d[: stage_words * 4], src_words.cpu().numpy()[: stage_words * 4])
+    assert (d[stage_words * 4:] == 12345).all()
+    # 8 bytes is not a 16-byte multiple; an offset of 4 bytes is misaligned;
+    # token_src without src_tokens is unpaired.
+    assert k.cbis_embed_from(M, D, ptr(TOK), ptr(TSRC), ptr(PREV), ptr(POS), cbis.DTYPES[edt], ptr(TE), ptr(PE), V,
+                             S, ptr(out), ptr(src_words), ptr(dst_words), 8, stream()) != 0
+    assert k.cbis_embed_from(M, D, ptr(TOK), ptr(TSRC), ptr(PREV), ptr(POS), cbis.DTYPES[edt], ptr(TE), ptr(PE), V,
+                             S, ptr(out), ptr(src_words) + 4, ptr(dst_words), 16, stream()) != 0
+    assert k.cbis_embed_from(M, D, ptr(TOK), ptr(TSRC), None, ptr(POS), cbis.DTYPES[edt], ptr(TE), ptr(PE), V,
+                             S, ptr(out), None, None, 0, stream()) != 0
+
+
 @pytest.mark.parametrize("N", [32000, 1001, 4 * 1024 * 9 + 12])
 def test_argmax_first_max_wins(cbis, oracle, dev, N):
     """Both load paths (16-byte rows in unrolled float4 rounds plus a tail,
