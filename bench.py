@@ -436,42 +436,67 @@ def run_c4(args, cbis, oracle):
     # runner without a per-element conversion); the runner redoes all of its
     # per-step host work (checks, slot resolution, block tables, one H2D copy).
     tok, pos, sid = (np.asarray(st[k], dtype=np.int32) for k in ("tok", "pos", "sid"))
-    step = lambda: runner.forward_step_greedy(tok, pos, sid)
-    # Every step is timed twice: host wall time around the call (the step
-    # returns after its tokens are back on the host) and the device time of
-    # its forward between two events on the runner's stream.  The collector
-    # is paused from before the warmup, whose steps absorb the idle GPU's
-    # slower first step after the collection.
-    wall, dev, host = [], [], []
-    with gc_paused():
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            t1 = time.perf_counter()
-            step()
-            wall.append((time.perf_counter() - t1) * 1000.0)
-            dev.append(runner.last_device_ms())
-            host.append(runner.last_host_ms())
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
-    value = 192.0 * args.steps / dt
-    stats = {"wall_median": float(np.median(wall)), "wall_mean": float(np.mean(wall)), "wall_min": min(wall),
-             "wall_max": max(wall), "device_median": float(np.median(dev)), "device_min": min(dev),
-             "device_max": max(dev), "region_mean": dt * 1000.0 / args.steps}
-    stats = {k: round(v, 4) for k, v in stats.items()}
+    # Pipelined steps, as the pipelined scheduler runs them: step k + 1 is
+    # queued before step k's tokens are waited for, and each of the 192
+    # decode rows takes its input token from its own row of the step before
+    # (read on the device); the prefill rows' tokens come from the host.
+    src = np.full(len(tok), -1, dtype=np.int32)
+    src[:192] = np.arange(192, dtype=np.int32)
+    # Every step is timed twice: host wall time (synchronous: around the
+    # call, which returns once the step's tokens are on the host; pipelined:
+    # between consecutive steps' results) and the device time of its forward
+    # between two events on the runner's stream.  The collector is paused
+    # from before the warmup, whose steps absorb the idle GPU's slower first
+    # step after the collection.
+    def timed(pipelined):
+        wall, dev, host = [], [], []
+        with gc_paused():
+            for _ in range(args.warmup):
+                runner.forward_step_greedy(tok, pos, sid)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            if pipelined:
+                prev = runner.enqueue_greedy(tok, pos, sid)
+                t_last = time.perf_counter()
+                for k in range(args.steps):
+                    nxt = runner.enqueue_greedy(tok, pos, sid, src) if k + 1 < args.steps else None
+                    runner.wait_greedy(prev)
+                    t1 = time.perf_counter()
+                    wall.append((t1 - t_last) * 1000.0)
+                    t_last = t1
+                    dev.append(runner.last_device_ms())
+                    host.append(runner.last_host_ms())
+                    prev = nxt
+            else:
+                for _ in range(args.steps):
+                    t1 = time.perf_counter()
+                    runner.forward_step_greedy(tok, pos, sid)
+                    wall.append((time.perf_counter() - t1) * 1000.0)
+                    dev.append(runner.last_device_ms())
+                    host.append(runner.last_host_ms())
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+        stats = {"wall_median": float(np.median(wall)), "wall_mean": float(np.mean(wall)), "wall_min": min(wall),
+                 "wall_max": max(wall), "device_median": float(np.median(dev)), "device_min": min(dev),
+                 "device_max": max(dev), "region_mean": dt * 1000.0 / args.steps}
+        stats = {k: round(v, 4) for k, v in stats.items()}
+        mode = "pipelined" if pipelined else "synchronous"
+        _log(f"c4 {mode} per-step wall ms: " + " ".join(f"{x:.3f}" for x in wall))
+        _log(f"c4 {mode} per-step device ms: " + " ".join(f"{x:.3f}" for x in dev))
+        med = float(np.median(wall))
+        for i, (w_, d_, h_) in enumerate(zip(wall, dev, host)):
+            if w_ > med + 1.0:
+                _log(f"c4 {mode} slow step {i}: wall {w_:.3f} ms, device {d_:.3f} ms; host phases: prepare "
+                     f"{h_[0]:.3f}, launch {h_[1]:.3f}, wait {h_[2]:.3f} ms")
+        value = 192.0 * args.steps / dt
+        _log(f"c4 {mode}: step median {stats['wall_median']:.3f} ms (mean over the region "
+             f"{stats['region_mean']:.3f}, device median {stats['device_median']:.3f}) -> {value:.1f} decode tok/s "
+             f"over the region ({1216 * args.steps / dt:.0f} rows/s)")
+        return value, stats
+
+    sync_value, sync_stats = timed(False)
+    value, stats = timed(True)
     ms_step = stats["wall_median"]
-    _log("c4 per-step wall ms: " + " ".join(f"{x:.3f}" for x in wall))
-    _log("c4 per-step device ms: " + " ".join(f"{x:.3f}" for x in dev))
-    med = float(np.median(wall))
-    for i, (w_, d_, h_) in enumerate(zip(wall, dev, host)):
-        if w_ > med + 1.0:
-            _log(f"c4 slow step {i}: wall {w_:.3f} ms, device {d_:.3f} ms; host phases: prepare + H2D "
-                 f"{h_[0]:.3f}, launch {h_[1]:.3f}, wait {h_[2]:.3f} ms")
-    _log(f"c4 step median {ms_step:.3f} ms (mean over the region {stats['region_mean']:.3f}, device median "
-         f"{stats['device_median']:.3f}) -> {value:.1f} decode tok/s over the region "
-         f"({1216 * args.steps / dt:.0f} rows/s)")
     att_ms, att_bytes = decode_attention_timing(cbis, st, max(10, args.steps))
     att_gbs = att_bytes / att_ms / 1e6
     _log(f"decode attention (1 layer): {att_ms:.4f} ms, {att_bytes / 1e9:.3f} GB -> {att_gbs:.0f} GB/s")
@@ -491,11 +516,14 @@ def run_c4(args, cbis, oracle):
         "unit": "decode tokens/s",
         "ms_per_step": round(ms_step, 4),
         "step_ms": stats,
+        "synchronous": {"value": round(sync_value, 2), "step_ms": sync_stats},
         "dtype": "bf16",
         "data": "synthetic (seeded weights N(0,0.02); K/V cache N(0,1); random token ids)",
         "config": {"workload": "c4_mixed_step", "model": "gpt-mid L16 d2048 h64x32 mlp8192 V32000",
                    "decode_rows": 192, "decode_kv_len": "U[256,4096]", "prefill_chunks": "2x512 (pos 0, 512)",
-                   "rows_per_step": 1216, "page_size": 16, "page_table": "shuffled", "parallelism": "none (1 GPU)"},
+                   "rows_per_step": 1216, "page_size": 16, "page_table": "shuffled", "parallelism": "none (1 GPU)",
+                   "steps": "pipelined (step k + 1 queued before step k's tokens are back; decode rows take "
+                            "their token from the step before on the device)"},
         "roofline": {"bound": "hbm", "kernel": "paged_decode_kernel<bf16>, one layer, one pass per row",
                      "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(att_gbs / HBM_PEAK_GBS, 4),
@@ -672,31 +700,49 @@ def run_c5(args, cbis, oracle):
     fp32 scales) and a bf16 paged K/V cache; 16 sequences whose caches hold
     32704 synthetic tokens greedy-decode 64 tokens each at positions
     32704..32767 (the last one is kMaxSeqLen - 1).  A step is 16 rows;
-    value = 16 * 64 / wall time of the 64 steps (median over `steps` runs)."""
+    value = 16 * 64 / wall time of the 64 steps (median over `steps` runs),
+    the steps pipelined (each queued before the previous one's tokens are
+    back, its rows reading their tokens from it on the device); the
+    synchronous loop's rate is reported beside it."""
     import torch
     st = c5_setup(cbis, oracle)
     runner, cache, seqs, first = st["runner"], st["cache"], st["seqs"], st["first"]
     n_seq, ctx, gen = st["n_seq"], st["ctx"], st["gen"]
 
-    def run():
+    def run_sync():
         toks = first
         for i in range(gen):
             toks = runner.forward_step_greedy(toks, [ctx + i] * n_seq, seqs)
         return toks
 
-    times = []
+    src = list(range(n_seq))
+
+    def run_pipelined():
+        prev = runner.enqueue_greedy(first, [ctx] * n_seq, seqs)
+        for i in range(1, gen):
+            nxt = runner.enqueue_greedy([-1] * n_seq, [ctx + i] * n_seq, seqs, src)
+            runner.wait_greedy(prev)
+            prev = nxt
+        return runner.wait_greedy(prev)
+
+    rate, last = {}, {}
     with gc_paused():
-        for _ in range(max(1, args.warmup)):
-            run()
-        for _ in range(args.steps):
-            torch.cuda.synchronize()
-            t1 = time.perf_counter()
-            run()
-            torch.cuda.synchronize()
-            times.append(time.perf_counter() - t1)
-    dt = float(np.median(times))
-    value = n_seq * gen / dt
-    _log(f"c5: {gen} steps in {dt * 1000:.2f} ms -> {value:.1f} tok/s ({dt * 1000 / gen:.3f} ms/step)")
+        for name, run in (("synchronous", run_sync), ("pipelined", run_pipelined)):
+            times = []
+            for _ in range(max(1, args.warmup)):
+                run()
+            for _ in range(args.steps):
+                torch.cuda.synchronize()
+                t1 = time.perf_counter()
+                last[name] = run()
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t1)
+            dt = float(np.median(times))
+            rate[name] = (n_seq * gen / dt, dt)
+            _log(f"c5 {name}: {gen} steps in {dt * 1000:.2f} ms -> {rate[name][0]:.1f} tok/s "
+                 f"({dt * 1000 / gen:.3f} ms/step)")
+    assert last["pipelined"] == last["synchronous"], "pipelined and synchronous greedy tokens differ"
+    value, dt = rate["pipelined"]
     cpu = None
     if not args.no_cpu:
         spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
@@ -711,7 +757,8 @@ def run_c5(args, cbis, oracle):
             "unit": "decode tokens/s", "ms_per_step": round(dt * 1000 / gen, 4), "dtype": "bf16 x fp8-e4m3",
             "data": "synthetic (fp8 weights absmax-quantised from N(0,0.02); K/V cache N(0,1))",
             "config": {"workload": "c5_long_context_fp8_decode", "sequences": n_seq, "kv_len": "32704..32767",
-                       "decode_tokens": gen, "kv_cache_gb": round(16 * n_seq * 32768 * 2048 * 2 * 2 / 1e9, 1)},
+                       "decode_tokens": gen, "kv_cache_gb": round(16 * n_seq * 32768 * 2048 * 2 * 2 / 1e9, 1),
+                       "steps": "pipelined", "synchronous_decode_tok_s": round(rate["synchronous"][0], 2)},
             "cpu_baseline": cpu}
 
 
