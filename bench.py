@@ -998,8 +998,8 @@ def main():
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": res["dtype"], "data": res["data"], "config": res["config"],
-            "step_ms": res["step_ms"], "roofline": res["roofline"], "gemm_roofline": res["gemm_roofline"],
-            "cpu_baseline": res["cpu_baseline"], "machine": res["machine"]}
+            "step_ms": res["step_ms"], "synchronous": res["synchronous"], "roofline": res["roofline"],
+            "gemm_roofline": res["gemm_roofline"], "cpu_baseline": res["cpu_baseline"], "machine": res["machine"]}
     print(json.dumps(line), flush=True)
 
 

@@ -102,6 +102,7 @@ KERNEL_SYMBOLS = {
     "cbis_paged_attention_workspace_size": (_SZ, [ctypes.POINTER(AttnDesc)]),
     "cbis_paged_attention": (_I, [ctypes.POINTER(AttnDesc), _P]),
     "cbis_paged_attention_static": (_I, [ctypes.POINTER(AttnDesc), _P]),
+    "cbis_paged_attention_proj": (_I, [ctypes.POINTER(AttnDesc), ctypes.POINTER(GemmDesc), _P]),
     "cbis_paged_prefill_attention": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
     "cbis_paged_attention_mixed": (_I, [ctypes.POINTER(AttnDesc), _I, _P, _P]),
     "cbis_embed": (_I, [_I, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P]),
@@ -147,6 +148,7 @@ RUNTIME_SYMBOLS = {
     "cbis_runner_logits_device": (_P, [_P]),
     "cbis_runner_stream": (_P, [_P]),
     "cbis_runner_set_graphs": (None, [_P, _I]),
+    "cbis_runner_set_fused_decode": (None, [_P, _I]),
     "cbis_runner_last_plan": (_I, [_P, _IP, _I]),
     "cbis_runner_last_device_ms": (ctypes.c_float, [_P]),
     "cbis_runner_last_host_ms": (None, [_P, ctypes.POINTER(ctypes.c_double)]),
@@ -454,7 +456,13 @@ class TransformerRunner:
     def set_graphs(self, enable: bool) -> None:
         runtime().cbis_runner_set_graphs(self._h, int(enable))
 
-    PLAN_FIELDS = ("rows", "decode_rows", "prefill_tiles", "sequences", "bt_width", "max_kv", "split_tokens")
+    def set_fused_decode(self, enable: bool) -> None:
+        """Small all-decode steps run attention + out-projection as one launch
+        per layer (the default) or as two."""
+        runtime().cbis_runner_set_fused_decode(self._h, int(enable))
+
+    PLAN_FIELDS = ("rows", "decode_rows", "prefill_tiles", "sequences", "bt_width", "max_kv", "split_tokens",
+                   "fused_attention_proj")
 
     def last_plan(self) -> dict:
         """How the last step ran; split_tokens 1 << 30 = one pass per decode

@@ -28,6 +28,7 @@
 // index, applied to V^T as well) and V^T read from an LDS copy of the 32-key
 // V tile with gfx950's transposing LDS read (ds_read_b64_tr_b16).
 #include <mutex>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -61,6 +62,21 @@ struct DecodeArgs {
   int split_tokens;
   int max_kv;  // clamp for kv_len (bt_stride * page_size)
   float qscale;
+  // The out-projection of cbis_paged_attention_proj (read only by the
+  // paged_decode_kernel instantiations with a weight type): Y[row, n] =
+  // attn(row) . W[n, :] (* scale[n]) (+ bias[n]) (+ res[row, n]) for the
+  // workgroup's 64 columns n; the grid is p_rows x (D / 64) workgroups.
+  const void* pw;
+  int64_t pldw;
+  const float* pscale;
+  const float* pbias;
+  const float* pres;
+  int64_t pldr;
+  float* py;
+  int64_t pldy;
+  int p_rows;
+  int pkpt;     // k per thread: D / 8
+  int px_bf16;  // the attention output is rounded to bf16 before the product
 };
 
 template <typename KVT>
@@ -95,8 +111,73 @@ __device__ inline uint4 load_stream(const T* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <typename KVT, int NW>
+// A fused workgroup's share of the out-projection weights: thread t takes
+// column part * 64 + (t >> 3) and k = (t & 7) * kpt .. + kpt - 1 (kpt <= KMAX),
+// loaded when the kernel starts, so their round trip overlaps the attention's.
+template <typename WT>
+struct ProjW {
+  __device__ void load(const DecodeArgs&, int, int) {}
+};
+template <>
+struct ProjW<float> {
+  static constexpr int KMAX = 32;
+  float4 w[KMAX / 4];
+  __device__ void load(const DecodeArgs& a, int part, int t) {
+    const float* p = (const float*)a.pw + (int64_t)(part * 64 + (t >> 3)) * a.pldw + (t & 7) * a.pkpt;
+#pragma unroll
+    for (int i = 0; i < KMAX / 4; ++i)
+      if (4 * i < a.pkpt) w[i] = *(const float4*)(p + 4 * i);
+  }
+  // sum over this thread's k of x[k] * W[n, k], in k order
+  __device__ float dot(const DecodeArgs& a, const float* x) const {
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < KMAX / 4; ++i) {
+      if (4 * i >= a.pkpt) break;
+      const float4 v = *(const float4*)(x + 4 * i);
+      d += v.x * w[i].x;
+      d += v.y * w[i].y;
+      d += v.z * w[i].z;
+      d += v.w * w[i].w;
+    }
+    return d;
+  }
+};
+template <>
+struct ProjW<uint16_t> {  // bf16
+  static constexpr int KMAX = 64;
+  uint4 w[KMAX / 8];
+  __device__ void load(const DecodeArgs& a, int part, int t) {
+    const uint16_t* p = (const uint16_t*)a.pw + (int64_t)(part * 64 + (t >> 3)) * a.pldw + (t & 7) * a.pkpt;
+#pragma unroll
+    for (int i = 0; i < KMAX / 8; ++i)
+      if (8 * i < a.pkpt) w[i] = *(const uint4*)(p + 8 * i);
+  }
+  __device__ float dot(const DecodeArgs& a, const float* x) const {
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < KMAX / 8; ++i) {
+      if (8 * i >= a.pkpt) break;
+      const float4 v0 = *(const float4*)(x + 8 * i), v1 = *(const float4*)(x + 8 * i + 4);
+      d += v0.x * bf16lo(w[i].x);
+      d += v0.y * bf16hi(w[i].x);
+      d += v0.z * bf16lo(w[i].y);
+      d += v0.w * bf16hi(w[i].y);
+      d += v1.x * bf16lo(w[i].z);
+      d += v1.y * bf16hi(w[i].z);
+      d += v1.z * bf16lo(w[i].w);
+      d += v1.w * bf16hi(w[i].w);
+    }
+    return d;
+  }
+};
+
+// WT void: decode attention.  WT float / uint16_t (bf16): the same
+// attention for one-pass rows of one head block, each row's workgroups then
+// applying the out-projection to it (cbis_paged_attention_proj).
+template <typename KVT, int NW, typename WT = void>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs a) {
+  constexpr bool PROJ = !std::is_void<WT>::value;
   constexpr int EPL = KVTraits<KVT>::EPL;
   constexpr int G = kHD / EPL;  // lanes per head
   constexpr int HPB = 64 / G;   // heads per block (one 1 KiB wave load)
@@ -104,6 +185,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
   int bid = blockIdx.x;
+  int part = 0;
+  ProjW<WT> pw;
+  if constexpr (PROJ) {
+    // Workgroups b, b + p_rows, ... share a row (and, with 8 rows, an XCD).
+    part = bid / a.p_rows;
+    bid -= part * a.p_rows;
+    pw.load(a, part, threadIdx.x);
+  }
   const int hb = bid % a.n_hblocks;
   bid /= a.n_hblocks;
   const int split = bid % a.n_splits;
@@ -117,6 +206,16 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
   // n_splits splits (the grid and workspace cover no more).
   const int nsplit_row = min((kv_len + a.split_tokens - 1) / a.split_tokens, a.n_splits);
   const int* bt = a.bt + (int64_t)(a.row_bt ? a.row_bt[row] : row) * a.bt_stride;
+  // Projection epilogue inputs of this thread's column, loaded now.
+  [[maybe_unused]] const int pcol = part * 64 + (threadIdx.x >> 3);
+  [[maybe_unused]] float p_sc = 1.f, p_bi = 0.f, p_res = 0.f;
+  if constexpr (PROJ) {
+    if ((threadIdx.x & 7) == 0) {
+      if (a.pscale) p_sc = a.pscale[pcol];
+      if (a.pbias) p_bi = a.pbias[pcol];
+      if (a.pres) p_res = a.pres[(int64_t)row * a.pldr + pcol];
+    }
+  }
 
   // The last head block may be partial (n_heads not a multiple of HPB): its
   // lanes past the last head read that head's slice (in bounds) and store
@@ -203,6 +302,48 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
 #pragma unroll
   for (int e = 0; e < EPL; ++e) sacc[wave][e][lane] = acc[e];
   __syncthreads();
+  if constexpr (PROJ) {
+    // The row's attention output (all heads) into LDS, normalised (and
+    // rounded as the separate path stores it), then each thread's share of
+    // the projection, summed over the column's 8 threads.
+    __shared__ __attribute__((aligned(16))) float so[512];
+    if (wave == 0) {
+      float M = sm[0][lane];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) M = fmaxf(M, sm[w][lane]);
+      float L = 0.f, O[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) O[e] = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float c = fast_exp2(sm[w][lane] - M);
+        L += sl[w][lane] * c;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) O[e] += sacc[w][e][lane] * c;
+      }
+      if (head_ok) {
+        const float inv = 1.f / L;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float v = O[e] * inv;
+          so[lane_off + e] = a.px_bf16 ? bf16_to_f32(f32_to_bf16(v)) : v;
+        }
+      }
+    }
+    __syncthreads();
+    float d = pw.dot(a, so + (threadIdx.x & 7) * a.pkpt);
+    d += __shfl_xor(d, 1);
+    d += __shfl_xor(d, 2);
+    d += __shfl_xor(d, 4);
+    if ((threadIdx.x & 7) == 0) {
+      // cbis_gemm's epilogue order: scale, bias, residual.
+      if (a.pscale) d *= p_sc;
+      if (a.pbias) d += p_bi;
+      if (a.pres) d += p_res;
+      a.py[(int64_t)row * a.pldy + pcol] = d;
+    }
+    return;
+  }
   if (wave != 0) return;
   float M = sm[0][lane];
 #pragma unroll
@@ -766,7 +907,7 @@ int head_blocks(const cbis_attn_desc* d) {
   return (int)cdiv(d->n_heads, hpb);
 }
 
-int validate(const cbis_attn_desc* d, const char* who) {
+int validate(const cbis_attn_desc* d, const char* who, bool need_out = true) {
   CBIS_REQUIRE(d, CBIS_ERR_INVALID, "%s: null descriptor", who);
   CBIS_REQUIRE(d->head_dim == kHD && d->page_size == kPS, CBIS_ERR_UNSUPPORTED,
                "%s: head_dim %d / page_size %d (this build supports 32 / 16)", who, d->head_dim, d->page_size);
@@ -777,8 +918,11 @@ int validate(const cbis_attn_desc* d, const char* who) {
   CBIS_REQUIRE(d->q_dtype == CBIS_F32 || d->q_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: q dtype", who);
   CBIS_REQUIRE(d->out_dtype == CBIS_F32 || d->out_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: out dtype", who);
   CBIS_REQUIRE(d->n_rows >= 0 && d->num_pages > 0 && d->bt_stride > 0, CBIS_ERR_INVALID, "%s: bad sizes", who);
-  CBIS_REQUIRE(d->q && d->k_pool && d->v_pool && d->block_table && d->out, CBIS_ERR_INVALID, "%s: null pointer", who);
-  CBIS_REQUIRE(d->ldo % 4 == 0 && ((uintptr_t)d->out & 15u) == 0, CBIS_ERR_INVALID, "%s: out rows must be 16-byte aligned", who);
+  CBIS_REQUIRE(d->q && d->k_pool && d->v_pool && d->block_table && (d->out || !need_out), CBIS_ERR_INVALID,
+               "%s: null pointer", who);
+  if (need_out)
+    CBIS_REQUIRE(d->ldo % 4 == 0 && ((uintptr_t)d->out & 15u) == 0, CBIS_ERR_INVALID,
+                 "%s: out rows must be 16-byte aligned", who);
   CBIS_REQUIRE(((uintptr_t)d->k_pool & 15u) == 0 && ((uintptr_t)d->v_pool & 15u) == 0, CBIS_ERR_INVALID,
                "%s: pools must be 16-byte aligned", who);
   return CBIS_OK;
@@ -855,6 +999,70 @@ int paged_attention_ws(const cbis_attn_desc* d, void* ws, size_t ws_bytes, hipSt
   rc = decode_launch(d, ws, ws_bytes, s, &m, &ns, who);
   if (rc || ns <= 1) return rc;
   return merge_launch(m, d->n_rows, s);
+}
+
+// Decode attention + out-projection in one launch (cbis_paged_attention_proj).
+int attention_proj(const cbis_attn_desc* d, const cbis_gemm_desc* g, hipStream_t s) {
+  const char* who = "cbis_paged_attention_proj";
+  int rc = validate(d, who, false);
+  if (rc) return rc;
+  CBIS_REQUIRE(d->row_pos && g, CBIS_ERR_INVALID, "%s: null row_pos / projection", who);
+  const int D = d->n_heads * kHD;
+  const int wbytes = g->w_dtype == CBIS_F32 ? 4 : g->w_dtype == CBIS_BF16 ? 2 : 0;
+  CBIS_REQUIRE(head_blocks(d) == 1 && D % 64 == 0 && wbytes && D * wbytes <= 1024, CBIS_ERR_UNSUPPORTED,
+               "%s: %d heads of %s K/V with %s weights (needs one head block, n_heads * head_dim a multiple of "
+               "64, at most 256 with fp32 weights or 512 with bf16)",
+               who, d->n_heads, d->kv_dtype == CBIS_F32 ? "fp32" : "bf16",
+               g->w_dtype == CBIS_F32 ? "fp32" : g->w_dtype == CBIS_BF16 ? "bf16" : "other");
+  CBIS_REQUIRE(g->N == D && g->K == D, CBIS_ERR_INVALID, "%s: projection N %d, K %d must equal n_heads * head_dim %d",
+               who, g->N, g->K, D);
+  CBIS_REQUIRE(g->y_dtype == CBIS_F32 && (g->x_dtype == CBIS_F32 || g->x_dtype == CBIS_BF16) &&
+                   g->epilogue == CBIS_EPI_NONE && !g->k_pool && !g->v_pool,
+               CBIS_ERR_UNSUPPORTED, "%s: fp32 Y, fp32 / bf16 X, no GELU, no K/V scatter", who);
+  CBIS_REQUIRE(g->W && g->Y && (!g->residual || g->ldr >= D) && g->ldy >= D, CBIS_ERR_INVALID,
+               "%s: null W / Y or short rows", who);
+  CBIS_REQUIRE(((uintptr_t)g->W & 15u) == 0 && g->ldw >= D && (g->ldw * wbytes) % 16 == 0, CBIS_ERR_INVALID,
+               "%s: W must be 16-byte aligned with 16-byte row pitch", who);
+  if (d->n_rows == 0) return CBIS_OK;
+  DecodeArgs a = {};
+  a.rows = d->rows;
+  a.q = d->q;
+  a.ldq = d->ldq;
+  a.q_bf16 = d->q_dtype == CBIS_BF16;
+  a.kpool = d->k_pool;
+  a.vpool = d->v_pool;
+  a.num_pages = d->num_pages;
+  a.bt = d->block_table;
+  a.bt_stride = d->bt_stride;
+  a.row_bt = d->row_bt;
+  a.row_pos = d->row_pos;
+  a.n_heads = d->n_heads;
+  a.n_hblocks = 1;
+  a.n_splits = 1;
+  a.split_tokens = 1 << 30;  // one pass per row
+  a.max_kv = (int)std::min<int64_t>(d->bt_stride * kPS, 1 << 30);
+  a.qscale = kLog2e / sqrtf((float)kHD);
+  a.pw = g->W;
+  a.pldw = g->ldw;
+  a.pscale = g->w_scale;
+  a.pbias = g->bias;
+  a.pres = g->residual;
+  a.pldr = g->ldr;
+  a.py = (float*)g->Y;
+  a.pldy = g->ldy;
+  a.p_rows = d->n_rows;
+  a.pkpt = D / 8;
+  a.px_bf16 = g->x_dtype == CBIS_BF16;
+  const int64_t grid = (int64_t)d->n_rows * (D / 64);
+  CBIS_REQUIRE(grid < (1LL << 31), CBIS_ERR_UNSUPPORTED, "%s: grid too large", who);
+  if (d->kv_dtype == CBIS_F32) {
+    if (g->w_dtype == CBIS_F32) paged_decode_kernel<float, 8, float><<<(unsigned)grid, 512, 0, s>>>(a);
+    else paged_decode_kernel<float, 8, uint16_t><<<(unsigned)grid, 512, 0, s>>>(a);
+  } else {
+    if (g->w_dtype == CBIS_F32) paged_decode_kernel<uint16_t, 8, float><<<(unsigned)grid, 512, 0, s>>>(a);
+    else paged_decode_kernel<uint16_t, 8, uint16_t><<<(unsigned)grid, 512, 0, s>>>(a);
+  }
+  return check_launch(who);
 }
 
 // Split-KV partials of cbis_paged_attention_static: a file-scope device
@@ -951,6 +1159,10 @@ size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d) {
 int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream) {
   return paged_attention_ws(d, d ? d->workspace : nullptr, d ? d->workspace_bytes : 0, (hipStream_t)stream,
                             "cbis_paged_attention");
+}
+
+int cbis_paged_attention_proj(const cbis_attn_desc* d, const cbis_gemm_desc* proj, cbis_stream_t stream) {
+  return attention_proj(d, proj, (hipStream_t)stream);
 }
 
 int cbis_paged_attention_static(const cbis_attn_desc* d, cbis_stream_t stream) {

@@ -268,6 +268,8 @@ void* cbis_runner_stream(cbis_runner* r) { return (void*)r->impl->stream(); }
 
 void cbis_runner_set_graphs(cbis_runner* r, int enable) { r->impl->set_graphs(enable != 0); }
 
+void cbis_runner_set_fused_decode(cbis_runner* r, int enable) { r->impl->set_fused_decode(enable != 0); }
+
 int cbis_runner_last_margins(const cbis_runner* r, float* out, int capacity) {
   return guard([&] {
     const std::vector<float>& m = r->impl->last_margins();

@@ -194,6 +194,10 @@ class TransformerRunner {
   const float* logits_device() const { return d_logits_; }
   hipStream_t stream() const { return stream_; }
   void set_graphs(bool on) { use_graphs_ = on; }
+  // Small all-decode steps run each layer's attention and out-projection as
+  // one launch (cbis_paged_attention_proj) when the model's widths allow it;
+  // off: two launches, as every other step.
+  void set_fused_decode(bool on) { fuse_decode_ = on; }
   // How the last step ran: {rows, decode rows, prefill tiles, sequences,
   // block-table width, max_kv bound, decode split_tokens (1 << 30: one pass
   // per row; 0: the attention library's own split)}.
@@ -231,6 +235,8 @@ class TransformerRunner {
   float last_device_ms_ = 0.f;
   double host_ms_[3] = {0, 0, 0};
   bool use_graphs_ = true;
+  bool fuse_decode_ = true;
+  bool attn_proj_ok_ = false;  // the model's widths and dtypes fit cbis_paged_attention_proj
 
   StepBuf bufs_[2];
   int next_buf_ = 0;          // the buffers the next step takes
@@ -255,6 +261,7 @@ class TransformerRunner {
   // current step
   int M_ = 0;
   int n_decode_ = 0, n_tiles_ = 0, n_seqs_ = 0, bt_width_ = 0, max_kv_ = 0, split_tokens_ = 0;
+  int fused_proj_ = 0;  // this step runs attention + out-projection as one launch per layer
   size_t meta_bytes_ = 0;
   const uint8_t* stage_src_ = nullptr;  // the step's metadata in host memory (device address) ...
   uint8_t* stage_dst_ = nullptr;        // ... and its device copy, which the step's embed launch fills

@@ -46,6 +46,10 @@ TransformerRunner::TransformerRunner(const ModelWeights& weights, PagedKVCache& 
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
   const size_t R = max_total_rows, D = cfg_.d_model, F = cfg_.mlp, V = cfg_.vocab;
   const size_t ae = dtype_size(cfg_.act_dtype());
+  // cbis_paged_attention_proj's limits: one head block (256 fp32 / 512 bf16
+  // K/V columns), a multiple of 64, at most 256 fp32 / 512 bf16 weight columns.
+  attn_proj_ok_ = D % 64 == 0 && D <= (cfg_.kv_dtype == CBIS_F32 ? 256u : 512u) &&
+                  (cfg_.weight_dtype == CBIS_F32 ? D <= 256 : cfg_.weight_dtype == CBIS_BF16 && D <= 512);
   for (StepBuf& b : bufs_) {
     hip_check(hipEventCreate(&b.ev_start), "hipEventCreate");
     hip_check(hipEventCreate(&b.ev_stop), "hipEventCreate");
@@ -192,6 +196,12 @@ void TransformerRunner::prepare(int b, const int* tok, const int* pos, const int
   n_seqs_ = (int)seqs.size();
   bt_width_ = width;
   max_kv_ = (max_kv + 255) / 256 * 256;  // coarse, so steps share split shapes (and graphs)
+  // Steps of decode rows only, at most 64 with keys up to 768 (the attention
+  // library's one-pass bound for such calls, so the fused launch reads each
+  // row's keys as the separate one would): one launch per layer for the
+  // attention and the out-projection.
+  fused_proj_ = fuse_decode_ && attn_proj_ok_ && tiles.empty() && (int)drows.size() == M && M <= 64 &&
+                max_kv_ <= 768;
   // Decode rows in one pass each (no split-KV partials, no merge) when they
   // give at least 1.5 rounds of resident decode workgroups (kDecodeSlots: two
   // per CU, one per row and head block) and no row is more than twice the
@@ -275,7 +285,7 @@ void TransformerRunner::prepare(int b, const int* tok, const int* pos, const int
 }
 
 std::vector<int> TransformerRunner::signature() const {
-  return {M_, n_decode_, n_tiles_, n_seqs_, bt_width_, max_kv_, split_tokens_};
+  return {M_, n_decode_, n_tiles_, n_seqs_, bt_width_, max_kv_, split_tokens_, fused_proj_};
 }
 
 void TransformerRunner::enqueue_forward(int b, bool greedy, bool from_prev) {
@@ -345,11 +355,8 @@ void TransformerRunner::enqueue_forward(int b, bool greedy, bool from_prev) {
     else cbis_check(cbis_gemm(&g, s), "qkv gemm");
     a.k_pool = cache_.k_base(l);
     a.v_pool = cache_.v_base(l);
-    // Single rows on the split-KV decode kernel, runs of rows on the MFMA
-    // prefill kernel (whose launch also merges the decode rows' splits).
     a.n_rows = n_decode_;
     a.rows = d_drows_;
-    cbis_check(cbis_paged_attention_mixed(&a, n_tiles_, d_tiles_, s), "attention");
     // out-projection + bias + residual, in place on x
     g = cbis_gemm_desc{};
     g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
@@ -358,8 +365,15 @@ void TransformerRunner::enqueue_forward(int b, bool greedy, bool from_prev) {
     g.w_dtype = wd; g.W = L.wo; g.ldw = D; g.w_scale = L.so;
     g.bias = L.bo; g.residual = d_x_; g.ldr = D;
     g.y_dtype = CBIS_F32; g.Y = d_x_; g.ldy = D;
-    if (ln_pro) cbis_check(cbis_gemm(&g, s), "out-proj gemm");
-    else cbis_check(cbis_gemm_layernorm(&g, L.ln2_w, L.ln2_b, 1e-5f, act, d_xn_, D, s), "out-proj gemm + ln2");
+    if (fused_proj_) {
+      cbis_check(cbis_paged_attention_proj(&a, &g, s), "attention + out-proj");
+    } else {
+      // Single rows on the split-KV decode kernel, runs of rows on the MFMA
+      // prefill kernel (whose launch also merges the decode rows' splits).
+      cbis_check(cbis_paged_attention_mixed(&a, n_tiles_, d_tiles_, s), "attention");
+      if (ln_pro) cbis_check(cbis_gemm(&g, s), "out-proj gemm");
+      else cbis_check(cbis_gemm_layernorm(&g, L.ln2_w, L.ln2_b, 1e-5f, act, d_xn_, D, s), "out-proj gemm + ln2");
+    }
     g = cbis_gemm_desc{};
     g.workspace = d_gemm_ws_; g.workspace_bytes = gemm_ws_bytes_;
     g.M = M; g.N = F; g.K = D;

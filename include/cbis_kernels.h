@@ -223,6 +223,22 @@ size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d);
 /* Split-KV decode attention: any set of rows, each with its own kv_len. */
 int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream);
 
+/* Decode attention fused with the out-projection that follows it (no
+ * reference counterpart: it saves one launch per layer of a small decode
+ * step).  For d's rows, as cbis_paged_attention computes them, but in one
+ * pass per row (split_tokens, workspace and out are not used):
+ * Y[r, :] = attn(r) . W^T (* w_scale) (+ bias) (+ residual[r, :]) with the
+ * attention output rounded to proj->x_dtype first (fp32 or bf16), i.e.
+ * cbis_gemm over the attention output that cbis_paged_attention would have
+ * stored, summed in another order.  proj: N = K = n_heads * head_dim, W fp32
+ * or bf16 (16-byte aligned rows), fp32 Y (may alias residual), no GELU, no
+ * K/V scatter; X and M are not read.  Supported: one head block
+ * (n_heads * head_dim <= 256 with fp32 K/V, <= 512 with bf16), that width
+ * a multiple of 64 and at most 256 with fp32 W (512 with bf16);
+ * CBIS_ERR_UNSUPPORTED otherwise.  Meant for short rows: a row's keys are
+ * read by n_heads * head_dim / 64 workgroups, each in one pass. */
+int cbis_paged_attention_proj(const cbis_attn_desc* d, const cbis_gemm_desc* proj, cbis_stream_t stream);
+
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops that forbid hipMalloc):
  * cbis_paged_attention with the split-KV partials in a library-owned static

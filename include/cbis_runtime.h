@@ -129,10 +129,16 @@ const float* cbis_runner_logits_device(cbis_runner* r);
 void* cbis_runner_stream(cbis_runner* r);
 /* Enable / disable HIP-graph replay of steps whose shape repeats. */
 void cbis_runner_set_graphs(cbis_runner* r, int enable);
+/* Enable (the default) / disable the fused attention + out-projection
+ * launch (cbis_paged_attention_proj) that steps of at most 64 decode rows
+ * with keys up to 768 use when the model's widths allow it (no reference
+ * counterpart; disabled, every step runs the two launches). */
+void cbis_runner_set_fused_decode(cbis_runner* r, int enable);
 /* How the last step ran (no reference counterpart: a diagnostic):
  * {rows, decode rows, prefill tiles, sequences, block-table width, max_kv
  * bound, decode split_tokens (1 << 30 = one pass per row, 0 = the attention
- * library's automatic split)}.  Writes min(capacity, 7) ints; returns 7. */
+ * library's automatic split), 1 if attention and out-projection ran as one
+ * launch per layer}.  Writes min(capacity, 8) ints; returns 8. */
 int cbis_runner_last_plan(const cbis_runner* r, int* out, int capacity);
 
 /* ---- Three-tier KV block manager (include/tiered_kv_manager.hpp:21-151,

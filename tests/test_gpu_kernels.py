@@ -1115,6 +1115,109 @@ def test_empty_calls_are_no_ops(cbis, dev):
     assert runner.forward_step_greedy([], [], []) == []
 
 
+@pytest.mark.parametrize("kvdt,wdt,H", [("f32", "f32", 8), ("f32", "f32", 2), ("f32", "bf16", 8), ("bf16", "bf16", 16),
+                                         ("bf16", "f32", 8), ("bf16", "bf16", 4)])
+def test_paged_attention_proj_matches_separate(cbis, oracle, dev, kvdt, wdt, H):
+    """cbis_paged_attention_proj against cbis_paged_attention (its output
+    stored in the projection's X dtype) followed by cbis_gemm with scale-free
+    weights, bias and the residual (Y aliasing it): a row subset through
+    rows / row_bt, kv lengths 1..768 ending mid-page.  The attention output
+    is the same to the bit before the projection (same kernel, same wave
+    split); only the projection's summation order differs.  Rows outside the
+    list keep their residual."""
+    import torch
+    D, P, S, M = 32 * H, 700, 6, 12
+    kv = np.array([1, 15, 16, 100, 500, 768], np.int32)
+    npages = (kv + 15) // 16
+    perm = rng(21).permutation(P).astype(np.int32)
+    bt = np.zeros((S, int(npages.max())), np.int32)
+    off = 0
+    for i in range(S):
+        bt[i, : npages[i]] = perm[off: off + npages[i]]
+        off += npages[i]
+    row_bt = rng(22).integers(0, S, M).astype(np.int32)
+    row_bt[:S] = np.arange(S)  # every length appears
+    pos = np.array([kv[row_bt[r]] - 1 if r < S else rng(23 + r).integers(0, kv[row_bt[r]]) for r in range(M)],
+                   np.int32)
+    rows = np.array(sorted(set(range(S)) | set(rng(24).choice(np.arange(S, M), 3, replace=False).tolist())),
+                    np.int32)
+    kvt = torch.float32 if kvdt == "f32" else torch.bfloat16
+    kp = torch.empty((P, 16, H, 32), dtype=kvt, device=dev)
+    vp = torch.empty_like(kp)
+    q = torch.empty((M, D), dtype=torch.float32, device=dev)
+    K = cbis.kernels()
+    for t, sd in ((kp, 31), (vp, 32), (q, 33)):
+        cbis.check(K.cbis_fill_normal_fast(ptr(t), cbis.DTYPES[kvdt] if t is not q else cbis.F32, t.numel(), sd, 1.0,
+                                           stream()))
+    wt = torch.float32 if wdt == "f32" else torch.bfloat16
+    W = (torch.randn((D, D), generator=torch.Generator().manual_seed(34)) * 0.05).to(wt).to(dev)
+    bias = (torch.randn(D, generator=torch.Generator().manual_seed(35)) * 0.1).to(dev)
+    resid = torch.randn((M, D), generator=torch.Generator().manual_seed(36)).to(dev)
+    xdt = "f32" if wdt == "f32" else "bf16"
+    BT, POS, ROWS, RBT = to_dev(bt, dev), to_dev(pos, dev), to_dev(rows, dev), to_dev(row_bt, dev)
+    # separate: attention into X, then the GEMM in place on a residual copy
+    attn = torch.zeros((M, D), dtype=torch.float32 if xdt == "f32" else torch.bfloat16, device=dev)
+    d = _attn_desc(cbis, len(rows), H, q, kp, vp, P, BT, bt.shape[1], POS, attn, cbis.DTYPES[kvdt],
+                   out_dtype=cbis.DTYPES[xdt], rows=ROWS, row_bt=RBT, max_kv=int(kv.max()))
+    cbis.check(K.cbis_paged_attention(ctypes.byref(d), stream()))
+    y_sep = resid.clone()
+    _gemm(cbis, M, D, D, attn, cbis.DTYPES[xdt], W, cbis.DTYPES[wdt], y_sep, cbis.F32, bias=bias, residual=y_sep)
+    # fused
+    y = resid.clone()
+    g = cbis.GemmDesc()
+    g.M, g.N, g.K = M, D, D
+    g.x_dtype, g.X, g.ldx = cbis.DTYPES[xdt], 0, D
+    g.w_dtype, g.W, g.ldw = cbis.DTYPES[wdt], ptr(W), D
+    g.bias, g.residual, g.ldr = ptr(bias), ptr(y), D
+    g.y_dtype, g.Y, g.ldy = cbis.F32, ptr(y), D
+    cbis.check(K.cbis_paged_attention_proj(ctypes.byref(d), ctypes.byref(g), stream()))
+    sync()
+    got, ref, r0 = y.cpu().numpy(), y_sep.cpu().numpy(), resid.cpu().numpy()
+    err = np.abs(got[rows] - ref[rows]).max()
+    assert err <= 1e-5 * max(1.0, np.abs(ref[rows]).max()), err
+    others = np.setdiff1d(np.arange(M), rows)
+    assert np.array_equal(got[others], r0[others])
+    # and the attention itself against the oracle (fp32 X only: exact output)
+    if xdt == "f32":
+        kvb = (lambda t: t.cpu().numpy()) if kvdt == "f32" else bits_u16
+        ra = oracle.paged_attention(q.cpu().numpy()[rows], kvb(kp), kvb(vp), bt, pos[rows], H, 32, 16,
+                                    row_bt=row_bt[rows], kv_dtype=0 if kvdt == "f32" else 1)
+        proj = ra.astype(np.float64) @ W.float().cpu().numpy().T.astype(np.float64) + bias.cpu().numpy() + r0[rows]
+        assert np.abs(got[rows] - proj).max() < FP32_TOL
+
+
+def test_paged_attention_proj_rejects_unsupported(cbis, dev):
+    """Widths past one head block or the weight budget, fp8 weights, GELU,
+    K/V scatter and a projection of another width are refused before any
+    launch (all pointers are dummies that are never dereferenced)."""
+    K = cbis.kernels()
+
+    def call(H, kvdt, wdt, **kw):
+        a = cbis.AttnDesc()
+        a.n_rows, a.n_heads, a.head_dim, a.page_size = 4, H, 32, 16
+        a.q_dtype, a.kv_dtype, a.out_dtype = cbis.F32, kvdt, cbis.F32
+        a.q = a.k_pool = a.v_pool = a.block_table = a.row_pos = 256
+        a.ldq, a.num_pages, a.bt_stride = 32 * H, 16, 4
+        g = cbis.GemmDesc()
+        g.M, g.N, g.K = 4, kw.get("N", 32 * H), 32 * H
+        g.x_dtype, g.w_dtype, g.y_dtype = cbis.F32, wdt, cbis.F32
+        g.W = g.Y = 256
+        g.ldw = g.ldy = g.ldr = 32 * H
+        g.epilogue = kw.get("epi", cbis.EPI_NONE)
+        if kw.get("kv"):
+            g.k_pool = g.v_pool = 256
+        return K.cbis_paged_attention_proj(ctypes.byref(a), ctypes.byref(g), None)
+
+    assert call(64, cbis.BF16, cbis.BF16) != 0          # 2048 wide: many head blocks
+    assert call(16, cbis.F32, cbis.F32) != 0            # fp32 K/V: 8 heads per block
+    assert call(16, cbis.BF16, cbis.F32) != 0           # 512 fp32 weight columns per thread budget
+    assert call(3, cbis.F32, cbis.F32) != 0             # 96: not a multiple of 64
+    assert call(8, cbis.F32, cbis.FP8E4M3) != 0         # fp8 weights
+    assert call(8, cbis.F32, cbis.F32, epi=cbis.EPI_GELU) != 0
+    assert call(8, cbis.F32, cbis.F32, kv=True) != 0
+    assert call(8, cbis.F32, cbis.F32, N=128) != 0
+
+
 def test_decode_attention_rejects_unsupported(cbis):
     d = cbis.AttnDesc()
     d.n_rows, d.n_heads, d.head_dim, d.page_size = 4, 8, 64, 16

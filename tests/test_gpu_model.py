@@ -284,6 +284,49 @@ def test_graph_replay_matches_eager(cbis):
     assert greedy == [int(np.argmax(r)) for r in eager]
 
 
+@pytest.mark.parametrize("wdt,kvdt,H", [("f32", "f32", 8), ("bf16", "bf16", 8), ("bf16", "bf16", 16)])
+def test_fused_decode_matches_two_launches(cbis, wdt, kvdt, H):
+    """Small all-decode steps run attention + out-projection as one launch
+    per layer (cbis_paged_attention_proj); the same steps with the fusion
+    off (two launches) give the same logits up to the projection's summation
+    order and the same greedy tokens.  A step with prefill rows, or keys past
+    768, takes the two launches either way."""
+    cfg = cbis.ModelConfig.make(vocab=512, n_layers=2, weight_dtype=wdt, kv_dtype=kvdt, n_heads=H,
+                                d_model=32 * H, max_seq=2048)
+    w = cbis.ModelWeights.synthetic(cfg, seed=4)
+    cache = cbis.PagedKVCache(2, 160, 16, H, 32, kvdt, pages_per_seq=64)
+    runner = cbis.TransformerRunner(w, cache, 256)
+    rng = np.random.default_rng(4)
+    lens = [3, 17, 40, 64, 100]
+    seqs = [cache.allocate_sequence() for _ in lens]
+    for s, n in zip(seqs, lens):
+        for p in range(n + 4):
+            assert cache.ensure_capacity(s, p)
+    tok = [int(t) for t in rng.integers(0, 512, sum(lens))]
+    pos = [p for n in lens for p in range(n)]
+    sid = [s for s, n in zip(seqs, lens) for _ in range(n)]
+    runner.forward_step(tok, pos, sid)  # prefill
+    assert runner.last_plan()["fused_attention_proj"] == 0
+    dec = ([int(t) for t in rng.integers(0, 512, len(lens))], list(lens), seqs)
+    runner.set_fused_decode(False)
+    two = runner.forward_step(*dec)
+    assert runner.last_plan()["fused_attention_proj"] == 0
+    runner.set_fused_decode(True)
+    one = runner.forward_step(*dec)  # rewrites the same K/V slots with the same values
+    assert runner.last_plan()["fused_attention_proj"] == 1
+    if wdt == "f32":
+        assert np.abs(one - two).max() <= 1e-4 * max(1.0, float(np.abs(two).max()))
+    else:  # a changed last bit can move a later bf16 rounding
+        assert row_rel_err(one, two) < 1e-2
+    assert runner.forward_step_greedy(*dec) == [int(np.argmax(r)) for r in one]
+    assert runner.last_plan()["fused_attention_proj"] == 1
+    # a row past 768 keys: two launches
+    long = cache.allocate_sequence()
+    assert cache.ensure_capacity(long, 1000)
+    runner.forward_step([5], [1000], [long])
+    assert runner.last_plan()["fused_attention_proj"] == 0
+
+
 @pytest.mark.parametrize("wdt", ["bf16", "fp8", "f32"])
 def test_packed_checkpoint_round_trip(cbis, tmp_path, wdt):
     """save_packed -> load_packed gives back the same config and the same
