@@ -223,9 +223,10 @@ size_t cbis_paged_attention_workspace_size(const cbis_attn_desc* d);
 /* Split-KV decode attention: any set of rows, each with its own kv_len. */
 int cbis_paged_attention(const cbis_attn_desc* d, cbis_stream_t stream);
 
-/* Decode attention fused with the out-projection that follows it (no
- * reference counterpart: it saves one launch per layer of a small decode
- * step).  For d's rows, as cbis_paged_attention computes them, but in one
+/* Decode attention fused with the out-projection that follows it: the
+ * attention, linear_forward and residual_add of src/transformer.cpp:78-83
+ * in one launch (one launch per layer fewer on small decode steps).  For
+ * d's rows, as cbis_paged_attention computes them, but in one
  * pass per row (split_tokens, workspace and out are not used):
  * Y[r, :] = attn(r) . W^T (* w_scale) (+ bias) (+ residual[r, :]) with the
  * attention output rounded to proj->x_dtype first (fp32 or bf16), i.e.
