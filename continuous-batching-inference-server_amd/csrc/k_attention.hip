@@ -7,8 +7,9 @@
 // j % page_size of physical page table[j / page_size] (:79-83), scores are
 // scaled by 1/sqrt(head_dim) (:72) and softmax-normalised (python/model.py:40-44).
 //
-// Decode kernel (HBM-bound).  A workgroup of NW = 8 waves (16 for one-pass
-// calls) owns one (row, head block, kv split).  A head block is the heads whose head_dim
+// Decode kernel (HBM-bound).  A workgroup of NW = 8 waves (16 for launches
+// of at least one workgroup per CU in one pass, or two per CU in splits)
+// owns one (row, head block, kv split).  A head block is the heads whose head_dim
 // slices of one token row form 1 KiB: 8 heads for fp32 K/V, 16 for bf16 (the
 // last block of a head count that is not a multiple is partial), so
 // one 16-byte-per-lane wave load reads one token's slice of the block fully
@@ -965,10 +966,13 @@ int decode_launch(const cbis_attn_desc* d, void* ws, size_t ws_bytes, hipStream_
   a.qscale = kLog2e / sqrtf((float)kHD);
   const int64_t grid = (int64_t)d->n_rows * ns * hblocks;
   CBIS_REQUIRE(grid < (1LL << 31), CBIS_ERR_UNSUPPORTED, "%s: grid too large", who);
-  // One pass per row over at least one workgroup per CU: 16 waves per
-  // workgroup, each wave half the pages of an 8-wave one (config 4, 768
-  // workgroups: 523 us against 536).  Split calls keep 8 waves.
-  const bool wide = ns == 1 && grid >= 256;
+  // 16 waves per workgroup, each wave half the pages of an 8-wave one, for
+  // one pass per row over at least one workgroup per CU (config 4, 768
+  // workgroups: 523 us against 536) and for split calls of at least two
+  // workgroups per CU (config 3, 768 workgroups: 5.83 TB/s against
+  // 5.68-5.75).  Split calls of one workgroup per CU keep 8 waves (config 5,
+  // 256 workgroups: 10.83 ms per step with 16 against 10.80).
+  const bool wide = grid >= 256 && (ns == 1 || grid >= 512);
   if (d->kv_dtype == CBIS_F32) {
     if (wide) paged_decode_kernel<float, 16><<<(unsigned)grid, 1024, 0, s>>>(a);
     else paged_decode_kernel<float, 8><<<(unsigned)grid, 512, 0, s>>>(a);
