@@ -56,7 +56,8 @@ class AttnDesc(ctypes.Structure):
                 ("kv_dtype", _I), ("k_pool", _P), ("v_pool", _P), ("num_pages", _I),
                 ("block_table", _P), ("bt_stride", _I64), ("row_bt", _P), ("row_pos", _P),
                 ("out_dtype", _I), ("out", _P), ("ldo", _I64),
-                ("max_kv_len", _I), ("split_tokens", _I), ("workspace", _P), ("workspace_bytes", _SZ)]
+                ("max_kv_len", _I), ("split_tokens", _I), ("workspace", _P), ("workspace_bytes", _SZ),
+                ("tile_pages", _I)]
 
 
 class EvictionParams(ctypes.Structure):

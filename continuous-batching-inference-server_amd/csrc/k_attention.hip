@@ -502,7 +502,8 @@ __global__ __launch_bounds__(256) void paged_attention_any_page_kernel(const flo
 // Prefill on MFMA.
 // ---------------------------------------------------------------------------
 struct PrefillArgs {
-  const int* tiles;  // [n_tiles][4]: first_row, n_valid, bt_row, first_pos
+  const int* tiles;  // [n_tiles][tile_ints]: first_row, n_valid, bt_row, first_pos (+ 8 page ids)
+  int tile_ints;     // 4, or 12 with the tile's first 8 page ids
   const void* q;
   int64_t ldq;
   int q_bf16;
@@ -578,7 +579,7 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
   // per-lane loads of one address, and no share of the K/V loads' counter),
   // and the tests on them compile to scalar branches.
   typedef const __attribute__((address_space(4))) int cint_t;
-  cint_t* td = (cint_t*)(a.tiles + 4 * (int64_t)tile);
+  cint_t* td = (cint_t*)(a.tiles + (int64_t)a.tile_ints * tile);
   const int row0 = td[0], nvalid = td[1], pos0 = td[3];
   cint_t* bt = (cint_t*)(a.bt + (int64_t)td[2] * a.bt_stride);
   const int D = a.n_heads * kHD;
@@ -808,8 +809,23 @@ __global__ __launch_bounds__(HPW * kPrefillWaves * 64, 2) void paged_prefill_ker
   constexpr int R = kPrefillRing;
   KV ring[R];
   int ids[R];
+  if (a.tile_ints == 12) {
+    // The first R blocks' page ids come with the tile descriptor (entries
+    // 4 + j0 / 16 and the next: pages min(j0, kv_end - 1) / 16 and
+    // min(j0 + 16, kv_end - 1) / 16, as id_of reads them), so their K/V
+    // loads follow the descriptor's round trip directly.
+    static_assert(32 * (kPrefillWaves * (kPrefillRing - 1) + kPrefillWaves - 1) / 16 + 1 < 8, "descriptor pages");
 #pragma unroll
-  for (int u = 0; u < R; ++u) ids[u] = id_of(key0(u));
+    for (int u = 0; u < R; ++u) {
+      const int k = key0(u) / 16;
+      const int pa = min(max(td[4 + k], 0), a.num_pages - 1);
+      const int pb = min(max(td[5 + k], 0), a.num_pages - 1);
+      ids[u] = col < 16 ? pa : pb;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < R; ++u) ids[u] = id_of(key0(u));
+  }
 #pragma unroll
   for (int u = 0; u < R - 1; ++u) load_block(key0(u), ids[u], ring[u]);
   for (int i0 = 0; i0 < nmine; i0 += R) {
@@ -1107,6 +1123,8 @@ int check_tiles(const cbis_attn_desc* d, int n_tiles, const int* tiles, const ch
   CBIS_REQUIRE(d->kv_dtype == CBIS_BF16, CBIS_ERR_UNSUPPORTED, "%s: prefill tiles need bf16 K/V", who);
   CBIS_REQUIRE(tiles && ((uintptr_t)tiles & 15u) == 0, CBIS_ERR_INVALID,
                "%s: tiles must be a 16-byte aligned device array", who);
+  CBIS_REQUIRE(d->tile_pages == 0 || d->tile_pages == 8, CBIS_ERR_INVALID, "%s: tile_pages %d (0 or 8)", who,
+               d->tile_pages);
   return CBIS_OK;
 }
 
@@ -1117,6 +1135,7 @@ int prefill_launch(const cbis_attn_desc* d, int n_tiles, const int* tiles, hipSt
                    int merge_rows, const char* who) {
   PrefillArgs a;
   a.tiles = tiles;
+  a.tile_ints = d->tile_pages == 8 ? 12 : 4;
   a.q = d->q;
   a.ldq = d->ldq;
   a.q_bf16 = d->q_dtype == CBIS_BF16;

@@ -29,6 +29,7 @@ namespace cbis {
 namespace {
 constexpr int kMinPrefillRun = 8;   // runs shorter than this use the decode kernel
 constexpr int kTileRows = CBIS_PREFILL_TILE_ROWS;  // query rows per prefill tile
+constexpr int kTileInts = 12;  // a prefill tile's descriptor with its first 8 page ids (tile_pages = 8)
 constexpr size_t kMaxGraphs = 64;
 size_t align_ints(size_t n) { return (n + 3) & ~(size_t)3; }
 }  // namespace
@@ -158,9 +159,15 @@ void TransformerRunner::prepare(int b, const int* tok, const int* pos, const int
     int j = i + 1;
     while (j < M && seq[j] == seq[i] && pos[j] == pos[j - 1] + 1) ++j;
     if (prefill_ok && j - i >= kMinPrefillRun) {
+      const std::vector<int>& pg = cache_.pages(seq[i]);
       for (int r = i; r < j; r += kTileRows) {
         const int nv = std::min(kTileRows, j - r);
         tiles.insert(tiles.end(), {r, nv, rowbt[r], pos[r]});
+        // The pages of the tile's first key blocks (tile_pages = 8): page
+        // min(16 k, kv_end - 1) / 16, kv_end = pos[r] + nv (within the
+        // sequence's pages, so within the step's block-table width).
+        const int last = pos[r] + nv - 1;
+        for (int k = 0; k < 8; ++k) tiles.push_back(pg[std::min(16 * k, last) / 16]);
       }
     } else {
       for (int r = i; r < j; ++r) {
@@ -180,19 +187,19 @@ void TransformerRunner::prepare(int b, const int* tok, const int* pos, const int
   // resident workgroups, workgroup w and w + grid/2 share a CU, so the
   // heaviest tile shares its CU with the lightest (config 4: 25.5 -> 23.3 us).
   {
-    const int nt = (int)tiles.size() / 4;
+    const int nt = (int)tiles.size() / kTileInts;
     std::vector<int> order(nt);
     for (int t = 0; t < nt; ++t) order[t] = t;
-    auto last_key = [&](int t) { return tiles[4 * t + 3] + tiles[4 * t + 1]; };
+    auto last_key = [&](int t) { return tiles[kTileInts * t + 3] + tiles[kTileInts * t + 1]; };
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return last_key(x) > last_key(y); });
     std::reverse(order.begin() + nt / 2, order.end());
     std::vector<int> sorted(tiles.size());
-    for (int t = 0; t < nt; ++t) std::copy_n(&tiles[4 * order[t]], 4, &sorted[4 * t]);
+    for (int t = 0; t < nt; ++t) std::copy_n(&tiles[kTileInts * order[t]], kTileInts, &sorted[kTileInts * t]);
     tiles.swap(sorted);
   }
   M_ = M;
   n_decode_ = (int)drows.size();
-  n_tiles_ = (int)tiles.size() / 4;
+  n_tiles_ = (int)tiles.size() / kTileInts;
   n_seqs_ = (int)seqs.size();
   bt_width_ = width;
   max_kv_ = (max_kv + 255) / 256 * 256;  // coarse, so steps share split shapes (and graphs)
@@ -325,6 +332,7 @@ void TransformerRunner::enqueue_forward(int b, bool greedy, bool from_prev) {
   a.split_tokens = split_tokens_;
   a.workspace = d_ws_;
   a.workspace_bytes = ws_bytes_;
+  a.tile_pages = 8;
 
   // LayerNorms that follow a residual GEMM (ln2 after the out-projection,
   // the next layer's ln1 or ln_f after fc2) run with it (cbis_gemm_layernorm:

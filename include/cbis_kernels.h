@@ -214,6 +214,9 @@ typedef struct cbis_attn_desc {
                               page_size, else the call fails with CBIS_ERR_INVALID */
   void* workspace;         /* fp32 partials when a row needs more than one split */
   size_t workspace_bytes;
+  int tile_pages;          /* prefill tiles: 0 = [n_tiles][4]; 8 = [n_tiles][12], the
+                              tile's first 8 page ids appended (see
+                              cbis_paged_prefill_attention) */
 } cbis_attn_desc;
 
 /* Bytes of workspace cbis_paged_attention needs for this descriptor (0 when
@@ -262,9 +265,13 @@ int cbis_paged_attention_static(const cbis_attn_desc* d, cbis_stream_t stream);
  * consecutive rows of one sequence.  tiles is a device array [n_tiles][4] of
  * {first_row, n_valid_rows, block_table_row, first_position}; row i of a tile
  * has position first_position + i and attends causally to keys [0, position].
- * Rows of a tile past CBIS_PREFILL_TILE_ROWS are not computed.
- * d->rows / row_bt / row_pos / max_kv_len / split_tokens / workspace are
- * ignored.  Supports bf16 K/V, head_dim 32, page_size 16. */
+ * With d->tile_pages = 8 a tile is 12 ints: those 4, then for k = 0..7 the
+ * block-table entry of page min(16 k, kv_end - 1) / 16 of its row, kv_end =
+ * min(first_position + n_valid_rows, bt_stride * page_size) (the pages the
+ * tile's first key blocks read, so their loads need no block-table read
+ * first; same results).  Rows of a tile past CBIS_PREFILL_TILE_ROWS are not
+ * computed.  d->rows / row_bt / row_pos / max_kv_len / split_tokens /
+ * workspace are ignored.  Supports bf16 K/V, head_dim 32, page_size 16. */
 int cbis_paged_prefill_attention(const cbis_attn_desc* d, int n_tiles, const int* tiles,
                                  cbis_stream_t stream);
 

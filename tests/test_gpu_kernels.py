@@ -1309,15 +1309,28 @@ def test_prefill_attention_mfma(cbis, oracle, dev, cached, n_rows, tile):
     for t, s, dt in ((kp, 31, cbis.BF16), (vp, 32, cbis.BF16), (q, 33, cbis.F32)):
         cbis.check(K.cbis_fill_normal_fast(ptr(t), dt, t.numel(), s, 1.0, stream()))
     pos = (cached + np.arange(n_rows)).astype(np.int32)
-    tiles = []
+    tiles, tiles12 = [], []
     for r in range(0, n_rows, tile):
-        tiles += [r, min(tile, n_rows - r), 0, cached + r]
+        nv = min(tile, n_rows - r)
+        tiles += [r, nv, 0, cached + r]
+        # the 12-int form: the tile's first 8 page ids, page min(16 k, kv_end - 1) / 16
+        tiles12 += [r, nv, 0, cached + r] + [int(bt[0, min(16 * k, cached + r + nv - 1) // 16]) for k in range(8)]
     T = to_dev(np.array(tiles, np.int32), dev)
     out = torch.empty((n_rows, H * 32), dtype=torch.bfloat16, device=dev)
     d = _attn_desc(cbis, n_rows, H, q, kp, vp, P, to_dev(bt, dev), bt.shape[1], None, out, cbis.BF16,
                    out_dtype=cbis.BF16)
     cbis.check(K.cbis_paged_prefill_attention(ctypes.byref(d), len(tiles) // 4, ptr(T), stream()))
+    # The same tiles with their first pages in the descriptor: the same loads, bit for bit.
+    T12 = to_dev(np.array(tiles12, np.int32), dev)
+    out12 = torch.empty_like(out)
+    d12 = _attn_desc(cbis, n_rows, H, q, kp, vp, P, to_dev(bt, dev), bt.shape[1], None, out12, cbis.BF16,
+                     out_dtype=cbis.BF16)
+    d12.tile_pages = 8
+    cbis.check(K.cbis_paged_prefill_attention(ctypes.byref(d12), len(tiles12) // 12, ptr(T12), stream()))
+    d12.tile_pages = 4
+    assert K.cbis_paged_prefill_attention(ctypes.byref(d12), len(tiles12) // 12, ptr(T12), stream()) != 0
     sync()
+    assert torch.equal(out12.view(torch.int16), out.view(torch.int16))
     ref = oracle.paged_attention(q.cpu().numpy(), bits_u16(kp), bits_u16(vp), np.repeat(bt, n_rows, 0), pos, H, 32,
                                  16, kv_dtype=1)
     got = out.float().cpu().numpy()
