@@ -152,3 +152,18 @@ def test_c1_pipelined_greedy(cbis, slots, chunk, budget, arrivals):
     s = cache.allocate_sequence()
     assert cache.ensure_capacity(s, 0)
     assert len(runner.forward_step_greedy([1], [0], [s])) == 1
+
+
+def test_runner_closed_with_a_step_queued(cbis):
+    """Closing a runner while a greedy step is still queued waits for it
+    (its buffers are freed only after the stream has run it); the cache and a
+    new runner over it then work, with the same tokens as before."""
+    w = _model(cbis, "f32", "f32")
+    cache, r, seqs = _setup(cbis, w, "f32", [[1, 2, 3, 4]])
+    s = seqs[0]
+    ref = r.forward_step_greedy([1, 2, 3, 4], [0, 1, 2, 3], [s] * 4)
+    r.enqueue_greedy([1, 2, 3, 4], [0, 1, 2, 3], [s] * 4)
+    r.enqueue_greedy([-1], [4], [s], token_src=[3])
+    r.close()
+    r2 = cbis.TransformerRunner(w, cache, 256)
+    assert r2.forward_step_greedy([1, 2, 3, 4], [0, 1, 2, 3], [s] * 4) == ref
