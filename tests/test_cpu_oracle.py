@@ -259,3 +259,74 @@ def test_prng_spec(oracle):
     assert abs(z.mean()) < 0.01 and abs(z.var() - 1.0) < 0.01 and np.abs(z).max() <= 6.0
     u = oracle.uniform_int(0, 3, 10000, 16, 64)
     assert u.min() == 16 and u.max() == 64
+
+
+def _torch_cpu(oracle):
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("torch_cpu", os.path.join(os.path.dirname(oracle.__file__),
+                                                                            "torch_cpu.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_torch_cpu_step_matches_model_py(oracle):
+    """The fp32 PyTorch CPU step (the cpu_baseline's forward) reproduces
+    python/model.py's G1 logits through the paged pools."""
+    tc = _torch_cpu(oracle)
+    g = np.load(os.path.join(GOLDEN, "g1_refmodel.npz"))
+    w = oracle.synthetic_weights(oracle.ModelSpec(), seed=0, pos_rows=64)
+    for i in range(len(g["lens"])):
+        ids = g[f"ids{i}"]
+        kp = [np.zeros((8, 16, 8, 32), np.float32) for _ in range(4)]
+        vp = [np.zeros((8, 16, 8, 32), np.float32) for _ in range(4)]
+        cache = oracle.PagedKVCacheOracle(8)
+        sid = cache.allocate_sequence()
+        for p in range(len(ids)):
+            assert cache.ensure_capacity(sid, p)
+        pos = list(range(len(ids)))
+        wp, wo, bt, rb = oracle.step_tables(cache, list(ids), pos, [sid] * len(ids))
+        lg = tc.TorchCpuStep(w, kp, vp).forward_step(ids, pos, wp, wo, bt, rb).double().numpy()
+        assert np.abs(lg - g[f"logits{i}"]).max() < 2e-5
+
+
+@pytest.mark.parametrize("wdt", ["f32", "bf16", "fp8"])
+def test_torch_cpu_step_matches_c_oracle(oracle, wdt):
+    """A mixed step -- 5 decode rows over cached keys and a 20-row prefill
+    chunk after 9 cached tokens, shuffled pages -- through the fp32 PyTorch
+    CPU step and the fp64 C oracle: same K/V written, logits within fp32
+    rounding (f32 model) or the bf16 bound."""
+    tc = _torch_cpu(oracle)
+    spec = oracle.ModelSpec(vocab=512, d_model=256, n_heads=8, head_dim=32, n_layers=2, mlp=1024, max_seq=256,
+                            weight_dtype=wdt, kv_dtype="f32" if wdt == "f32" else "bf16")
+    w = oracle.synthetic_weights(spec, seed=3, pos_rows=256)
+    P = 64
+    cache = oracle.PagedKVCacheOracle(P)
+    rng = np.random.default_rng(7)
+    rng.shuffle(cache.free)  # pages handed out in a random order
+    tok, pos, sid = [], [], []
+    for kv in (17, 40, 1, 96, 63):
+        s = cache.allocate_sequence()
+        assert cache.ensure_capacity(s, kv - 1)
+        tok.append(int(rng.integers(0, 512))); pos.append(kv - 1); sid.append(s)
+    s = cache.allocate_sequence()
+    assert cache.ensure_capacity(s, 28)
+    for p in range(9, 29):
+        tok.append(int(rng.integers(0, 512))); pos.append(p); sid.append(s)
+    om = oracle.OracleModel(w, max_pages=P)
+    for pools in (om.kpools, om.vpools):
+        for a in pools:
+            vals = rng.standard_normal(a.shape).astype(np.float32)
+            a[...] = vals if a.dtype == np.float32 else oracle.f32_to_bf16_bits(vals)
+    kp = [a.copy() for a in om.kpools]
+    vp = [a.copy() for a in om.vpools]
+    wp, wo, bt, rb = oracle.step_tables(cache, tok, pos, sid)
+    ref = om.forward_step(tok, pos, wp, wo, bt, rb)
+    lg = tc.TorchCpuStep(w, kp, vp).forward_step(tok, pos, wp, wo, bt, rb).double().numpy()
+    rel = (np.abs(lg - ref).max(axis=1) / np.abs(ref).max(axis=1)).max()
+    assert rel < (1e-4 if wdt == "f32" else 2e-2), rel
+    for l in range(2):  # the step's own K/V slots, as written by each
+        for mine, theirs in ((kp[l], om.kpools[l]), (vp[l], om.vpools[l])):
+            a = mine.astype(np.float64) if wdt == "f32" else oracle.bf16_bits_to_f32(mine).astype(np.float64)
+            b = theirs.astype(np.float64) if wdt == "f32" else oracle.bf16_bits_to_f32(theirs).astype(np.float64)
+            assert np.abs(a - b).max() < (1e-4 if wdt == "f32" else 0.05)
