@@ -336,36 +336,53 @@ def cpu_step_sample(oracle, spec, cache, tok, pos, sid):
 
 
 def cpu_baseline_c4(oracle, st, cbis, runs=3):
-    """The C oracle on config 4's step, scaled to 16 layers from one layer
-    (bounded samples of ~10-30 s of CPU work), median of `runs` runs each:
-    all cores on every row (the reported value), and 1 core on every 16th
-    row (12 decode rows; the 64 prefill rows at positions that are multiples
-    of 16), scaled by rows."""
+    """Config 4's step on the host's cores as the reference computes on the
+    CPU: python/model.py's operators in fp32 PyTorch (oracle/torch_cpu.py),
+    over the GPU cache's layer-0 K/V copied to the host.  One layer over all
+    1216 rows and the lm_head (median of `runs` runs each), scaled to 16
+    layers; then the same on 1 thread (one run)."""
+    import torch
+    import torch_cpu
     spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
                             max_seq=32768, weight_dtype="bf16", kv_dtype="bf16")
-    run = cpu_step_sampler(oracle, spec, st["cache"], st["tok"], st["pos"], st["sid"])
-    lib = oracle.lib()
-    cores = lib.orc_num_threads()
+    cache, tok, pos, sid = st["cache"], st["tok"], st["pos"], st["sid"]
+    w = oracle.synthetic_weights(spec, seed=0, pos_rows=max(pos) + 1)
+    P = cache.max_pages()
+    kp = np.empty((P, 16, spec.n_heads, spec.head_dim), np.uint16)
+    vp = np.empty_like(kp)
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    for dst, src in ((kp, cache.k_base(0)), (vp, cache.v_base(0))):
+        assert hip.hipMemcpy(dst.ctypes.data, src, dst.nbytes, 2) == 0
+    wp, wo, bt, rb = oracle.step_tables(cache, tok, pos, sid)
+    model = torch_cpu.TorchCpuStep(w, [kp], [vp])
 
-    def median_step(rows, scale):
-        ts = [run(rows) for _ in range(runs)]
-        tl = float(np.median([t[0] for t in ts])) * scale
-        th = float(np.median([t[1] for t in ts])) * scale
-        return tl, th, tl * 16 + th
+    def once():
+        with torch.no_grad():
+            x = model.embed(tok, pos)
+            t0 = time.perf_counter()
+            x = model.layer(0, x, pos, wp, wo, bt, rb)
+            t1 = time.perf_counter()
+            model.head(x)
+            return t1 - t0, time.perf_counter() - t1
 
-    tl, th, t_step = median_step(None, 1.0)
-    sub = [i for i, p in enumerate(st["pos"]) if (i < 192 and i % 16 == 0) or (i >= 192 and p % 16 == 0)]
-    old = lib.orc_set_num_threads(1)
+    cores = torch.get_num_threads()
+    once()  # first-touch of the weights and pools
+    ts = [once() for _ in range(runs)]
+    tl, th = float(np.median([t[0] for t in ts])), float(np.median([t[1] for t in ts]))
+    t_step = tl * 16 + th
+    torch.set_num_threads(1)
     try:
-        tl1, th1, t_step1 = median_step(sub, len(st["tok"]) / len(sub))
+        tl1, th1 = once()
     finally:
-        lib.orc_set_num_threads(old)
+        torch.set_num_threads(cores)
+    t_step1 = tl1 * 16 + th1
     return {"value": round(192.0 / t_step, 3), "unit": "decode tokens/s", "cores": cores, "kind": "port",
             "value_1core": round(192.0 / t_step1, 4),
-            "sample": f"oracle fp64 forward of config 4's 1216-row step, 1 of 16 layers (median of {runs}: "
-                      f"{tl:.2f} s) + lm_head ({th:.2f} s), scaled to 16 layers: step {t_step:.1f} s on {cores} "
-                      f"threads; on 1 thread the {len(sub)} rows of every 16th position (median of {runs}), "
-                      f"scaled by rows: layer {tl1:.1f} s + lm_head {th1:.1f} s -> step {t_step1:.0f} s"}
+            "sample": f"fp32 PyTorch CPU forward (oracle/torch_cpu.py: python/model.py's operators over the paged "
+                      f"K/V) of config 4's 1216-row step, 1 of 16 layers (median of {runs}: {tl:.3f} s) + lm_head "
+                      f"({th:.3f} s), scaled to 16 layers: step {t_step:.2f} s on {cores} threads; on 1 thread "
+                      f"layer {tl1:.2f} s + lm_head {th1:.2f} s -> step {t_step1:.1f} s"}
 
 
 def recorded_traffic(name):
