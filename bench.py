@@ -282,70 +282,13 @@ def gemm_timing(cbis, st, iters):
     return res, tot_flops, tot_ms
 
 
-def cpu_step_sampler(oracle, spec, cache, tok, pos, sid):
-    """Sets up the C oracle (fp64, OpenMP) on one layer of a forward step over
-    the GPU cache's layer-0 K/V (copied to the host) and returns
-    run(rows=None) -> (t_layer, t_head): the time of that layer over the
-    given rows (all by default) and separately of the 0-layer remainder
-    (embedding + ln_f + lm_head) over them."""
-    w = oracle.synthetic_weights(spec, seed=0, pos_rows=max(pos) + 1)
-    om = oracle.OracleModel(w, max_pages=1)
-    P = cache.max_pages()
-    om.kpools = [np.empty((P, 16, spec.n_heads, spec.head_dim), np.uint16)]
-    om.vpools = [np.empty((P, 16, spec.n_heads, spec.head_dim), np.uint16)]
-    hip = ctypes.CDLL("libamdhip64.so")
-    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    for dst, src in ((om.kpools[0], cache.k_base(0)), (om.vpools[0], cache.v_base(0))):
-        assert hip.hipMemcpy(dst.ctypes.data, src, dst.nbytes, 2) == 0
-    om._kp = (ctypes.c_void_p * 1)(om.kpools[0].ctypes.data)
-    om._vp = (ctypes.c_void_p * 1)(om.vpools[0].ctypes.data)
-    M = len(tok)
-    wpage = np.empty(M, np.int32)
-    woff = np.empty(M, np.int32)
-    uniq, row_bt = {}, np.empty(M, np.int32)
-    for i in range(M):
-        wpage[i], woff[i] = cache.resolve_slot(sid[i], pos[i])
-        row_bt[i] = uniq.setdefault(sid[i], len(uniq))
-    tables = {q: cache.pages(q) for q in uniq}
-    width = max(len(t) for t in tables.values())
-    bt = np.zeros((len(uniq), width), np.int32)
-    for q, j in uniq.items():
-        bt[j, : len(tables[q])] = tables[q]
-    tok_a, pos_a = np.asarray(tok, np.int32), np.asarray(pos, np.int32)
-
-    def run(rows=None):
-        r = np.arange(M) if rows is None else np.asarray(rows)
-        args = (tok_a[r], pos_a[r], wpage[r], woff[r], bt, row_bt[r])
-        om._mdl.n_layers = 1
-        t0 = time.time()
-        om.forward_step(*args)
-        t_layer_plus_head = time.time() - t0
-        om._mdl.n_layers = 0
-        t1 = time.time()
-        om.forward_step(*args)
-        t_head = time.time() - t1
-        om._mdl.n_layers = 1
-        return t_layer_plus_head - t_head, t_head
-
-    return run
-
-
-def cpu_step_sample(oracle, spec, cache, tok, pos, sid):
-    """One all-core run of cpu_step_sampler over every row."""
-    return cpu_step_sampler(oracle, spec, cache, tok, pos, sid)()
-
-
-def cpu_baseline_c4(oracle, st, cbis, runs=3):
-    """Config 4's step on the host's cores as the reference computes on the
-    CPU: python/model.py's operators in fp32 PyTorch (oracle/torch_cpu.py),
-    over the GPU cache's layer-0 K/V copied to the host.  One layer over all
-    1216 rows and the lm_head (median of `runs` runs each), scaled to 16
-    layers; then the same on 1 thread (one run)."""
+def torch_step_sampler(oracle, spec, cache, tok, pos, sid):
+    """The reference's CPU forward (python/model.py's operators, fp32 PyTorch:
+    oracle/torch_cpu.py) on one layer of a forward step over the GPU cache's
+    layer-0 K/V (copied to the host).  Returns run() -> (t_layer, t_head): the
+    time of that layer over every row, and of the final LayerNorm + lm_head."""
     import torch
     import torch_cpu
-    spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
-                            max_seq=32768, weight_dtype="bf16", kv_dtype="bf16")
-    cache, tok, pos, sid = st["cache"], st["tok"], st["pos"], st["sid"]
     w = oracle.synthetic_weights(spec, seed=0, pos_rows=max(pos) + 1)
     P = cache.max_pages()
     kp = np.empty((P, 16, spec.n_heads, spec.head_dim), np.uint16)
@@ -357,7 +300,7 @@ def cpu_baseline_c4(oracle, st, cbis, runs=3):
     wp, wo, bt, rb = oracle.step_tables(cache, tok, pos, sid)
     model = torch_cpu.TorchCpuStep(w, [kp], [vp])
 
-    def once():
+    def run():
         with torch.no_grad():
             x = model.embed(tok, pos)
             t0 = time.perf_counter()
@@ -366,23 +309,41 @@ def cpu_baseline_c4(oracle, st, cbis, runs=3):
             model.head(x)
             return t1 - t0, time.perf_counter() - t1
 
+    return run
+
+
+def cpu_baseline_step(oracle, spec, cache, tok, pos, sid, decode_rows, runs=3):
+    """A step's CPU time as the reference computes on the CPU (fp32 PyTorch,
+    torch_step_sampler): one layer over all rows and the lm_head, each the
+    median of `runs` runs after a first-touch run, scaled to 16 layers, on the
+    host's threads; then one run on 1 thread.  Returns the cpu_baseline
+    object (decode tokens/s of the step's decode_rows)."""
+    import torch
+    run = torch_step_sampler(oracle, spec, cache, tok, pos, sid)
     cores = torch.get_num_threads()
-    once()  # first-touch of the weights and pools
-    ts = [once() for _ in range(runs)]
+    run()
+    ts = [run() for _ in range(runs)]
     tl, th = float(np.median([t[0] for t in ts])), float(np.median([t[1] for t in ts]))
     t_step = tl * 16 + th
     torch.set_num_threads(1)
     try:
-        tl1, th1 = once()
+        tl1, th1 = run()
     finally:
         torch.set_num_threads(cores)
     t_step1 = tl1 * 16 + th1
-    return {"value": round(192.0 / t_step, 3), "unit": "decode tokens/s", "cores": cores, "kind": "port",
-            "value_1core": round(192.0 / t_step1, 4),
+    return {"value": round(decode_rows / t_step, 4), "unit": "decode tokens/s", "cores": cores, "kind": "port",
+            "value_1core": round(decode_rows / t_step1, 4),
             "sample": f"fp32 PyTorch CPU forward (oracle/torch_cpu.py: python/model.py's operators over the paged "
-                      f"K/V) of config 4's 1216-row step, 1 of 16 layers (median of {runs}: {tl:.3f} s) + lm_head "
+                      f"K/V) of the {len(tok)}-row step, 1 of 16 layers (median of {runs}: {tl:.3f} s) + lm_head "
                       f"({th:.3f} s), scaled to 16 layers: step {t_step:.2f} s on {cores} threads; on 1 thread "
                       f"layer {tl1:.2f} s + lm_head {th1:.2f} s -> step {t_step1:.1f} s"}
+
+
+def cpu_baseline_c4(oracle, st, cbis, runs=3):
+    """Config 4's step (192 decode rows + two 512-row chunks) on the host."""
+    spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
+                            max_seq=32768, weight_dtype="bf16", kv_dtype="bf16")
+    return cpu_baseline_step(oracle, spec, st["cache"], st["tok"], st["pos"], st["sid"], 192, runs)
 
 
 def recorded_traffic(name):
@@ -667,16 +628,33 @@ def run_c1(args, cbis, oracle):
     toks = toks[True]
     cpu = None
     if not args.no_cpu:
+        # The whole workload through the same scheduler with the reference's
+        # CPU forward (fp32 PyTorch, oracle/torch_cpu.py) as the step.
+        import torch
+        import torch_cpu
         spec = oracle.ModelSpec(vocab=512, n_layers=4, max_seq=128)
-        om = oracle.OracleModel(oracle.synthetic_weights(spec, seed=0, pos_rows=128), max_pages=128)
+        pools = [[np.zeros((128, 16, 8, 32), np.float32) for _ in range(4)] for _ in range(2)]
+        tm = torch_cpu.TorchCpuStep(oracle.synthetic_weights(spec, seed=0, pos_rows=128), *pools)
+        step_s = []
+
+        class CpuStep:
+            def forward_step(self, *a):
+                t = time.perf_counter()
+                with torch.no_grad():
+                    lg = tm.forward_step(*a).double().numpy()
+                step_s.append((len(a[0]), time.perf_counter() - t))
+                return lg
+
         t0 = time.time()
-        gen, _ = oracle.run_continuous(om, oracle.PagedKVCacheOracle(128), reqs)
+        gen, _ = oracle.run_continuous(CpuStep(), oracle.PagedKVCacheOracle(128), reqs)
         cpu_s = time.time() - t0
-        assert gen == toks, "CPU oracle and GPU greedy tokens differ"
-        cpu = {"value": round((n_prompt + sum(dl)) / cpu_s, 2), "unit": "prompt+generated tok/s",
-               "cores": oracle.lib().orc_num_threads(), "kind": "port",
-               "sample": f"oracle fp64 run_continuous of the whole config-1 workload ({cpu_s:.1f} s); "
-                         f"greedy tokens identical to the GPU run"}
+        dec = [t for m, t in step_s if m == len(reqs)]  # the steps of one decode row per request
+        dec_s = float(np.median(dec))
+        cpu = {"value": round(len(reqs) / dec_s, 2), "unit": "decode tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port", "tokens_match_gpu": gen == toks,
+               "sample": f"fp32 PyTorch CPU step (oracle/torch_cpu.py: python/model.py's operators) through the "
+                         f"same scheduler over the whole config-1 workload ({cpu_s:.2f} s, {len(step_s)} steps): "
+                         f"median {len(reqs)}-row decode step {dec_s * 1e3:.3f} ms"}
     return {"metric": "decode tokens/s (config 1 tiny GPT continuous batching)", "value": round(value, 1),
             "unit": "decode tokens/s", "ms_per_step": round(dec_ms / (len(dl) and 31), 4), "dtype": "f32",
             "data": "synthetic (seeded weights N(0,0.02); prompt ids U[0,511])",
@@ -764,12 +742,7 @@ def run_c5(args, cbis, oracle):
     if not args.no_cpu:
         spec = oracle.ModelSpec(vocab=32000, d_model=2048, n_heads=64, head_dim=32, n_layers=1, mlp=8192,
                                 max_seq=32768, weight_dtype="fp8", kv_dtype="bf16")
-        t_layer, t_head = cpu_step_sample(oracle, spec, cache, first, [ctx] * n_seq, seqs)
-        t_step = t_layer * 16 + t_head
-        cpu = {"value": round(n_seq / t_step, 4), "unit": "decode tokens/s", "cores": oracle.lib().orc_num_threads(),
-               "kind": "port",
-               "sample": f"oracle fp64 forward of one 16-row config-5 step (kv 32704), 1 of 16 layers "
-                         f"({t_layer:.1f}s) + lm_head ({t_head:.1f}s), scaled to 16 layers; step {t_step:.1f}s"}
+        cpu = cpu_baseline_step(oracle, spec, cache, first, [ctx] * n_seq, seqs, n_seq, runs=1)
     return {"metric": "decode tokens/s (config 5 long-context fp8 decode)", "value": round(value, 2),
             "unit": "decode tokens/s", "ms_per_step": round(dt * 1000 / gen, 4), "dtype": "bf16 x fp8-e4m3",
             "data": "synthetic (fp8 weights absmax-quantised from N(0,0.02); K/V cache N(0,1))",
