@@ -1936,6 +1936,18 @@ bool skinny_path(const cbis_gemm_desc* d) {
   return d->M <= kSkinnyMaxM && w_al && d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0;
 }
 
+// Whether a plain call (no greedy epilogue, LayerNorm prologue or fused
+// split-K reduce, which are the skinny kernel's own) of decode-sized M runs
+// on the skinny kernel: always up to 32 rows; bf16 x bf16 calls of 33..64
+// rows take the direct-to-LDS tiles instead, whose workgroups read X once
+// per tile where the skinny kernel reads all of it once per 16 columns
+// (config 2 at M = 64, qkv / out / MLP up / MLP down: 7.0 / 7.0 / 7.6 / 10.4
+// us skinny, 4.2 / 4.2 / 4.7 / 7.0 tiled).  fp32 weights keep the skinny
+// kernel (M = 64 qkv 8.3 us against 9.1 on the fp32 tiles), fp8 weights too.
+bool plain_skinny(const cbis_gemm_desc* d) {
+  return skinny_path(d) && (d->M <= 32 || !dma_eligible(d));
+}
+
 // Whether cbis_layernorm_gemm(_argmax) forms d's LayerNorm inside the GEMM.
 bool ln_prologue_ok(const cbis_gemm_desc* d, const float* x, int64_t ldx, const float* gamma, const float* beta) {
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
@@ -2006,8 +2018,7 @@ int gemm_run(const cbis_gemm_desc* d, hipStream_t s, GemmArgs& g, float4* amax =
 
   // Decode-sized M: weight streaming (K a multiple of 32 for bf16 and fp32,
   // of 64 for fp8; W rows 16-byte aligned).
-  const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * we) % 16 == 0;
-  if (d->M <= kSkinnyMaxM && w_al && d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0) {
+  if (amax || ln || fused_reduce ? skinny_path(d) : plain_skinny(d)) {
     if (fused_reduce && !amax && !ln) {
       const SplitPlan p = plan_skinny_split(d->M, d->N, d->K, d->w_dtype);
       const size_t need = (size_t)p.ksplit * d->M * d->N * sizeof(float);
@@ -2240,10 +2251,7 @@ size_t cbis_gemm_layernorm_workspace_size(const cbis_gemm_desc* d) {
 size_t cbis_gemm_workspace_size(const cbis_gemm_desc* d) {
   if (!d || d->M <= 0 || d->N <= 0 || d->K <= 0) return 0;
   // gemm_run's skinny path never splits in cbis_gemm.
-  const int wb = d->w_dtype == CBIS_F32 ? 4 : (d->w_dtype == CBIS_BF16 ? 2 : 1);
-  if (d->M <= kSkinnyMaxM && ((uintptr_t)d->W & 15u) == 0 && (d->ldw * wb) % 16 == 0 &&
-      d->K % (d->w_dtype == CBIS_FP8E4M3 ? 64 : 32) == 0)
-    return 0;
+  if (plain_skinny(d)) return 0;
   if (d->x_dtype == CBIS_F32 && d->w_dtype == CBIS_F32) {
     // gemm_run's fp32 paths: the skinny kernel (no split) or plan_f32.
     const bool w_al = ((uintptr_t)d->W & 15u) == 0 && (d->ldw * 4) % 16 == 0;

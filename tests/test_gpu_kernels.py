@@ -367,7 +367,8 @@ def test_gemm_layernorm_skinny_split(cbis, oracle, dev, M, N, K, parts, wdt):
         d.y_dtype, d.Y, d.ldy = cbis.F32, ptr(Y), N
         need = K_.cbis_gemm_layernorm_workspace_size(ctypes.byref(d))
         assert need == (parts * M * N * 4 if parts > 1 else 0)
-        assert K_.cbis_gemm_workspace_size(ctypes.byref(d)) == 0  # plain cbis_gemm keeps the skinny kernel whole
+        if wdt == "fp8" or M <= 32:  # plain cbis_gemm keeps the skinny kernel whole (bf16 x bf16 calls of
+            assert K_.cbis_gemm_workspace_size(ctypes.byref(d)) == 0  # 33..64 rows take the tiles)
         ws = torch.empty(max(4, need // 4), dtype=torch.float32, device=dev)
         d.workspace, d.workspace_bytes = ptr(ws), need
         ln = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
@@ -393,7 +394,9 @@ def test_gemm_layernorm_skinny_split(cbis, oracle, dev, M, N, K, parts, wdt):
 @pytest.mark.parametrize("M,K", [(1, 256), (8, 256), (33, 512), (64, 512), (16, 2048), (100, 256), (8, 4096)])
 def test_layernorm_gemm_matches_layernorm_then_gemm(cbis, oracle, dev, M, K, wdt):
     """cbis_layernorm_gemm (Y = LayerNorm(x) . W^T + b, GELU) against
-    cbis_layernorm into X followed by cbis_gemm: bit-identical Y.  Decode-sized
+    cbis_layernorm into X followed by cbis_gemm: bit-identical Y where both
+    GEMMs run on the same kernel (bf16 x bf16 plain calls of 33..64 rows run
+    on the tiles: within fp32 rounding there).  Decode-sized
     calls with short rows (M <= 64, K <= 512) form the normalised rows inside
     the skinny GEMM (X is then left untouched); M = 100 and K = 2048 / 4096
     take the two-kernel path."""
@@ -437,7 +440,13 @@ def test_layernorm_gemm_matches_layernorm_then_gemm(cbis, oracle, dev, M, K, wdt
             # the prologue path leaves X untouched; the two-kernel path writes LayerNorm(x) there
             untouched = bool((Xbuf.float() == 7.0).all())
             assert untouched == (M <= 64 and K <= 512), (M, K)
-    assert np.array_equal(outs[0], outs[1])
+    if wdt == "bf16" and 32 < M <= 64:
+        # The plain bf16 x bf16 GEMM of 33..64 rows runs on the tiles, which
+        # sum in another order than the skinny kernel: fp32 rounding apart.
+        a, b_ = outs[0].view(np.float32), outs[1].view(np.float32)
+        assert (np.abs(a - b_) / (1.0 + np.abs(b_))).max() < 1e-5
+    else:
+        assert np.array_equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("wdt", ["f32", "bf16", "fp8"])
@@ -534,8 +543,9 @@ def test_gemm_fp8_decode_every_code(cbis, oracle, dev):
 @pytest.mark.parametrize("M", [1, 8, 16, 33, 64])
 @pytest.mark.parametrize("wdt", ["f32", "bf16", "fp8"])
 def test_gemm_skinny_decode_rows(cbis, oracle, dev, M, wdt):
-    """Decode-sized M (weight-streaming kernel) for every weight dtype, with
-    bias + GELU and with bias + a residual aliasing Y, against the oracle."""
+    """Decode-sized M for every weight dtype (the weight-streaming kernel;
+    bf16 x bf16 calls of 33..64 rows the direct-to-LDS tiles), with bias +
+    GELU and with bias + a residual aliasing Y, against the oracle."""
     import torch
     N, K = 1040, 1024  # N not a multiple of the 16-column tile
     w = oracle.normal(16, 2, N * K, 0.02).reshape(N, K)
